@@ -1,0 +1,31 @@
+// Host-side interface of the NVFP4 GEMV kernels (decode regime).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace apex_hip {
+
+// Arguments of one GEMV launch.  codes/scales/tensor_scale index 0 is the plain
+// matrix (or the gate of a GeGLU pair), index 1 the up matrix of a GeGLU pair.
+struct GemvArgs {
+    const void *x;              // [tokens, K] fp32 or bf16 bits, row stride K
+    const uint32_t *codes[2];   // [rows, K/8]
+    const uint8_t *scales[2];   // [rows, K/16]
+    float tensor_scale[2];
+    void *out;                  // [tokens, out_stride] fp32 or bf16 bits
+    uint32_t rows, K, tokens, out_stride;
+};
+
+enum class GemvMode { PlainF32, PlainBF16, GegluBF16, GegluF32 };
+
+// Tuning knobs (set from the device properties at backend init, or by sweeps).
+extern int kTargetWavesPerCU;
+extern int kNumCUs;
+
+hipError_t gemv_launch(const GemvArgs &a, GemvMode mode, bool x_is_bf16, hipStream_t stream);
+hipError_t geglu_f32_launch(const float *gate, const float *up, float *out, uint32_t count,
+                            hipStream_t stream);
+hipError_t dequant_launch(const uint32_t *codes, const uint8_t *scales, void *out, uint32_t rows,
+                          uint32_t K, float tensor_scale, bool bf16, hipStream_t stream);
+
+} // namespace apex_hip

@@ -1,0 +1,103 @@
+// NVFP4 GEMV entry points (decode regime), the standalone GeGLU and the dequantiser.
+// The GEMV kernel templates live in gemv_kernels.h and are instantiated per
+// (activation type, epilogue) in gemv_*.hip so the variants compile in parallel.
+#include "gemv_kernels.h"
+
+namespace apex_hip {
+namespace gemv_detail {
+extern template hipError_t gemv_dispatch<float, 0>(const GemvArgs &, hipStream_t);
+extern template hipError_t gemv_dispatch<float, 3>(const GemvArgs &, hipStream_t);
+extern template hipError_t gemv_dispatch<uint16_t, 1>(const GemvArgs &, hipStream_t);
+extern template hipError_t gemv_dispatch<uint16_t, 2>(const GemvArgs &, hipStream_t);
+} // namespace gemv_detail
+
+namespace {
+using gemv_detail::kThreads;
+
+// Standalone GeGLU, fp32, in place allowed (shaders/geglu.metal:6-24).
+__global__ __launch_bounds__(kThreads) void geglu_f32_kernel(const float *gate, const float *up,
+                                                             float *out, uint32_t count) {
+    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < count)
+        out[i] = gelu_tanh(gate[i]) * up[i];
+}
+
+// Dequantise W to bf16 or fp32 rows: one thread per 16-element block.
+template <bool BF16>
+__global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t *codes,
+                                                           const uint8_t *scales, void *out,
+                                                           uint32_t rows, uint32_t K,
+                                                           float tensor_scale) {
+    const uint64_t nblk = (uint64_t)rows * (K / 16);
+    const uint64_t b = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (b >= nblk)
+        return;
+    const float s = e4m3_to_f32(scales[b]) * tensor_scale;
+    const uint32_t words[2] = {codes[2 * b], codes[2 * b + 1]};
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        f32x2_t v[4];
+        e2m1x8_to_f32(words[w], v);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float val = v[j][h] * s;
+                const uint64_t o = b * 16 + w * 8 + 2 * j + h;
+                if constexpr (BF16)
+                    static_cast<uint16_t *>(out)[o] = f32_to_bf16_bits(val);
+                else
+                    static_cast<float *>(out)[o] = val;
+            }
+        }
+    }
+}
+
+} // namespace
+
+int kTargetWavesPerCU = 8;
+int kNumCUs = 256;
+
+hipError_t gemv_launch(const GemvArgs &a, GemvMode mode, bool x_is_bf16, hipStream_t stream) {
+    if (a.tokens == 0 || a.rows == 0)
+        return hipSuccess;
+    // Activation type and epilogue go together: fp32 activations keep the reference's
+    // fp32 contract (fp32 outputs), bf16 activations produce bf16 outputs.
+    switch (mode) {
+    case GemvMode::PlainF32:
+        return x_is_bf16 ? hipErrorInvalidValue : gemv_detail::gemv_dispatch<float, 0>(a, stream);
+    case GemvMode::GegluF32:
+        return x_is_bf16 ? hipErrorInvalidValue : gemv_detail::gemv_dispatch<float, 3>(a, stream);
+    case GemvMode::PlainBF16:
+        return x_is_bf16 ? gemv_detail::gemv_dispatch<uint16_t, 1>(a, stream) : hipErrorInvalidValue;
+    case GemvMode::GegluBF16:
+        return x_is_bf16 ? gemv_detail::gemv_dispatch<uint16_t, 2>(a, stream) : hipErrorInvalidValue;
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t geglu_f32_launch(const float *gate, const float *up, float *out, uint32_t count,
+                            hipStream_t stream) {
+    if (count == 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(geglu_f32_kernel, dim3((count + kThreads - 1) / kThreads), dim3(kThreads),
+                       0, stream, gate, up, out, count);
+    return hipGetLastError();
+}
+
+hipError_t dequant_launch(const uint32_t *codes, const uint8_t *scales, void *out, uint32_t rows,
+                          uint32_t K, float tensor_scale, bool bf16, hipStream_t stream) {
+    const uint64_t nblk = (uint64_t)rows * (K / 16);
+    if (nblk == 0)
+        return hipSuccess;
+    const dim3 grid((unsigned)((nblk + kThreads - 1) / kThreads));
+    if (bf16)
+        hipLaunchKernelGGL(dequant_kernel<true>, grid, dim3(kThreads), 0, stream, codes, scales,
+                           out, rows, K, tensor_scale);
+    else
+        hipLaunchKernelGGL(dequant_kernel<false>, grid, dim3(kThreads), 0, stream, codes, scales,
+                           out, rows, K, tensor_scale);
+    return hipGetLastError();
+}
+
+} // namespace apex_hip

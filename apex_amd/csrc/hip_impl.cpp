@@ -1,0 +1,693 @@
+// The one translation unit holding the HIP C-ABI glue of the APEX backend
+// (the role src/metal_impl.cpp + src/backend/metal_backend.cpp play for Metal).
+// Declarations and contracts: include/apex_hip.h.
+#include "apex_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "gemv.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct ApexError : std::runtime_error {
+    int code;
+    ApexError(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+[[noreturn]] void fail(int code, const std::string &msg) { throw ApexError(code, msg); }
+
+void hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess)
+        fail(APEX_HIP_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <class F> int guard(F &&f) {
+    try {
+        f();
+        return APEX_HIP_OK;
+    } catch (const ApexError &e) {
+        g_last_error = e.what();
+        return e.code;
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+        return APEX_HIP_E_INVALID;
+    }
+}
+
+// CU count of the current device, read once per process for launch sizing.
+void init_device_tuning() {
+    static bool done = false;
+    if (done)
+        return;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0)
+        apex_hip::kNumCUs = cus;
+    done = true;
+}
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+void require(bool ok, const char *msg) {
+    if (!ok)
+        fail(APEX_HIP_E_INVALID, msg);
+}
+
+void check_nvfp4_shape(uint32_t rows, uint32_t K) {
+    (void)rows;
+    require(K % 16 == 0, "hidden_dim (K) must be a multiple of 16");
+    require(K > 0, "hidden_dim (K) must be positive");
+}
+
+// ------------------------------------------------------------------------------------
+// Direct-entry implementations (shared by the registry launchers)
+// ------------------------------------------------------------------------------------
+
+void matmul_impl(const void *x, bool bf16, const uint32_t *codes, const uint8_t *scales,
+                 float ts, void *out, uint32_t tokens, uint32_t rows, uint32_t K,
+                 hipStream_t stream) {
+    check_nvfp4_shape(rows, K);
+    if (tokens == 0 || rows == 0)
+        return;
+    require(x && codes && scales && out, "null pointer");
+    init_device_tuning();
+    apex_hip::GemvArgs a{};
+    a.x = x;
+    a.codes[0] = a.codes[1] = codes;
+    a.scales[0] = a.scales[1] = scales;
+    a.tensor_scale[0] = a.tensor_scale[1] = ts;
+    a.out = out;
+    a.rows = rows;
+    a.K = K;
+    a.tokens = tokens;
+    a.out_stride = rows;
+    hip_check(apex_hip::gemv_launch(a, bf16 ? apex_hip::GemvMode::PlainBF16
+                                            : apex_hip::GemvMode::PlainF32,
+                                    bf16, stream),
+              "matmul_nvfp4 launch");
+}
+
+void geglu_impl(const void *x, bool bf16, const uint32_t *gc, const uint8_t *gs, float gts,
+                const uint32_t *uc, const uint8_t *us, float uts, void *out, uint32_t tokens,
+                uint32_t rows, uint32_t K, hipStream_t stream) {
+    check_nvfp4_shape(rows, K);
+    if (tokens == 0 || rows == 0)
+        return;
+    require(x && gc && gs && uc && us && out, "null pointer");
+    init_device_tuning();
+    apex_hip::GemvArgs a{};
+    a.x = x;
+    a.codes[0] = gc;
+    a.codes[1] = uc;
+    a.scales[0] = gs;
+    a.scales[1] = us;
+    a.tensor_scale[0] = gts;
+    a.tensor_scale[1] = uts;
+    a.out = out;
+    a.rows = rows;
+    a.K = K;
+    a.tokens = tokens;
+    a.out_stride = rows;
+    hip_check(apex_hip::gemv_launch(a, bf16 ? apex_hip::GemvMode::GegluBF16
+                                            : apex_hip::GemvMode::GegluF32,
+                                    bf16, stream),
+              "geglu_nvfp4 launch");
+}
+
+} // namespace
+
+// ------------------------------------------------------------------------------------
+// Backend object
+// ------------------------------------------------------------------------------------
+
+struct apex_hip_buffer {
+    void *dev = nullptr;
+    void *host = nullptr;     // pinned mirror (owned) or the wrapped pointer
+    size_t length = 0;
+    std::string category;
+    bool wrapped = false;
+    bool host_valid = false;  // host bytes are current
+    bool dev_valid = true;    // device bytes are current
+};
+
+struct apex_hip_backend {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+};
+
+namespace {
+
+void ensure_device_current(apex_hip_backend *b, apex_hip_buffer *buf) {
+    if (buf->dev_valid)
+        return;
+    hip_check(hipMemcpyAsync(buf->dev, buf->host, buf->length, hipMemcpyHostToDevice, b->stream),
+              "upload");
+    if (buf->wrapped) // pageable source: make sure the copy has consumed it
+        hip_check(hipStreamSynchronize(b->stream), "upload sync");
+    buf->dev_valid = true;
+}
+
+// ---- registry ---------------------------------------------------------------------
+
+struct LaunchCtx {
+    void *ptr[16];
+    size_t avail[16]; // bytes from the offset to the end of the buffer
+    uint32_t u[16];
+    float f[16];
+    apex_hip_dim3 grid, block;
+    hipStream_t stream;
+};
+
+using Launcher = void (*)(const LaunchCtx &);
+
+struct KernelSpec {
+    const char *name;
+    const char *sig;     // one letter per argument: B buffer, U uint32, F float
+    uint32_t out_mask;   // bit i set: argument i is written by the kernel
+    Launcher launch;
+};
+
+void need(const LaunchCtx &c, int i, uint64_t bytes, const char *what) {
+    if (bytes > c.avail[i])
+        fail(APEX_HIP_E_INVALID, std::string(what) + ": buffer too small (need " +
+                                     std::to_string(bytes) + " bytes, have " +
+                                     std::to_string(c.avail[i]) + ")");
+}
+
+// matmul_nvfp4: reference argument order of src/ops.h:40-45.
+void launch_matmul_nvfp4(const LaunchCtx &c) {
+    const uint32_t K = c.u[4], w_rows = c.u[5], tokens = c.grid.y;
+    const uint64_t simd_per_group = ((uint64_t)c.block.x * c.block.y * c.block.z) / 32;
+    const uint64_t covered = (uint64_t)c.grid.x * simd_per_group;
+    const uint32_t rows = (uint32_t)(covered < w_rows ? covered : w_rows);
+    check_nvfp4_shape(rows, K);
+    need(c, 0, (uint64_t)tokens * K * 4, "matmul_nvfp4 input");
+    need(c, 1, (uint64_t)rows * K / 2, "matmul_nvfp4 weights");
+    need(c, 2, (uint64_t)rows * K / 16, "matmul_nvfp4 scales");
+    if (tokens > 0 && rows > 0)
+        need(c, 3, (uint64_t)(tokens - 1) * w_rows * 4 + (uint64_t)rows * 4, "matmul_nvfp4 output");
+    if (tokens == 0 || rows == 0)
+        return;
+    // Output rows are strided by w_rows even when the grid covers fewer rows.
+    init_device_tuning();
+    apex_hip::GemvArgs a{};
+    a.x = c.ptr[0];
+    a.codes[0] = a.codes[1] = (const uint32_t *)c.ptr[1];
+    a.scales[0] = a.scales[1] = (const uint8_t *)c.ptr[2];
+    a.tensor_scale[0] = a.tensor_scale[1] = 1.0f;
+    a.out = c.ptr[3];
+    a.rows = rows;
+    a.K = K;
+    a.tokens = tokens;
+    a.out_stride = w_rows;
+    hip_check(apex_hip::gemv_launch(a, apex_hip::GemvMode::PlainF32, false, c.stream),
+              "matmul_nvfp4 launch");
+}
+
+// geglu_f32: src/ops.h:53-54.
+void launch_geglu_f32(const LaunchCtx &c) {
+    const uint64_t threads = (uint64_t)c.grid.x * c.grid.y * c.grid.z *
+                             ((uint64_t)c.block.x * c.block.y * c.block.z);
+    const uint32_t count = (uint32_t)(threads < c.u[3] ? threads : c.u[3]);
+    need(c, 0, (uint64_t)count * 4, "geglu_f32 gate");
+    need(c, 1, (uint64_t)count * 4, "geglu_f32 up");
+    need(c, 2, (uint64_t)count * 4, "geglu_f32 output");
+    hip_check(apex_hip::geglu_f32_launch((const float *)c.ptr[0], (const float *)c.ptr[1],
+                                         (float *)c.ptr[2], count, c.stream),
+              "geglu_f32 launch");
+}
+
+void launch_matmul_nvfp4_bf16(const LaunchCtx &c) {
+    const uint32_t K = c.u[4], rows = c.u[5], tokens = c.u[6];
+    check_nvfp4_shape(rows, K);
+    need(c, 0, (uint64_t)tokens * K * 2, "matmul_nvfp4_bf16 input");
+    need(c, 1, (uint64_t)rows * K / 2, "matmul_nvfp4_bf16 weights");
+    need(c, 2, (uint64_t)rows * K / 16, "matmul_nvfp4_bf16 scales");
+    need(c, 3, (uint64_t)tokens * rows * 2, "matmul_nvfp4_bf16 output");
+    matmul_impl(c.ptr[0], true, (const uint32_t *)c.ptr[1], (const uint8_t *)c.ptr[2], c.f[7],
+                c.ptr[3], tokens, rows, K, c.stream);
+}
+
+template <bool BF16> void launch_geglu_nvfp4(const LaunchCtx &c) {
+    const uint32_t K = c.u[6], rows = c.u[7], tokens = c.u[8];
+    const uint64_t es = BF16 ? 2 : 4;
+    check_nvfp4_shape(rows, K);
+    need(c, 0, (uint64_t)tokens * K * es, "geglu_nvfp4 input");
+    need(c, 1, (uint64_t)rows * K / 2, "geglu_nvfp4 gate weights");
+    need(c, 2, (uint64_t)rows * K / 16, "geglu_nvfp4 gate scales");
+    need(c, 3, (uint64_t)rows * K / 2, "geglu_nvfp4 up weights");
+    need(c, 4, (uint64_t)rows * K / 16, "geglu_nvfp4 up scales");
+    need(c, 5, (uint64_t)tokens * rows * es, "geglu_nvfp4 output");
+    geglu_impl(c.ptr[0], BF16, (const uint32_t *)c.ptr[1], (const uint8_t *)c.ptr[2], c.f[9],
+               (const uint32_t *)c.ptr[3], (const uint8_t *)c.ptr[4], c.f[10], c.ptr[5], tokens,
+               rows, K, c.stream);
+}
+
+template <bool BF16> void launch_dequant(const LaunchCtx &c) {
+    const uint32_t K = c.u[3], rows = c.u[4];
+    check_nvfp4_shape(rows, K);
+    need(c, 0, (uint64_t)rows * K / 2, "dequant weights");
+    need(c, 1, (uint64_t)rows * K / 16, "dequant scales");
+    need(c, 2, (uint64_t)rows * K * (BF16 ? 2 : 4), "dequant output");
+    hip_check(apex_hip::dequant_launch((const uint32_t *)c.ptr[0], (const uint8_t *)c.ptr[1],
+                                       c.ptr[2], rows, K, c.f[5], BF16, c.stream),
+              "dequant launch");
+}
+
+const KernelSpec kKernels[] = {
+    {"matmul_nvfp4", "BBBBUU", 1u << 3, launch_matmul_nvfp4},
+    {"geglu_f32", "BBBU", 1u << 2, launch_geglu_f32},
+    {"matmul_nvfp4_bf16", "BBBBUUUF", 1u << 3, launch_matmul_nvfp4_bf16},
+    {"geglu_nvfp4_f32", "BBBBBBUUUFF", 1u << 5, launch_geglu_nvfp4<false>},
+    {"geglu_nvfp4_bf16", "BBBBBBUUUFF", 1u << 5, launch_geglu_nvfp4<true>},
+    {"dequant_nvfp4_f32", "BBBUUF", 1u << 2, launch_dequant<false>},
+    {"dequant_nvfp4_bf16", "BBBUUF", 1u << 2, launch_dequant<true>},
+};
+constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
+
+const KernelSpec *find_kernel(const char *name) {
+    if (!name)
+        fail(APEX_HIP_E_UNKNOWN_KERNEL, "kernel name is null");
+    for (const KernelSpec &k : kKernels)
+        if (std::strcmp(k.name, name) == 0)
+            return &k;
+    fail(APEX_HIP_E_UNKNOWN_KERNEL, std::string("cannot find kernel: ") + name);
+}
+
+// Maximum threads per threadgroup accepted, as MTL::ComputePipelineState's
+// maxTotalThreadsPerThreadgroup bounds the reference (metal_backend.cpp:169-171).
+constexpr uint64_t kMaxThreadsPerGroup = 1024;
+
+const KernelSpec *validate(const char *kernel, const apex_hip_arg *args, size_t nargs,
+                           apex_hip_dim3 grid, apex_hip_dim3 block) {
+    const KernelSpec *k = find_kernel(kernel);
+    const size_t want = std::strlen(k->sig);
+    if (nargs != want)
+        fail(APEX_HIP_E_ARGS, std::string(kernel) + ": expected " + std::to_string(want) +
+                                  " arguments (" + k->sig + "), got " + std::to_string(nargs));
+    if (nargs && !args)
+        fail(APEX_HIP_E_ARGS, std::string(kernel) + ": argument array is null");
+    for (size_t i = 0; i < nargs; ++i) {
+        const char kind = k->sig[i];
+        const apex_hip_arg &a = args[i];
+        if (kind == 'B') {
+            if (!a.buffer)
+                fail(APEX_HIP_E_ARGS, std::string(kernel) + ": argument " + std::to_string(i) +
+                                          " must be a buffer");
+        } else {
+            if (a.buffer || !a.bytes || a.size != 4)
+                fail(APEX_HIP_E_ARGS, std::string(kernel) + ": argument " + std::to_string(i) +
+                                          " must be a 4-byte value");
+        }
+    }
+    const uint64_t threads = (uint64_t)block.x * block.y * block.z;
+    if (threads > kMaxThreadsPerGroup)
+        fail(APEX_HIP_E_THREADGROUP, std::string(kernel) + ": threadgroup too large");
+    if (threads == 0 || (uint64_t)grid.x * grid.y * grid.z == 0)
+        fail(APEX_HIP_E_INVALID, std::string(kernel) + ": empty grid or threadgroup");
+    return k;
+}
+
+} // namespace
+
+extern "C" {
+
+const char *apex_hip_last_error(void) { return g_last_error.c_str(); }
+
+int apex_hip_abi_version(void) { return APEX_HIP_ABI_VERSION; }
+
+int apex_hip_backend_create(int device, apex_hip_backend **out) {
+    return guard([&] {
+        require(out != nullptr, "out is null");
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+            fail(APEX_HIP_E_DEVICE, "HipBackend: no HIP device found");
+        if (device < 0 || device >= n)
+            fail(APEX_HIP_E_DEVICE, "HipBackend: device index out of range");
+        hip_check(hipSetDevice(device), "hipSetDevice");
+        auto *b = new apex_hip_backend();
+        b->device = device;
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, device) == hipSuccess)
+            b->name = p.gcnArchName;
+        if (hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking) != hipSuccess) {
+            delete b;
+            fail(APEX_HIP_E_DEVICE, "HipBackend: failed to create stream");
+        }
+        init_device_tuning();
+        *out = b;
+    });
+}
+
+void apex_hip_backend_destroy(apex_hip_backend *b) {
+    if (!b)
+        return;
+    if (b->stream) {
+        (void)hipStreamSynchronize(b->stream);
+        (void)hipStreamDestroy(b->stream);
+    }
+    delete b;
+}
+
+int apex_hip_device_name(apex_hip_backend *b, char *buf, size_t len) {
+    return guard([&] {
+        require(b && buf && len > 0, "null argument");
+        std::snprintf(buf, len, "%s", b->name.c_str());
+    });
+}
+
+int apex_hip_wrap_no_copy(apex_hip_backend *b, void *host, size_t bytes, apex_hip_buffer **out) {
+    return guard([&] {
+        require(b && out, "null argument");
+        const size_t page = 16384;
+        if (reinterpret_cast<uintptr_t>(host) % page || bytes % page || !host)
+            fail(APEX_HIP_E_ALIGN, "wrapNoCopy: pointer and length must be page multiples");
+        auto *buf = new apex_hip_buffer();
+        if (bytes && hipMalloc(&buf->dev, bytes) != hipSuccess) {
+            delete buf;
+            fail(APEX_HIP_E_OOM, "wrapNoCopy: device allocation failed");
+        }
+        buf->host = host;
+        buf->length = bytes;
+        buf->wrapped = true;
+        buf->host_valid = true;
+        buf->dev_valid = false;
+        *out = buf;
+    });
+}
+
+int apex_hip_allocate(apex_hip_backend *b, size_t bytes, const char *category,
+                      apex_hip_buffer **out) {
+    return guard([&] {
+        require(b && out, "null argument");
+        auto *buf = new apex_hip_buffer();
+        if (bytes) {
+            if (hipMalloc(&buf->dev, bytes) != hipSuccess) {
+                delete buf;
+                fail(APEX_HIP_E_OOM, "allocate: device allocation failed");
+            }
+            if (hipMemsetAsync(buf->dev, 0, bytes, b->stream) != hipSuccess) {
+                (void)hipFree(buf->dev);
+                delete buf;
+                fail(APEX_HIP_E_DEVICE, "allocate: zero fill failed");
+            }
+        }
+        buf->length = bytes;
+        buf->category = category ? category : "";
+        buf->dev_valid = true;
+        buf->host_valid = false;
+        *out = buf;
+    });
+}
+
+int apex_hip_contents(apex_hip_backend *b, apex_hip_buffer *buf, void **out) {
+    return guard([&] {
+        require(b && buf && out, "null argument");
+        if (!buf->host) {
+            if (buf->length && hipHostMalloc(&buf->host, buf->length, hipHostMallocDefault) != hipSuccess)
+                fail(APEX_HIP_E_OOM, "contents: host mirror allocation failed");
+            buf->host_valid = false;
+        }
+        if (!buf->host_valid) {
+            hip_check(hipStreamSynchronize(b->stream), "contents: sync");
+            if (buf->length)
+                hip_check(hipMemcpy(buf->host, buf->dev, buf->length, hipMemcpyDeviceToHost),
+                          "contents: download");
+            buf->host_valid = true;
+        }
+        buf->dev_valid = false; // the caller may write through the pointer
+        *out = buf->host;
+    });
+}
+
+int apex_hip_release(apex_hip_backend *b, apex_hip_buffer *buf) {
+    return guard([&] {
+        if (!buf)
+            return;
+        if (b && b->stream)
+            (void)hipStreamSynchronize(b->stream);
+        if (buf->dev)
+            (void)hipFree(buf->dev);
+        if (buf->host && !buf->wrapped)
+            (void)hipHostFree(buf->host);
+        delete buf;
+    });
+}
+
+int apex_hip_run(apex_hip_backend *b, const char *kernel, const apex_hip_arg *args, size_t nargs,
+                 apex_hip_dim3 threadgroups, apex_hip_dim3 threads_per_group) {
+    return guard([&] {
+        require(b != nullptr, "backend is null");
+        const KernelSpec *k = validate(kernel, args, nargs, threadgroups, threads_per_group);
+        LaunchCtx c{};
+        c.grid = threadgroups;
+        c.block = threads_per_group;
+        c.stream = b->stream;
+        for (size_t i = 0; i < nargs; ++i) {
+            const apex_hip_arg &a = args[i];
+            if (k->sig[i] == 'B') {
+                if (a.offset > a.buffer->length)
+                    fail(APEX_HIP_E_INVALID, std::string(kernel) + ": offset beyond buffer end");
+                ensure_device_current(b, a.buffer);
+                c.ptr[i] = static_cast<char *>(a.buffer->dev) + a.offset;
+                c.avail[i] = a.buffer->length - a.offset;
+            } else if (k->sig[i] == 'U') {
+                std::memcpy(&c.u[i], a.bytes, 4);
+            } else {
+                std::memcpy(&c.f[i], a.bytes, 4);
+            }
+        }
+        k->launch(c);
+        for (size_t i = 0; i < nargs; ++i)
+            if (k->out_mask & (1u << i))
+                args[i].buffer->host_valid = false;
+    });
+}
+
+int apex_hip_sync(apex_hip_backend *b) {
+    return guard([&] {
+        require(b != nullptr, "backend is null");
+        hip_check(hipStreamSynchronize(b->stream), "sync");
+    });
+}
+
+int apex_hip_buffer_device_ptr(apex_hip_buffer *buf, void **out) {
+    return guard([&] {
+        require(buf && out, "null argument");
+        *out = buf->dev;
+    });
+}
+
+size_t apex_hip_buffer_length(apex_hip_buffer *buf) { return buf ? buf->length : 0; }
+
+void *apex_hip_backend_stream(apex_hip_backend *b) { return b ? (void *)b->stream : nullptr; }
+
+int apex_hip_kernel_count(void) { return kNumKernels; }
+
+const char *apex_hip_kernel_name(int index) {
+    return (index >= 0 && index < kNumKernels) ? kKernels[index].name : nullptr;
+}
+
+const char *apex_hip_kernel_signature(const char *kernel) {
+    for (const KernelSpec &k : kKernels)
+        if (kernel && std::strcmp(k.name, kernel) == 0)
+            return k.sig;
+    return nullptr;
+}
+
+int apex_hip_validate_run(const char *kernel, const apex_hip_arg *args, size_t nargs,
+                          apex_hip_dim3 threadgroups, apex_hip_dim3 threads_per_group) {
+    return guard([&] { validate(kernel, args, nargs, threadgroups, threads_per_group); });
+}
+
+// ---- direct entry points ----------------------------------------------------------
+
+int apex_nvfp4_matmul_f32(const float *x, const uint32_t *codes, const uint8_t *scales,
+                          float tensor_scale, float *out, uint32_t tokens, uint32_t rows,
+                          uint32_t K, void *stream) {
+    return guard([&] {
+        matmul_impl(x, false, codes, scales, tensor_scale, out, tokens, rows, K, as_stream(stream));
+    });
+}
+
+int apex_nvfp4_matmul_bf16(const uint16_t *x, const uint32_t *codes, const uint8_t *scales,
+                           float tensor_scale, uint16_t *out, uint32_t tokens, uint32_t rows,
+                           uint32_t K, void *stream) {
+    return guard([&] {
+        matmul_impl(x, true, codes, scales, tensor_scale, out, tokens, rows, K, as_stream(stream));
+    });
+}
+
+int apex_nvfp4_geglu_f32(const float *x, const uint32_t *gate_codes, const uint8_t *gate_scales,
+                         float gate_tensor_scale, const uint32_t *up_codes,
+                         const uint8_t *up_scales, float up_tensor_scale, float *out,
+                         uint32_t tokens, uint32_t rows, uint32_t K, void *stream) {
+    return guard([&] {
+        geglu_impl(x, false, gate_codes, gate_scales, gate_tensor_scale, up_codes, up_scales,
+                   up_tensor_scale, out, tokens, rows, K, as_stream(stream));
+    });
+}
+
+int apex_nvfp4_geglu_bf16(const uint16_t *x, const uint32_t *gate_codes,
+                          const uint8_t *gate_scales, float gate_tensor_scale,
+                          const uint32_t *up_codes, const uint8_t *up_scales,
+                          float up_tensor_scale, uint16_t *out, uint32_t tokens, uint32_t rows,
+                          uint32_t K, void *stream) {
+    return guard([&] {
+        geglu_impl(x, true, gate_codes, gate_scales, gate_tensor_scale, up_codes, up_scales,
+                   up_tensor_scale, out, tokens, rows, K, as_stream(stream));
+    });
+}
+
+int apex_geglu_f32(const float *gate, const float *up, float *out, uint32_t count, void *stream) {
+    return guard([&] {
+        if (count == 0)
+            return;
+        require(gate && up && out, "null pointer");
+        hip_check(apex_hip::geglu_f32_launch(gate, up, out, count, as_stream(stream)),
+                  "geglu_f32 launch");
+    });
+}
+
+int apex_nvfp4_dequant_f32(const uint32_t *codes, const uint8_t *scales, float tensor_scale,
+                           float *out, uint32_t rows, uint32_t K, void *stream) {
+    return guard([&] {
+        check_nvfp4_shape(rows, K);
+        require(rows == 0 || (codes && scales && out), "null pointer");
+        hip_check(apex_hip::dequant_launch(codes, scales, out, rows, K, tensor_scale, false,
+                                           as_stream(stream)),
+                  "dequant launch");
+    });
+}
+
+int apex_nvfp4_dequant_bf16(const uint32_t *codes, const uint8_t *scales, float tensor_scale,
+                            uint16_t *out, uint32_t rows, uint32_t K, void *stream) {
+    return guard([&] {
+        check_nvfp4_shape(rows, K);
+        require(rows == 0 || (codes && scales && out), "null pointer");
+        hip_check(apex_hip::dequant_launch(codes, scales, out, rows, K, tensor_scale, true,
+                                           as_stream(stream)),
+                  "dequant launch");
+    });
+}
+
+// ---- plumbing ----------------------------------------------------------------------
+
+int apex_hip_device_count(int *out) {
+    return guard([&] {
+        require(out != nullptr, "out is null");
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess)
+            n = 0;
+        *out = n;
+    });
+}
+
+int apex_hip_set_device(int device) {
+    return guard([&] { hip_check(hipSetDevice(device), "hipSetDevice"); });
+}
+
+int apex_hip_malloc(size_t bytes, void **out) {
+    return guard([&] {
+        require(out != nullptr, "out is null");
+        *out = nullptr;
+        if (bytes && hipMalloc(out, bytes) != hipSuccess)
+            fail(APEX_HIP_E_OOM, "hipMalloc failed for " + std::to_string(bytes) + " bytes");
+    });
+}
+
+int apex_hip_free(void *ptr) {
+    return guard([&] {
+        if (ptr)
+            hip_check(hipFree(ptr), "hipFree");
+    });
+}
+
+int apex_hip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    return guard([&] { hip_check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "h2d"); });
+}
+
+int apex_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    return guard([&] { hip_check(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "d2h"); });
+}
+
+int apex_hip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    return guard([&] { hip_check(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice), "d2d"); });
+}
+
+int apex_hip_memset(void *dst, int value, size_t bytes) {
+    return guard([&] { hip_check(hipMemset(dst, value, bytes), "memset"); });
+}
+
+int apex_hip_device_synchronize(void) {
+    return guard([&] { hip_check(hipDeviceSynchronize(), "device sync"); });
+}
+
+int apex_hip_stream_create(void **out) {
+    return guard([&] {
+        require(out != nullptr, "out is null");
+        hipStream_t s;
+        hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "stream create");
+        *out = s;
+    });
+}
+
+int apex_hip_stream_destroy(void *stream) {
+    return guard([&] { hip_check(hipStreamDestroy(as_stream(stream)), "stream destroy"); });
+}
+
+int apex_hip_stream_synchronize(void *stream) {
+    return guard([&] { hip_check(hipStreamSynchronize(as_stream(stream)), "stream sync"); });
+}
+
+int apex_hip_event_create(void **out) {
+    return guard([&] {
+        require(out != nullptr, "out is null");
+        hipEvent_t e;
+        hip_check(hipEventCreate(&e), "event create");
+        *out = e;
+    });
+}
+
+int apex_hip_event_destroy(void *event) {
+    return guard([&] { hip_check(hipEventDestroy(static_cast<hipEvent_t>(event)), "event destroy"); });
+}
+
+int apex_hip_event_record(void *event, void *stream) {
+    return guard([&] {
+        hip_check(hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream)), "event record");
+    });
+}
+
+int apex_hip_event_synchronize(void *event) {
+    return guard([&] {
+        hip_check(hipEventSynchronize(static_cast<hipEvent_t>(event)), "event sync");
+    });
+}
+
+int apex_hip_event_elapsed_ms(void *start, void *stop, float *ms) {
+    return guard([&] {
+        require(ms != nullptr, "ms is null");
+        hip_check(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                      static_cast<hipEvent_t>(stop)),
+                  "event elapsed");
+    });
+}
+
+int apex_hip_set_gemv_waves_per_cu(int waves) {
+    return guard([&] {
+        require(waves >= 1 && waves <= 32, "waves per CU must be in [1, 32]");
+        apex_hip::kTargetWavesPerCU = waves;
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,90 @@
+// Device-side NVFP4 decode helpers for gfx950 (CDNA4).
+//
+// Format (src/nvfp4.h:27-43, shaders/quant.h:7-23): a row of K weights is K/8 uint32
+// code words -- element 8w+i is nibble i (LSB first) of word w -- and K/16 FP8 E4M3
+// scale bytes, one per 16-element block.  w = e2m1(code) * e4m3(scale).
+//
+// Decode strategy (measured on gfx950):
+//  * v_cvt_scalef32_pk_{f32,bf16}_fp4 turns one byte (two nibbles, low nibble first)
+//    into two values with the OCP E2M1 table, which is the reference's table
+//    including code 8 -> -0.0.  Its scale operand contributes only its exponent
+//    (0.75 acts as 0.5), so it is always passed 1.0 and the E4M3 block scale is
+//    applied separately, in fp32.
+//  * E4M3 scales decode with an integer construction that has no NaN encoding, so
+//    0x7F / 0xFF give +-480 exactly as the reference's decoder does (the hardware
+//    fp8 conversion would give NaN there).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace apex_hip {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// E4M3 byte (in the low 8 bits of `b`) -> fp32, reference semantics.
+// Magnitude bits 0eeeemmm placed at float bits 20..26 give 2^(e-127) * (1 + m/8) for
+// e > 0 and the fp32 denormal m * 2^-129 for e == 0; multiplying by 2^120 (exact)
+// yields (1 + m/8) * 2^(e-7) and m/512.  0x7F -> 1.875 * 2^8 = 480.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+    const float mag = __uint_as_float((b & 0x7Fu) << 20) * 0x1p120f;
+    return __uint_as_float(__float_as_uint(mag) | ((b & 0x80u) << 24));
+}
+
+// Eight E2M1 codes of one word -> four bf16 pairs (elements 2j, 2j+1 in pair j).
+__device__ __forceinline__ void e2m1x8_to_bf16(uint32_t w, bf16x2_t out[4]) {
+    out[0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 0);
+    out[1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 1);
+    out[2] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 2);
+    out[3] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 3);
+}
+
+// Eight E2M1 codes of one word -> eight fp32 values.
+__device__ __forceinline__ void e2m1x8_to_f32(uint32_t w, f32x2_t out[4]) {
+    out[0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+    out[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+    out[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+    out[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))
+        return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// GeLU, tanh approximation, fp32 constants of shaders/geglu.metal:15-16.
+__device__ __forceinline__ float gelu_tanh(float g) {
+    const float t = tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g));
+    return 0.5f * g * (1.0f + t);
+}
+
+// Sum over aligned groups of G lanes (G in {8, 16, 32, 64}) of a wave64; every lane
+// of a group receives the group total.  DPP within rows of 16, then cross-row swaps.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G == 8 || G == 16 || G == 32 || G == 64, "group size");
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)); // row_half_mirror
+    if constexpr (G >= 16)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)); // row_mirror
+    if constexpr (G >= 32)
+        v += __shfl_xor(v, 16, 64);
+    if constexpr (G >= 64)
+        v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+} // namespace apex_hip

@@ -1,0 +1,219 @@
+"""Seeded synthetic inputs for the NVFP4 matmul path (numpy only).
+
+Weights use the reference's NVFP4 layout (src/ops.h:9-16, src/nvfp4.h:27-43):
+codes are uint32 [rows, K/8] with element 8w+i in nibble i (LSB first) of word w,
+scales are uint8 [rows, K/16] FP8 E4M3 codes.  Distributions:
+
+* activations and router logits: N(0,1) rounded to bf16 (round-to-nearest-even);
+* codes: every nibble uniform over the 16 E2M1 codes (uniform random bytes);
+* scales: |N(0,1)| * 0.05 rounded to E4M3 (round-to-nearest-even, saturating);
+* per-tensor FP32 scale: 1.0.
+
+Draw order inside every builder is fixed (documented per function), so a seed pins
+the bytes.  tests/test_synth.py pins the generator with SHA-256 digests.
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+
+E2M1_VALUES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                        -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0], dtype=np.float32)
+
+# Byte offsets of the six pieces of one expert slot, in the order tools/repack.py:182-189
+# fixes (gate W, gate S, up W, up S, down W, down S), and the 16 KiB-aligned stride.
+PIECES = ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")
+SLOT_ALIGN = 16384
+
+
+def bf16_from_f32(a) -> np.ndarray:
+    """Round float32 to bf16 bits (uint16), nearest-even."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def e4m3_from_f32(v) -> np.ndarray:
+    """Round float32 to FP8 E4M3 codes, nearest-even, saturating at +-448."""
+    v = np.asarray(v, dtype=np.float32).astype(np.float64)
+    sign = np.signbit(v).astype(np.uint8) << 7
+    a = np.abs(v)
+    out = np.zeros(a.shape, dtype=np.uint8)
+    sub = a < 2.0 ** -6
+    out[sub] = np.rint(a[sub] * 512.0).astype(np.uint8)  # 8 lands exactly on code 0x08
+    nrm = ~sub
+    an = np.minimum(a[nrm], 464.0)
+    frac, ex = np.frexp(an)  # an = frac * 2^ex, frac in [0.5, 1)
+    ex = ex - 1
+    mant = np.rint((2.0 * frac - 1.0) * 8.0)
+    carry = mant == 8.0
+    mant[carry] = 0.0
+    ex[carry] += 1
+    code = ((ex + 7) << 3).astype(np.int64) | mant.astype(np.int64)
+    code[(an >= 464.0) | (code > 0x7E)] = 0x7E
+    out[nrm] = code.astype(np.uint8)
+    return out | sign
+
+
+def e4m3_to_f32(b) -> np.ndarray:
+    """Decode E4M3 codes like src/nvfp4.h:17-25 (0x7F/0xFF -> +-480, no NaN)."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.int64)
+    e = (b >> 3) & 0xF
+    m = (b & 7).astype(np.float64)
+    v = np.where(e == 0, m / 512.0, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    return np.where(b & 0x80, -v, v).astype(np.float32)
+
+
+def normal_bf16(rng: np.random.Generator, shape) -> np.ndarray:
+    return bf16_from_f32(rng.standard_normal(shape, dtype=np.float32))
+
+
+@dataclasses.dataclass
+class Nvfp4Weights:
+    codes: np.ndarray   # uint32 [rows, K/8]
+    scales: np.ndarray  # uint8  [rows, K/16]
+    tensor_scale: float = 1.0
+
+    @property
+    def rows(self) -> int:
+        return self.codes.shape[0]
+
+    @property
+    def K(self) -> int:
+        return self.codes.shape[1] * 8
+
+    def dequant(self) -> np.ndarray:
+        """fp32 [rows, K] = e2m1 * e4m3 * tensor_scale (exact for a power-of-two scale)."""
+        c = self.codes.view(np.uint8)
+        lo = (c & 0xF).astype(np.int64)
+        hi = (c >> 4).astype(np.int64)
+        nib = np.stack([lo, hi], axis=-1).reshape(self.rows, self.K)
+        w = E2M1_VALUES[nib] * np.repeat(e4m3_to_f32(self.scales), 16, axis=1)
+        return (w * np.float32(self.tensor_scale)).astype(np.float32)
+
+
+def nvfp4_weights(rng: np.random.Generator, rows: int, K: int) -> Nvfp4Weights:
+    """Draw order: code bytes (rows*K/2 uniform uint8), then rows*K/16 normals for scales."""
+    if K % 16:
+        raise ValueError("K must be a multiple of 16")
+    codes = rng.integers(0, 256, size=rows * K // 2, dtype=np.uint8)
+    codes = codes.view(np.uint32).reshape(rows, K // 8)
+    scales = e4m3_from_f32(np.abs(rng.standard_normal(rows * K // 16, dtype=np.float32)) * 0.05)
+    return Nvfp4Weights(codes, scales.reshape(rows, K // 16))
+
+
+# ---------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------
+
+def gemv_case(seed: int = 0, tokens: int = 1, rows: int = 2048, K: int = 2048):
+    """Single NVFP4 GEMV (2048x2048 at batch 1 by default).  Draws: W, then x [T,K]."""
+    rng = np.random.default_rng(seed)
+    w = nvfp4_weights(rng, rows, K)
+    x = normal_bf16(rng, (tokens, K))
+    return x, w
+
+
+def geglu_case(seed: int = 0, tokens: int = 1, rows: int = 21504, K: int = 5376):
+    """Decode fused GeGLU.  Draws: x [T,K], gate W, up W."""
+    rng = np.random.default_rng(seed)
+    x = normal_bf16(rng, (tokens, K))
+    gate = nvfp4_weights(rng, rows, K)
+    up = nvfp4_weights(rng, rows, K)
+    return x, gate, up
+
+
+def gemm_case(seed: int = 0, M: int = 2048, N: int = 21504, K: int = 5376):
+    """Prefill dense GEMM A[M,K] x W[N,K]^T.  Draws: W, then A."""
+    rng = np.random.default_rng(seed)
+    w = nvfp4_weights(rng, N, K)
+    a = normal_bf16(rng, (M, K))
+    return a, w
+
+
+@dataclasses.dataclass
+class ExpertSlots:
+    """128 experts in the fixed-stride slot format of tools/repack.py:180-257."""
+    data: np.ndarray            # uint8 [E * stride]
+    stride: int
+    offsets: dict               # piece name -> byte offset inside a slot
+    E: int
+    H: int
+    I: int
+
+    def piece(self, e: int, name: str) -> np.ndarray:
+        I, H = self.I, self.H
+        base = e * self.stride + self.offsets[name]
+        shapes = {"gate_w": (I, H // 8, np.uint32), "gate_s": (I, H // 16, np.uint8),
+                  "up_w": (I, H // 8, np.uint32), "up_s": (I, H // 16, np.uint8),
+                  "down_w": (H, I // 8, np.uint32), "down_s": (H, I // 16, np.uint8)}
+        r, c, dt = shapes[name]
+        n = r * c * np.dtype(dt).itemsize
+        return self.data[base:base + n].view(dt).reshape(r, c)
+
+
+def slot_layout(H: int, I: int):
+    sizes = {"gate_w": I * H // 2, "gate_s": I * H // 16, "up_w": I * H // 2,
+             "up_s": I * H // 16, "down_w": H * I // 2, "down_s": H * I // 16}
+    offsets, off = {}, 0
+    for name in PIECES:
+        offsets[name] = off
+        off += sizes[name]
+    stride = (off + SLOT_ALIGN - 1) // SLOT_ALIGN * SLOT_ALIGN
+    return offsets, stride, off
+
+
+def expert_slots(rng: np.random.Generator, E: int, H: int, I: int) -> ExpertSlots:
+    """Draws per expert e = 0..E-1: gate W, up W, down W (each codes then scales)."""
+    offsets, stride, _ = slot_layout(H, I)
+    data = np.zeros(E * stride, dtype=np.uint8)
+    for e in range(E):
+        base = e * stride
+        for proj, (rows, K) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            w = nvfp4_weights(rng, rows, K)
+            cw = w.codes.view(np.uint8).reshape(-1)
+            cs = w.scales.reshape(-1)
+            o = base + offsets[proj + "_w"]
+            data[o:o + cw.size] = cw
+            o = base + offsets[proj + "_s"]
+            data[o:o + cs.size] = cs
+    return ExpertSlots(data, stride, offsets, E, H, I)
+
+
+def moe_decode_case(seed: int = 0, tokens: int = 16, H: int = 2816, I: int = 704, E: int = 128):
+    """MoE decode.  Draws: x [T,H], logits [T,E] (both N(0,1) bf16), then expert slots."""
+    rng = np.random.default_rng(seed)
+    x = normal_bf16(rng, (tokens, H))
+    logits = normal_bf16(rng, (tokens, E))
+    slots = expert_slots(rng, E, H, I)
+    return x, logits, slots
+
+
+def zipf_logits(rng: np.random.Generator, tokens: int, E: int, s: float = 1.1,
+                n_empty: int = 8) -> np.ndarray:
+    """Skewed router logits: popularity p_e ~ rank_e^-s over a seeded permutation of
+    experts, the n_empty lowest-ranked experts get p = 0 (logit -inf, never routed);
+    logits[t,e] = bf16(log p_e + Gumbel(t,e)).  Draws: permutation, then T*E Gumbels."""
+    rank = rng.permutation(E) + 1
+    p = rank.astype(np.float64) ** -s
+    p[rank > E - n_empty] = 0.0
+    p /= p.sum()
+    with np.errstate(divide="ignore"):
+        logp = np.log(p)
+    g = rng.gumbel(size=(tokens, E))
+    return bf16_from_f32((logp[None, :] + g).astype(np.float32))
+
+
+def moe_prefill_case(seed: int = 0, tokens: int = 4096, H: int = 2816, I: int = 704,
+                     E: int = 128):
+    """MoE prefill with Zipf(1.1) routing.  Draws: x [T,H], skewed logits, expert slots."""
+    rng = np.random.default_rng(seed)
+    x = normal_bf16(rng, (tokens, H))
+    logits = zipf_logits(rng, tokens, E)
+    slots = expert_slots(rng, E, H, I)
+    return x, logits, slots

@@ -1,0 +1,211 @@
+/*
+ * apex_hip.h -- C ABI of the MI355X (gfx950) HIP backend for APEX's NVFP4 matmul path.
+ *
+ * Three layers, all plain C (pointers, sizes, no HIP or C++ types):
+ *
+ *  1. The backend object.  One-for-one with the reference's apex::Backend interface
+ *     (src/backend/backend.h:39-63) and its Metal implementation
+ *     (src/backend/metal_backend.{h,cpp}); the C++ class apex::HipBackend
+ *     (apex_amd/host/hip_backend.h) is a thin adapter over these calls, and the
+ *     reference's src/ops.h calls it unchanged.  Kernels are selected by name as in
+ *     metal_backend.cpp:54-82 and bound by position as in metal_backend.cpp:162-167.
+ *  2. Direct entry points on device pointers and a stream, for hosts that manage
+ *     their own device memory.  The backend's kernels call the same code.
+ *  3. Plumbing (device memory, copies, streams, events) for hosts without their own
+ *     HIP runtime, e.g. Python through ctypes.
+ *
+ * Every function returns APEX_HIP_OK (0) on success or a nonzero APEX_HIP_E_* code;
+ * apex_hip_last_error() then describes the failure (per calling thread).  The
+ * reference throws std::runtime_error in the same places (metal_backend.cpp:18-34,
+ * 61-76, 91-93, 117-119, 169-171); apex::HipBackend turns nonzero codes back into
+ * std::runtime_error.  A backend object is not thread-safe (one stream, one host
+ * thread), like MetalBackend.
+ */
+#ifndef APEX_HIP_H
+#define APEX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define APEX_HIP_ABI_VERSION 1
+
+enum {
+    APEX_HIP_OK = 0,
+    APEX_HIP_E_INVALID = 1,        /* bad argument value or shape */
+    APEX_HIP_E_UNKNOWN_KERNEL = 2, /* metal_backend.cpp:61-64 "cannot find function" */
+    APEX_HIP_E_ARGS = 3,           /* wrong argument count or kind for a kernel */
+    APEX_HIP_E_ALIGN = 4,          /* metal_backend.cpp:89-93 wrapNoCopy alignment */
+    APEX_HIP_E_DEVICE = 5,         /* HIP runtime error or no device */
+    APEX_HIP_E_OOM = 6,            /* allocation failed (metal_backend.cpp:117-119) */
+    APEX_HIP_E_THREADGROUP = 7     /* metal_backend.cpp:169-171 "threadgroup too large" */
+};
+
+typedef struct apex_hip_backend apex_hip_backend;
+typedef struct apex_hip_buffer apex_hip_buffer;
+
+/* src/backend/backend.h:15-29 (Arg): a buffer plus byte offset, or `size` value bytes
+ * at `bytes` (copied when the kernel is queued, so temporaries are fine). */
+typedef struct {
+    apex_hip_buffer *buffer;
+    size_t offset;
+    const void *bytes;
+    size_t size;
+} apex_hip_arg;
+
+/* src/backend/backend.h:33-37 (Dim3). */
+typedef struct {
+    uint32_t x, y, z;
+} apex_hip_dim3;
+
+/* Description of the failure of the last call that returned nonzero on this thread. */
+const char *apex_hip_last_error(void);
+int apex_hip_abi_version(void);
+
+/* ---------------------------------------------------------------------------------
+ * 1. Backend object
+ * -------------------------------------------------------------------------------*/
+
+/* MetalBackend::MetalBackend (metal_backend.cpp:14-35): opens `device` and creates
+ * one in-order stream.  The kernels are linked in, so there is no library path. */
+int apex_hip_backend_create(int device, apex_hip_backend **out);
+
+/* MetalBackend::~MetalBackend (metal_backend.cpp:37-45). */
+void apex_hip_backend_destroy(apex_hip_backend *backend);
+
+/* MetalBackend::deviceName (metal_backend.cpp:47-49): gcnArchName of the device. */
+int apex_hip_device_name(apex_hip_backend *backend, char *buf, size_t len);
+
+/* Backend::wrapNoCopy (backend.h:45-46, metal_backend.cpp:88-107).  `host` and
+ * `bytes` must be multiples of 16384, as in the reference.  HBM is not the host's
+ * memory, so the bytes are uploaded once, before the first kernel that reads the
+ * buffer; `host` must stay valid until release.  Not counted by any tracker. */
+int apex_hip_wrap_no_copy(apex_hip_backend *backend, void *host, size_t bytes,
+                          apex_hip_buffer **out);
+
+/* Backend::allocate (backend.h:48-49, metal_backend.cpp:113-126): `bytes` of
+ * zero-filled device memory.  `category` is kept for the caller's memory tracker. */
+int apex_hip_allocate(apex_hip_backend *backend, size_t bytes, const char *category,
+                      apex_hip_buffer **out);
+
+/* Backend::contents (backend.h:51-52, metal_backend.cpp:131): a host pointer to the
+ * buffer's bytes.  The reference's memory is unified; here the buffer has a host
+ * mirror: this call waits for queued kernels if the device copy is newer, downloads
+ * it, and marks the host copy as the one to upload before the next kernel that uses
+ * the buffer.  Do not call it inside timed regions. */
+int apex_hip_contents(apex_hip_backend *backend, apex_hip_buffer *buffer, void **out);
+
+/* Backend::release (backend.h:54-55, metal_backend.cpp:136-149). */
+int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
+
+/* Backend::run (backend.h:57-60, metal_backend.cpp:151-174): queue kernel `kernel`
+ * with positional arguments.  Returns at once; kernels run in queue order.
+ * Kernels and argument lists (B = buffer, U = uint32 value, F = float value):
+ *   matmul_nvfp4      B input f32 [T,K], B weights u32 [rows,K/8], B scales u8
+ *                     [rows,K/16], B output f32 [T,rows], U hidden_dim K, U w_rows.
+ *                     T = threadgroups.y and rows covered = min(w_rows,
+ *                     threadgroups.x * threads/32), as the reference launch
+ *                     (src/ops.h:34-46, shaders/matmul.metal:14-18) implies.
+ *   geglu_f32         B gate, B up, B output, U count (in place allowed);
+ *                     src/ops.h:48-55, shaders/geglu.metal:6-24.
+ *   matmul_nvfp4_bf16 B input bf16 [T,K], B weights, B scales, B output bf16 [T,rows],
+ *                     U hidden_dim, U w_rows, U tokens, F tensor_scale.
+ *   geglu_nvfp4_f32   B input f32, B gate weights, B gate scales, B up weights,
+ *   geglu_nvfp4_bf16  B up scales, B output [T,rows], U hidden_dim, U w_rows,
+ *                     U tokens, F gate tensor_scale, F up tensor_scale:
+ *                     gelu_tanh(gate.x) * (up.x) in one pass (src/ops.h:65-67 fused).
+ *   dequant_nvfp4_f32 B weights, B scales, B output [rows,K], U hidden_dim,
+ *   dequant_nvfp4_bf16 U w_rows, F tensor_scale (src/nvfp4.h:27-43 on the device).
+ * For the kernels after geglu_f32 the launch shape is chosen by the backend; the
+ * caller's threadgroups/threads must only be nonzero. */
+int apex_hip_run(apex_hip_backend *backend, const char *kernel, const apex_hip_arg *args,
+                 size_t nargs, apex_hip_dim3 threadgroups, apex_hip_dim3 threads_per_group);
+
+/* Backend::sync (backend.h:62-63, metal_backend.cpp:176-184): wait for all queued
+ * kernels. */
+int apex_hip_sync(apex_hip_backend *backend);
+
+/* No reference counterpart (the reference's buffers are host-visible): the device
+ * address of a buffer (valid until release), its length, and the backend's stream
+ * (a hipStream_t) for hosts mixing backend kernels with direct entry points. */
+int apex_hip_buffer_device_ptr(apex_hip_buffer *buffer, void **out);
+size_t apex_hip_buffer_length(apex_hip_buffer *buffer);
+void *apex_hip_backend_stream(apex_hip_backend *backend);
+
+/* Registry introspection and argument validation (host only, no device needed):
+ * the checks apex_hip_run applies before anything touches the GPU. */
+int apex_hip_kernel_count(void);
+const char *apex_hip_kernel_name(int index);
+const char *apex_hip_kernel_signature(const char *kernel);
+int apex_hip_validate_run(const char *kernel, const apex_hip_arg *args, size_t nargs,
+                          apex_hip_dim3 threadgroups, apex_hip_dim3 threads_per_group);
+
+/* ---------------------------------------------------------------------------------
+ * 2. Direct entry points: device pointers, `stream` is a hipStream_t (NULL = default).
+ *    W is NVFP4 [rows, K]: codes uint32 [rows, K/8], scales E4M3 [rows, K/16];
+ *    K % 16 == 0.  tensor_scale multiplies every weight (1.0 = reference).
+ * -------------------------------------------------------------------------------*/
+
+/* shaders/matmul.metal:4-53 / src/tests/cpu_ref.h:48-63: out[t, r] = sum_k W[r,k] x[t,k]
+ * with fp32 activations and outputs. */
+int apex_nvfp4_matmul_f32(const float *x, const uint32_t *codes, const uint8_t *scales,
+                          float tensor_scale, float *out, uint32_t tokens, uint32_t rows,
+                          uint32_t K, void *stream);
+
+/* Same product with bf16 activations and bf16 outputs (fp32 accumulation). */
+int apex_nvfp4_matmul_bf16(const uint16_t *x, const uint32_t *codes, const uint8_t *scales,
+                           float tensor_scale, uint16_t *out, uint32_t tokens, uint32_t rows,
+                           uint32_t K, void *stream);
+
+/* src/ops.h:65-67 fused: out[t, r] = gelu_tanh(Wg[r].x_t) * (Wu[r].x_t). */
+int apex_nvfp4_geglu_f32(const float *x, const uint32_t *gate_codes, const uint8_t *gate_scales,
+                         float gate_tensor_scale, const uint32_t *up_codes,
+                         const uint8_t *up_scales, float up_tensor_scale, float *out,
+                         uint32_t tokens, uint32_t rows, uint32_t K, void *stream);
+int apex_nvfp4_geglu_bf16(const uint16_t *x, const uint32_t *gate_codes,
+                          const uint8_t *gate_scales, float gate_tensor_scale,
+                          const uint32_t *up_codes, const uint8_t *up_scales,
+                          float up_tensor_scale, uint16_t *out, uint32_t tokens, uint32_t rows,
+                          uint32_t K, void *stream);
+
+/* shaders/geglu.metal:6-24: out[i] = gelu_tanh(gate[i]) * up[i]; out may alias gate. */
+int apex_geglu_f32(const float *gate, const float *up, float *out, uint32_t count,
+                   void *stream);
+
+/* src/nvfp4.h:27-43 on the device: out[r, k] = e2m1 * e4m3 * tensor_scale. */
+int apex_nvfp4_dequant_f32(const uint32_t *codes, const uint8_t *scales, float tensor_scale,
+                           float *out, uint32_t rows, uint32_t K, void *stream);
+int apex_nvfp4_dequant_bf16(const uint32_t *codes, const uint8_t *scales, float tensor_scale,
+                            uint16_t *out, uint32_t rows, uint32_t K, void *stream);
+
+/* ---------------------------------------------------------------------------------
+ * 3. Plumbing (no reference counterpart).
+ * -------------------------------------------------------------------------------*/
+int apex_hip_device_count(int *out);
+int apex_hip_set_device(int device);
+int apex_hip_malloc(size_t bytes, void **out);
+int apex_hip_free(void *ptr);
+int apex_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int apex_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int apex_hip_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int apex_hip_memset(void *dst, int value, size_t bytes);
+int apex_hip_device_synchronize(void);
+int apex_hip_stream_create(void **out);
+int apex_hip_stream_destroy(void *stream);
+int apex_hip_stream_synchronize(void *stream);
+int apex_hip_event_create(void **out);
+int apex_hip_event_destroy(void *event);
+int apex_hip_event_record(void *event, void *stream);
+int apex_hip_event_synchronize(void *event);
+int apex_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* Launch tuning of the GEMV kernels: target resident waves per CU (default 8). */
+int apex_hip_set_gemv_waves_per_cu(int waves);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* APEX_HIP_H */

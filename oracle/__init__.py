@@ -1,0 +1,229 @@
+"""Python access to the CPU oracle (liboracle.so) and, where it was built, to the
+reference's own CPU code (oracle/_ref/libapexref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg.  The product path (apex_amd) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+REF_PATH = HERE / "_ref" / "libapexref.so"
+
+_P = C.c_void_p
+_SZ = C.c_size_t
+_F = C.c_float
+
+
+class ExpertLayout(C.Structure):
+    _fields_ = [("slot_stride", _SZ), ("gate_w", _SZ), ("gate_s", _SZ), ("up_w", _SZ),
+                ("up_s", _SZ), ("down_w", _SZ), ("down_s", _SZ)]
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = C.CDLL(str(LIB_PATH))
+        L.orc_e2m1_to_float.restype = _F
+        L.orc_e2m1_to_float.argtypes = [C.c_uint32]
+        L.orc_e4m3_to_float.restype = _F
+        L.orc_e4m3_to_float.argtypes = [C.c_uint8]
+        L.orc_decode_row.argtypes = [_P, _P, _P, _SZ]
+        L.orc_matvec_nvfp4.argtypes = [_P, _P, _P, _P, _SZ, _SZ, _SZ, _F]
+        L.orc_matvec_nvfp4_rows.argtypes = [_P, _P, _P, _P, _SZ, _SZ, _P, _SZ, _F]
+        L.orc_gelu_tanh.restype = _F
+        L.orc_gelu_tanh.argtypes = [_F]
+        L.orc_geglu.argtypes = [_P, _P, _P, _SZ]
+        L.orc_dense_mlp.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ]
+        L.orc_diff.argtypes = [_P, _P, _SZ, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        L.orc_moe_route.argtypes = [_P, _SZ, _SZ, _SZ, _P, _P]
+        L.orc_moe_ffn.argtypes = [_P, C.POINTER(ExpertLayout), _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ]
+        L.orc_e4m3_from_float.restype = C.c_uint8
+        L.orc_e4m3_from_float.argtypes = [_F]
+        L.orc_bf16_to_float.restype = _F
+        L.orc_bf16_to_float.argtypes = [C.c_uint16]
+        L.orc_float_to_bf16.restype = C.c_uint16
+        L.orc_float_to_bf16.argtypes = [_F]
+        _lib = L
+    return _lib
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a, a.ctypes.data
+
+
+def e2m1(code: int) -> float:
+    return lib().orc_e2m1_to_float(code)
+
+
+def e4m3(byte: int) -> float:
+    return lib().orc_e4m3_to_float(byte)
+
+
+def decode(codes, scales) -> np.ndarray:
+    """Dequantise every row: fp32 [rows, K]."""
+    codes, pc = _c(codes, np.uint32)
+    scales, ps = _c(scales, np.uint8)
+    rows, K = codes.shape[0], codes.shape[1] * 8
+    out = np.empty((rows, K), np.float32)
+    for r in range(rows):
+        lib().orc_decode_row(pc + r * K // 2, ps + r * K // 16, out[r].ctypes.data, K)
+    return out
+
+
+def matvec(codes, scales, x, tensor_scale: float = 1.0) -> np.ndarray:
+    """fp32 [T, rows] = W x (fp64 accumulation), x fp32 [T, K]."""
+    codes, pc = _c(codes, np.uint32)
+    scales, ps = _c(scales, np.uint8)
+    x, px = _c(np.atleast_2d(x), np.float32)
+    rows, K = codes.shape[0], codes.shape[1] * 8
+    T = x.shape[0]
+    assert x.shape[1] == K
+    out = np.empty((T, rows), np.float32)
+    lib().orc_matvec_nvfp4(pc, ps, px, out.ctypes.data, T, rows, K, tensor_scale)
+    return out
+
+
+def matvec_rows(codes, scales, x, row_ids, tensor_scale: float = 1.0) -> np.ndarray:
+    """fp32 [T, len(row_ids)]: the matvec restricted to the listed rows."""
+    codes, pc = _c(codes, np.uint32)
+    scales, ps = _c(scales, np.uint8)
+    x, px = _c(np.atleast_2d(x), np.float32)
+    ids, pi = _c(row_ids, np.int64)
+    K = codes.shape[1] * 8
+    T = x.shape[0]
+    out = np.empty((T, ids.size), np.float32)
+    lib().orc_matvec_nvfp4_rows(pc, ps, px, out.ctypes.data, T, K, pi, ids.size, tensor_scale)
+    return out
+
+
+def gelu(g: float) -> float:
+    return lib().orc_gelu_tanh(g)
+
+
+def geglu(gate, up) -> np.ndarray:
+    gate, pg = _c(gate, np.float32)
+    up, pu = _c(up, np.float32)
+    out = np.empty_like(gate)
+    lib().orc_geglu(pg, pu, out.ctypes.data, gate.size)
+    return out
+
+
+def dense_mlp(gate, up, down, x) -> np.ndarray:
+    """gate/up/down: (codes, scales) pairs; x fp32 [T, H] -> fp32 [T, H]."""
+    gc, pgc = _c(gate[0], np.uint32)
+    gs, pgs = _c(gate[1], np.uint8)
+    uc, puc = _c(up[0], np.uint32)
+    us, pus = _c(up[1], np.uint8)
+    dc, pdc = _c(down[0], np.uint32)
+    ds, pds = _c(down[1], np.uint8)
+    x, px = _c(np.atleast_2d(x), np.float32)
+    I, H = gc.shape[0], gc.shape[1] * 8
+    out = np.empty((x.shape[0], H), np.float32)
+    lib().orc_dense_mlp(pgc, pgs, puc, pus, pdc, pds, px, out.ctypes.data, x.shape[0], H, I)
+    return out
+
+
+def diff(a, b):
+    """(max_abs, rel_l2) as src/tests/cpu_ref.h:27-46."""
+    a, pa = _c(np.ravel(a), np.float32)
+    b, pb = _c(np.ravel(b), np.float32)
+    assert a.size == b.size
+    mx, rel = C.c_double(), C.c_double()
+    lib().orc_diff(pa, pb, a.size, C.byref(mx), C.byref(rel))
+    return mx.value, rel.value
+
+
+def moe_route(logits, k: int):
+    """Top-k (ties to the lower id) + softmax over the k: ids int32 [T,k], w fp32 [T,k]."""
+    logits, pl = _c(np.atleast_2d(logits), np.float32)
+    T, E = logits.shape
+    ids = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    lib().orc_moe_route(pl, T, E, k, ids.ctypes.data, w.ctypes.data)
+    return ids, w
+
+
+def moe_ffn(slots, x, ids, weights) -> np.ndarray:
+    """slots: apex_amd.synth.ExpertSlots; x fp32 [T,H]; ids/weights [T,k] -> fp32 [T,H]."""
+    data, pd = _c(slots.data, np.uint8)
+    x, px = _c(np.atleast_2d(x), np.float32)
+    ids, pi = _c(ids, np.int32)
+    w, pw = _c(weights, np.float32)
+    o = slots.offsets
+    lay = ExpertLayout(slots.stride, o["gate_w"], o["gate_s"], o["up_w"], o["up_s"],
+                       o["down_w"], o["down_s"])
+    T, k = ids.shape
+    y = np.empty((T, slots.H), np.float32)
+    lib().orc_moe_ffn(pd, C.byref(lay), px, pi, pw, y.ctypes.data, T, k, slots.H, slots.I)
+    return y
+
+
+def e4m3_from_float(v: float) -> int:
+    return lib().orc_e4m3_from_float(v)
+
+
+def bf16_to_float(b: int) -> float:
+    return lib().orc_bf16_to_float(b)
+
+
+def float_to_bf16(f: float) -> int:
+    return lib().orc_float_to_bf16(f)
+
+
+# ---- the reference's own CPU code, compiled from its sources (where available) ----
+
+def ref_available() -> bool:
+    return REF_PATH.exists()
+
+
+def ref():
+    """ctypes handle on oracle/_ref/libapexref.so (built from src/nvfp4.h, src/tests/cpu_ref.h)."""
+    global _ref
+    if _ref is None:
+        if not REF_PATH.exists():
+            raise ImportError(f"{REF_PATH} missing (reference not mounted when built)")
+        R = C.CDLL(str(REF_PATH))
+        R.ref_e2m1_to_float.restype = _F
+        R.ref_e2m1_to_float.argtypes = [C.c_uint32]
+        R.ref_e4m3_to_float.restype = _F
+        R.ref_e4m3_to_float.argtypes = [C.c_uint8]
+        R.ref_decode_row.argtypes = [_P, _P, _P, _SZ]
+        R.ref_matvec_nvfp4.argtypes = [_P, _P, _P, _P, _SZ, _SZ, _SZ]
+        R.ref_gelu_tanh.restype = _F
+        R.ref_gelu_tanh.argtypes = [_F]
+        R.ref_diff.argtypes = [_P, _P, _SZ, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        _ref = R
+    return _ref
+
+
+def ref_matvec(codes, scales, x) -> np.ndarray:
+    codes, pc = _c(codes, np.uint32)
+    scales, ps = _c(scales, np.uint8)
+    x, px = _c(np.atleast_2d(x), np.float32)
+    rows, K = codes.shape[0], codes.shape[1] * 8
+    out = np.empty((x.shape[0], rows), np.float32)
+    ref().ref_matvec_nvfp4(pc, ps, px, out.ctypes.data, x.shape[0], rows, K)
+    return out
+
+
+def ref_decode(codes, scales) -> np.ndarray:
+    codes, pc = _c(codes, np.uint32)
+    scales, ps = _c(scales, np.uint8)
+    rows, K = codes.shape[0], codes.shape[1] * 8
+    out = np.empty((rows, K), np.float32)
+    for r in range(rows):
+        ref().ref_decode_row(pc + r * K // 2, ps + r * K // 16, out[r].ctypes.data, K)
+    return out

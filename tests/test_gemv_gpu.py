@@ -1,0 +1,144 @@
+"""GPU parity of the decode-regime kernels (GEMV, fused GeGLU, dequant) against the
+CPU oracle, through the C ABI.  Oracle = fp64 restatement of src/tests/cpu_ref.h."""
+import numpy as np
+import pytest
+
+import oracle
+from apex_amd import hip, synth
+from tests.helpers import TOL_BF16, TOL_REF_GATE, all_codes_weights, bf16, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return hip.DeviceArray.from_numpy(a)
+
+
+def run_matmul(x, w, bf16_io, tensor_scale=1.0):
+    T, K = x.shape
+    out = hip.DeviceArray((T, w.rows), np.uint16 if bf16_io else np.float32)
+    f = hip.nvfp4_matmul_bf16 if bf16_io else hip.nvfp4_matmul_f32
+    f(dev(x), dev(w.codes), dev(w.scales), out, T, w.rows, K, tensor_scale)
+    hip.synchronize()
+    return out.numpy()
+
+
+def test_dequant_bit_exact_every_code_and_scale():
+    """src/nvfp4.h:27-43 on the device: all 16 x 256 (code, scale) pairs, bit for bit,
+    including code 8 -> -0.0 and scales 0x7F/0xFF -> +-480."""
+    w = all_codes_weights()
+    want = oracle.decode(w.codes, w.scales)
+    out = hip.DeviceArray((w.rows, w.K), np.float32)
+    hip.nvfp4_dequant(dev(w.codes), dev(w.scales), out, w.rows, w.K)
+    got = out.numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    outb = hip.DeviceArray((w.rows, w.K), np.uint16)
+    hip.nvfp4_dequant(dev(w.codes), dev(w.scales), outb, w.rows, w.K)
+    # every e2m1 x e4m3 product has <= 6 significant bits: bf16 holds it exactly
+    assert np.array_equal(bf16(outb.numpy()).view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_random_matches_reference_decoder():
+    _, w = synth.gemv_case(seed=3, rows=64, K=2048)
+    out = hip.DeviceArray((w.rows, w.K), np.float32)
+    hip.nvfp4_dequant(dev(w.codes), dev(w.scales), out, w.rows, w.K)
+    assert np.array_equal(out.numpy().view(np.uint32), oracle.decode(w.codes, w.scales).view(np.uint32))
+
+
+def test_gemv_2048_f32_contract():
+    """Single NVFP4 GEMV 2048x2048 (the reference op), fp32 in/out, seed 0."""
+    x, w = synth.gemv_case(seed=0)
+    xf = bf16(x)
+    got = run_matmul(xf, w, bf16_io=False)
+    want = oracle.matvec(w.codes, w.scales, xf)
+    assert rel_l2(got, want) < TOL_REF_GATE
+
+
+def test_gemv_2048_bf16():
+    """Same case with bf16 activations and bf16 output (the configured dtype)."""
+    x, w = synth.gemv_case(seed=0)
+    got = bf16(run_matmul(x, w, bf16_io=True))
+    want = oracle.matvec(w.codes, w.scales, bf16(x))
+    assert rel_l2(got, want) < TOL_BF16
+    # the kernel's fp32 result rounds to the oracle's bf16 for nearly every element
+    assert np.mean(got == bf16(synth.bf16_from_f32(want))) > 0.97
+
+
+@pytest.mark.parametrize("rows,K,T", [
+    (1, 16, 1), (3, 48, 2), (7, 32, 1), (64, 704, 3), (37, 2112, 5), (300, 2816, 1),
+    (128, 5376, 2), (16, 8192, 4), (9, 8208, 2), (33, 1024, 16), (200, 256, 9),
+])
+def test_gemv_shapes_f32(rows, K, T):
+    rng = np.random.default_rng(rows * 1000 + K + T)
+    w = synth.nvfp4_weights(rng, rows, K)
+    x = rng.standard_normal((T, K), dtype=np.float32)
+    got = run_matmul(x, w, bf16_io=False)
+    want = oracle.matvec(w.codes, w.scales, x)
+    assert rel_l2(got, want) < TOL_REF_GATE
+
+
+@pytest.mark.parametrize("rows,K,T", [(5, 16, 1), (64, 704, 1), (300, 2816, 3), (96, 5376, 1),
+                                      (17, 8192, 2), (40, 4112, 1)])
+def test_gemv_shapes_bf16(rows, K, T):
+    rng = np.random.default_rng(rows + 7 * K + T)
+    w = synth.nvfp4_weights(rng, rows, K)
+    x = synth.normal_bf16(rng, (T, K))
+    got = bf16(run_matmul(x, w, bf16_io=True))
+    want = oracle.matvec(w.codes, w.scales, bf16(x))
+    assert rel_l2(got, want) < TOL_BF16
+
+
+def test_tensor_scale_is_linear():
+    """The per-tensor FP32 scale multiplies the output (power of two: exactly)."""
+    x, w = synth.gemv_case(seed=1, rows=256, K=2048)
+    xf = bf16(x)
+    a = run_matmul(xf, w, bf16_io=False, tensor_scale=1.0)
+    b = run_matmul(xf, w, bf16_io=False, tensor_scale=0.25)
+    assert np.array_equal(b, a * np.float32(0.25))
+    c = run_matmul(xf, w, bf16_io=False, tensor_scale=0.3)
+    assert rel_l2(c, oracle.matvec(w.codes, w.scales, xf, tensor_scale=0.3)) < TOL_REF_GATE
+
+
+def run_geglu(x, gate, up, bf16_io):
+    T, K = x.shape
+    out = hip.DeviceArray((T, gate.rows), np.uint16 if bf16_io else np.float32)
+    f = hip.nvfp4_geglu_bf16 if bf16_io else hip.nvfp4_geglu_f32
+    f(dev(x), dev(gate.codes), dev(gate.scales), dev(up.codes), dev(up.scales), out, T,
+      gate.rows, K)
+    hip.synchronize()
+    return out.numpy()
+
+
+def geglu_oracle(x_f32, gate, up):
+    g = oracle.matvec(gate.codes, gate.scales, x_f32)
+    u = oracle.matvec(up.codes, up.scales, x_f32)
+    return oracle.geglu(g, u)
+
+
+@pytest.mark.parametrize("rows,K,T", [(8, 32, 1), (704, 2816, 1), (333, 2112, 2), (64, 5376, 4)])
+def test_fused_geglu_small(rows, K, T):
+    rng = np.random.default_rng(rows + K + T)
+    x = synth.normal_bf16(rng, (T, K))
+    gate = synth.nvfp4_weights(rng, rows, K)
+    up = synth.nvfp4_weights(rng, rows, K)
+    want = geglu_oracle(bf16(x), gate, up)
+    assert rel_l2(bf16(run_geglu(x, gate, up, True)), want) < TOL_BF16
+    assert rel_l2(run_geglu(bf16(x), gate, up, False), want) < TOL_REF_GATE
+
+
+def test_fused_geglu_decode_full_size():
+    """Decode fused GeGLU at batch 1: x [1,5376], gate/up [21504 x 5376], seed 0."""
+    x, gate, up = synth.geglu_case(seed=0)
+    got = bf16(run_geglu(x, gate, up, True))
+    want = geglu_oracle(bf16(x), gate, up)
+    assert rel_l2(got, want) < TOL_BF16
+
+
+def test_standalone_geglu_f32_in_place():
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal(10001, dtype=np.float32) * 3
+    u = rng.standard_normal(10001, dtype=np.float32)
+    dg, du = dev(g), dev(u)
+    hip.geglu_f32(dg, du, dg, g.size)  # in place, as src/ops.h:67 does
+    hip.synchronize()
+    assert rel_l2(dg.numpy(), oracle.geglu(g, u)) < 1e-6
