@@ -14,17 +14,23 @@ struct GemvArgs {
     float tensor_scale[2];
     void *out;                  // [tokens, out_stride] fp32 or bf16 bits
     uint32_t rows, K, tokens, out_stride;
+    uint32_t sets_per_wave;     // filled by the launcher
+    uint32_t mapping;           // row-set order: 0 grid-strided, 1 per-wave ranges, 2 per-workgroup ranges
 };
 
 enum class GemvMode { PlainF32, PlainBF16, GegluBF16, GegluF32 };
 
 // Tuning knobs (set from the device properties at backend init, or by sweeps).
 extern int kTargetWavesPerCU;
+extern int kGemvMapping;
+extern int kGemvDepth;
 extern int kNumCUs;
 
 hipError_t gemv_launch(const GemvArgs &a, GemvMode mode, bool x_is_bf16, hipStream_t stream);
 hipError_t geglu_f32_launch(const float *gate, const float *up, float *out, uint32_t count,
                             hipStream_t stream);
+// Streaming-read probe over [p, p+bytes) (bytes < 2 GiB); sink needs 8 * CUs words.
+hipError_t read_probe_launch(const void *p, size_t bytes, uint32_t *sink, hipStream_t stream);
 hipError_t dequant_launch(const uint32_t *codes, const uint8_t *scales, void *out, uint32_t rows,
                           uint32_t K, float tensor_scale, bool bf16, hipStream_t stream);
 

@@ -53,9 +53,32 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t *codes
     }
 }
 
+// Streaming-read probe: every lane reads 16-byte pieces of [p, p + bytes) with
+// buffer loads (grid-stride, 4 loads in flight per iteration) and folds them into a
+// checksum so the loads cannot be dropped.  Measures the achievable HBM read rate.
+__global__ __launch_bounds__(kThreads) void read_probe_kernel(const void *p, uint32_t pieces,
+                                                              uint32_t *sink) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(p, pieces * 16u);
+    const uint32_t stride = gridDim.x * kThreads;
+    uint32_t acc = 0;
+    for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < pieces; i += 4 * stride) {
+        u32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            v[u] = load_b128(r, (i + u * stride) * 16u); // past the end reads zeros
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    if (acc == 0x9E3779B9u) // practically never: keeps the loads live
+        sink[blockIdx.x] = acc;
+}
+
 } // namespace
 
-int kTargetWavesPerCU = 8;
+int kTargetWavesPerCU = 12;
+int kGemvMapping = 0;
+int kGemvDepth = 2;
 int kNumCUs = 256;
 
 hipError_t gemv_launch(const GemvArgs &a, GemvMode mode, bool x_is_bf16, hipStream_t stream) {
@@ -82,6 +105,16 @@ hipError_t geglu_f32_launch(const float *gate, const float *up, float *out, uint
         return hipSuccess;
     hipLaunchKernelGGL(geglu_f32_kernel, dim3((count + kThreads - 1) / kThreads), dim3(kThreads),
                        0, stream, gate, up, out, count);
+    return hipGetLastError();
+}
+
+hipError_t read_probe_launch(const void *p, size_t bytes, uint32_t *sink, hipStream_t stream) {
+    const size_t pieces = bytes / 16;
+    if (pieces == 0 || pieces >= (1ull << 27))
+        return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)kNumCUs * 8;
+    hipLaunchKernelGGL(read_probe_kernel, dim3(grid), dim3(kThreads), 0, stream, p,
+                       (uint32_t)pieces, sink);
     return hipGetLastError();
 }
 

@@ -33,6 +33,7 @@ namespace gemv_detail {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
+
 template <typename XT> struct XTraits;
 template <> struct XTraits<float> {
     static constexpr int kPieces = 8; // 16-byte pieces per 32-element chunk
@@ -47,54 +48,83 @@ template <int SLOTS> struct RowRegs {
     uint32_t scales[SLOTS];
 };
 
+// Loads go through buffer descriptors spanning exactly the matrix, so they need no
+// branches or clamps: a row set past the last row reads zeros.  Keeping the loads
+// straight-line lets the compiler count outstanding loads exactly and keep the next
+// row sets' loads in flight while the current one is computed.  Slot s sits at a
+// fixed immediate offset s*G*16 (codes) and s*G*2 (scales) from the lane's base,
+// except the last slot, whose offset adders `last_c`/`last_s` are out of range for
+// lanes past the end of the row, so those lanes read zero codes and zero scales.
 template <int SLOTS, int G>
-__device__ __forceinline__ void load_row(RowRegs<SLOTS> &r, const uint32_t *codes,
-                                         const uint8_t *scales, uint32_t row, bool row_ok,
-                                         int gl, int nchunks, uint32_t K) {
-    const u32x4_t *crow = reinterpret_cast<const u32x4_t *>(codes + (size_t)row * (K / 8));
-    const uint16_t *srow = reinterpret_cast<const uint16_t *>(scales + (size_t)row * (K / 16));
+__device__ __forceinline__ void load_row(RowRegs<SLOTS> &r, __amdgpu_buffer_rsrc_t rc,
+                                         __amdgpu_buffer_rsrc_t rs, uint32_t row, int gl,
+                                         uint32_t K, uint32_t last_c, uint32_t last_s) {
+    const uint32_t co = row * (K / 2) + (uint32_t)gl * 16;
+    const uint32_t so = row * (K / 16) + (uint32_t)gl * 2;
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const int c = gl + s * G;
-        if (row_ok && c < nchunks) {
-            r.codes[s] = __builtin_nontemporal_load(crow + c);
-            r.scales[s] = srow[c];
-        } else {
-            r.codes[s] = u32x4_t{0, 0, 0, 0};
-            r.scales[s] = 0;
-        }
+    for (int s = 0; s < SLOTS - 1; ++s) {
+        r.codes[s] = load_b128<APEX_WEIGHT_CPOL>(rc, co + s * G * 16);
+        r.scales[s] = load_u16<APEX_WEIGHT_CPOL>(rs, so + s * G * 2);
     }
+    r.codes[SLOTS - 1] = load_b128<APEX_WEIGHT_CPOL>(rc, co + last_c);
+    r.scales[SLOTS - 1] = load_u16<APEX_WEIGHT_CPOL>(rs, so + last_s);
 }
 
-// Accumulate one chunk (32 weights in `cw`, scale bytes in `sc`) against token tt's x.
-__device__ __forceinline__ float chunk_dot(const u32x4_t &cw, uint32_t sc, const uint4 *xl,
-                                           int nchunks, int c, uint16_t) {
-    const uint32_t words[4] = {cw[0], cw[1], cw[2], cw[3]};
-    float acc = 0.0f;
+// x pieces of one chunk for one token: 16-byte piece p holds elements [8p, 8p+8)
+// (bf16) or [4p, 4p+4) (fp32) of the chunk.
+template <typename XT> struct XChunk {
+    u32x4_t p[XTraits<XT>::kPieces];
+};
+
+template <typename XT>
+__device__ __forceinline__ XChunk<XT> lds_chunk(const uint4 *xl, int nchunks, int c) {
+    XChunk<XT> x;
+#pragma unroll
+    for (int p = 0; p < XTraits<XT>::kPieces; ++p)
+        x.p[p] = __builtin_bit_cast(u32x4_t, xl[p * nchunks + c]);
+    return x;
+}
+
+// The two E4M3 scales of a chunk (bytes 0 and 1 of `sc`).  The packed hardware
+// conversion is exact for every code except 0x7F/0xFF, which it maps to NaN where the
+// reference decodes +-480; a row that meets one comes out NaN and is recomputed with
+// the exact integer decode (see compute_row_set).
+template <bool EXACT>
+__device__ __forceinline__ f32x2_t chunk_scales(uint32_t sc) {
+    if constexpr (EXACT)
+        return f32x2_t{e4m3_to_f32(sc), e4m3_to_f32(sc >> 8)};
+    else
+        return __builtin_amdgcn_cvt_pk_f32_fp8((int)sc, false);
+}
+
+// One chunk (32 weights in `cw`, block scales `s`) dotted with x into acc: per
+// 16-element block an unscaled fp32 partial, then acc += scale * partial
+// (shaders/matmul.metal:38-46 order).
+__device__ __forceinline__ void chunk_dot(const u32x4_t &cw, f32x2_t s,
+                                          const XChunk<uint16_t> &x, float &acc) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         float partial = 0.0f;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int p = 2 * b + h;
-            const uint4 xv = xl[p * nchunks + c];
             bf16x2_t w[4];
-            e2m1x8_to_bf16(words[p], w);
-            const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+            e2m1x8_to_bf16(cw[p], w);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                partial = __builtin_amdgcn_fdot2_f32_bf16(w[j], __builtin_bit_cast(bf16x2_t, xs[j]),
+            for (int j = 0; j < 4; ++j) {
+                // Copy the lane out of the vector first: __builtin_bit_cast applied
+                // directly to an ext-vector element reads element 0 (clang 22).
+                const uint32_t xw = x.p[p][j];
+                partial = __builtin_amdgcn_fdot2_f32_bf16(w[j], __builtin_bit_cast(bf16x2_t, xw),
                                                           partial, false);
+            }
         }
-        acc = __builtin_fmaf(e4m3_to_f32(sc >> (8 * b)), partial, acc);
+        acc = __builtin_fmaf(s[b], partial, acc);
     }
-    return acc;
 }
 
-__device__ __forceinline__ float chunk_dot(const u32x4_t &cw, uint32_t sc, const uint4 *xl,
-                                           int nchunks, int c, float) {
-    const uint32_t words[4] = {cw[0], cw[1], cw[2], cw[3]};
-    float acc = 0.0f;
+__device__ __forceinline__ void chunk_dot(const u32x4_t &cw, f32x2_t s, const XChunk<float> &x,
+                                          float &acc) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         float partial = 0.0f;
@@ -102,30 +132,104 @@ __device__ __forceinline__ float chunk_dot(const u32x4_t &cw, uint32_t sc, const
         for (int h = 0; h < 2; ++h) {
             const int wi = 2 * b + h;
             f32x2_t w[4];
-            e2m1x8_to_f32(words[wi], w);
-            const uint4 x0 = xl[(2 * wi) * nchunks + c];
-            const uint4 x1 = xl[(2 * wi + 1) * nchunks + c];
-            const float xs[8] = {__uint_as_float(x0.x), __uint_as_float(x0.y),
-                                 __uint_as_float(x0.z), __uint_as_float(x0.w),
-                                 __uint_as_float(x1.x), __uint_as_float(x1.y),
-                                 __uint_as_float(x1.z), __uint_as_float(x1.w)};
+            e2m1x8_to_f32(cw[wi], w);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                partial = __builtin_fmaf(w[j][0], xs[2 * j], partial);
-                partial = __builtin_fmaf(w[j][1], xs[2 * j + 1], partial);
+                const u32x4_t &xp = x.p[2 * wi + j / 2];
+                partial = __builtin_fmaf(w[j][0], __uint_as_float(xp[(2 * j) % 4]), partial);
+                partial = __builtin_fmaf(w[j][1], __uint_as_float(xp[(2 * j) % 4 + 1]), partial);
             }
         }
-        acc = __builtin_fmaf(e4m3_to_f32(sc >> (8 * b)), partial, acc);
+        acc = __builtin_fmaf(s[b], partial, acc);
     }
-    return acc;
+}
+
+// Accumulate all chunks of the row set whose loads are in `r`, then sum over the
+// group.  Lanes past the end of a row hold zero codes and scales and read a zero x
+// chunk, so they add exactly 0.
+template <bool EXACT, typename XT, int G, int SLOTS, int TT, int NMAT, bool XREG>
+__device__ __forceinline__ void row_set_sums(float (&acc)[NMAT][TT], const RowRegs<SLOTS> (&r)[NMAT],
+                                             const XChunk<XT> (&xr)[SLOTS], const uint4 *lds_x,
+                                             int plane, int nchunks, int gl) {
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+            acc[m][tt] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int c = gl + s * G;
+        const int cx = c < nchunks ? c : nchunks; // entry nchunks of each LDS plane is zero
+        f32x2_t sc[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+            sc[m] = chunk_scales<EXACT>(r[m].scales[s]);
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+            XChunk<XT> x;
+            if constexpr (XREG)
+                x = xr[s];
+            else
+                x = lds_chunk<XT>(lds_x + tt * plane, nchunks + 1, cx);
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+                chunk_dot(r[m].codes[s], sc[m], x, acc[m][tt]);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+            acc[m][tt] = group_sum<G>(acc[m][tt]);
+}
+
+// Row sums (reduced over the group, one per token) of the row set whose loads are in
+// `r`, for one matrix.  A NaN sum means a 0x7F/0xFF scale (or a NaN in x) was met:
+// the row set is then recomputed with the exact decode.
+template <typename XT, int G, int SLOTS, int TT>
+__device__ __forceinline__ void row_set_result(float (&acc)[1][TT], const RowRegs<SLOTS> (&r)[1],
+                                               const uint4 *lds_x, int plane, int nchunks,
+                                               int gl) {
+    const XChunk<XT> no_xr[SLOTS] = {};
+    row_set_sums<false, XT, G, SLOTS, TT, 1, false>(acc, r, no_xr, lds_x, plane, nchunks, gl);
+    bool nan = false;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+        nan |= __builtin_isnan(acc[0][tt]);
+    if (nan)
+        row_set_sums<true, XT, G, SLOTS, TT, 1, false>(acc, r, no_xr, lds_x, plane, nchunks, gl);
+}
+
+// Output element of a plain GEMV (MODE 0: fp32, MODE 1: bf16).
+template <int MODE>
+__device__ __forceinline__ void store_plain(const GemvArgs &a, size_t o, float v) {
+    if constexpr (MODE == 0)
+        static_cast<float *>(a.out)[o] = v * a.tensor_scale[0];
+    else
+        static_cast<uint16_t *>(a.out)[o] = f32_to_bf16_bits(v * a.tensor_scale[0]);
 }
 
 // MODE: 0 plain fp32 out, 1 plain bf16 out, 2 GeGLU bf16 out, 3 GeGLU fp32 out.
-template <typename XT, int MODE, int G, int SLOTS, int TT>
+//
+// Work units are row sets (R = 64/G rows).  Wave w of workgroup b owns the sets
+// b*4 + w + j*step (j < kmax, step = 4*grid) and walks them in NM passes, one per
+// matrix -- for GeGLU all its gate row sets, then the same up row sets -- so at any
+// moment the whole GPU streams one window of one matrix, the pattern that measured
+// fastest (streaming gate and up side by side was ~20% slower).  Plain GEMVs store
+// each row's result at once; GeGLU parks the reduced sums in LDS, and after one
+// barrier the workgroup applies gelu_tanh(gate) * up (shaders/geglu.metal:15-23).
+//
+// x is staged per block of TT tokens in LDS, piece-major.  The staging loads are
+// issued first, then the first DEPTH-1 row sets' weight loads, and only then does the
+// wave wait -- for the x loads alone -- write LDS and meet the barrier, so the weight
+// latency overlaps the staging.
+template <typename XT, int MODE, int G, int SLOTS, int TT, int DEPTH>
 __global__ __launch_bounds__(kThreads) void nvfp4_gemv_kernel(GemvArgs a) {
-    constexpr int NMAT = (MODE >= 2) ? 2 : 1;
+    constexpr int NM = (MODE >= 2) ? 2 : 1; // matrices
     constexpr int R = 64 / G;
     constexpr int PIECES = XTraits<XT>::kPieces;
+    // entries per token plane <= PIECES * (SLOTS*G + 1); staging loads per thread:
+    constexpr int NX = (TT * PIECES * (SLOTS * G + 1) + kThreads - 1) / kThreads;
     extern __shared__ uint4 lds_x[];
 
     const int nchunks = (int)(a.K / 32);
@@ -134,98 +238,141 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemv_kernel(GemvArgs a) {
     const int sub = lane / G;
     const int gl = lane % G;
     const uint32_t nsets = (a.rows + R - 1) / R;
-    const uint32_t wave_stride = gridDim.x * kWaves;
-    const uint32_t first_set = blockIdx.x * kWaves + wave;
-    const int plane = PIECES * nchunks; // uint4 entries per token in LDS
+    const int stride_c = nchunks + 1;    // LDS entries per piece plane
+    const int plane = PIECES * stride_c; // LDS entries per token
+    const uint32_t kmax = a.sets_per_wave;
+    const uint32_t total_k = NM * kmax;  // iterations of every wave
+    // GeGLU sums after the x planes: [NM][TT][4 * kmax * R] floats
+    float *res = reinterpret_cast<float *>(lds_x + TT * plane);
+    const uint32_t res_per = kWaves * kmax * R;
 
+    __amdgpu_buffer_rsrc_t rc[NM], rs[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        rc[m] = make_rsrc(a.codes[m], a.rows * (a.K / 2));
+        rs[m] = make_rsrc(a.scales[m], a.rows * (a.K / 16));
+    }
+
+    const uint32_t base = blockIdx.x * kWaves + wave;
+    const uint32_t step = gridDim.x * kWaves;
+    // A row at or past a.rows lies outside the buffer descriptors: its loads read zeros
+    // without touching memory.  Prefetches past the end use it.
+    const uint32_t oob_row = a.rows + sub;
+    // Offsets of the last slot: out of range (>= 2^31 > any descriptor size) for
+    // lanes whose last chunk lies past the end of the row.
+    const bool last_ok = gl + (SLOTS - 1) * G < nchunks;
+    const uint32_t last_c = last_ok ? (SLOTS - 1) * G * 16 : 0x80000000u;
+    const uint32_t last_s = last_ok ? (SLOTS - 1) * G * 2 : 0x80000000u;
+
+    // Loads of iteration k (matrix k / kmax, set base + (k % kmax) * step) into `r`.
+    auto issue = [&](RowRegs<SLOTS> &r, uint32_t k) {
+        const uint32_t m = (NM == 2 && k >= kmax) ? 1u : 0u;
+        const uint32_t set = base + (k - m * kmax) * step;
+        const uint32_t row = (k < total_k && set < nsets) ? set * R + sub : oob_row;
+        load_row<SLOTS, G>(r, rc[NM == 2 ? m : 0], rs[NM == 2 ? m : 0], row, gl, a.K, last_c,
+                           last_s);
+    };
+
+    RowRegs<SLOTS> buf[DEPTH][1];
     for (uint32_t t0 = 0; t0 < a.tokens; t0 += TT) {
-        // Stage x[t0 .. t0+TT) piece-major: entry (tt*PIECES + p)*nchunks + c holds
-        // bytes [16p, 16p+16) of chunk c of token t0+tt.
-        __syncthreads();
-        const int total = TT * plane;
-        for (int q = threadIdx.x; q < total; q += kThreads) {
+        // 1. staging loads of x[t0 .. t0+TT): thread-linear entry q = tt*plane +
+        //    c*PIECES + p (natural order); the zero chunk c = nchunks and tokens past
+        //    the end fall outside the descriptor and read zeros.
+        const uint32_t ntok = min((uint32_t)TT, a.tokens - t0);
+        const __amdgpu_buffer_rsrc_t rx =
+            make_rsrc(static_cast<const XT *>(a.x) + (size_t)t0 * a.K,
+                      ntok * a.K * (uint32_t)sizeof(XT));
+        u32x4_t xv[NX];
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const int q = threadIdx.x + i * kThreads;
             const int tt = q / plane;
             const int rem = q - tt * plane;
             const int c = rem / PIECES;
             const int p = rem - c * PIECES;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (t0 + tt < a.tokens)
-                v = reinterpret_cast<const uint4 *>(static_cast<const XT *>(a.x) +
-                                                    (size_t)(t0 + tt) * a.K)[rem];
-            lds_x[(tt * PIECES + p) * nchunks + c] = v;
+            const uint32_t off = (c < nchunks && tt < TT)
+                                     ? ((uint32_t)tt * a.K * (uint32_t)sizeof(XT) +
+                                        (uint32_t)(c * PIECES + p) * 16)
+                                     : 0x80000000u;
+            xv[i] = load_b128(rx, off);
+        }
+        // 2. first iterations' weights
+        __syncthreads(); // readers of the previous token block are done with LDS
+#pragma unroll
+        for (int i = 0; i < DEPTH - 1; ++i)
+            issue(buf[i][0], i);
+        // 3. x into LDS, piece-major: entry tt*plane + p*stride_c + c
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const int q = threadIdx.x + i * kThreads;
+            if (q < TT * plane) {
+                const int tt = q / plane;
+                const int rem = q - tt * plane;
+                const int c = rem / PIECES;
+                const int p = rem - c * PIECES;
+                lds_x[tt * plane + p * stride_c + c] = __builtin_bit_cast(uint4, xv[i]);
+            }
         }
         __syncthreads();
 
-        RowRegs<SLOTS> cur[NMAT], nxt[NMAT];
-        uint32_t set = first_set;
-        if (set < nsets) {
-            const uint32_t row = set * R + sub;
+        // DEPTH-stage pipeline over rotating register sets: while iteration k is
+        // computed, the loads of k+1 .. k+DEPTH-1 are in flight.  The body is unrolled
+        // DEPTH times so every buffer index is a constant and the compiler can count
+        // outstanding loads exactly.
+        for (uint32_t k0 = 0;; k0 += DEPTH) {
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-                load_row<SLOTS, G>(cur[m], a.codes[m], a.scales[m], row, row < a.rows, gl,
-                                   nchunks, a.K);
+            for (int i = 0; i < DEPTH; ++i) {
+                const uint32_t k = k0 + i;
+                if (k >= total_k)
+                    goto epilogue;
+                issue(buf[(i + DEPTH - 1) % DEPTH][0], k + DEPTH - 1);
+                const uint32_t m = (NM == 2 && k >= kmax) ? 1u : 0u;
+                const uint32_t j = k - m * kmax;
+                const uint32_t set = base + j * step;
+                if (set >= nsets)
+                    continue;
+                float acc[1][TT];
+                row_set_result<XT, G, SLOTS, TT>(acc, buf[i], lds_x, plane, nchunks, gl);
+                if (gl != 0)
+                    continue;
+                const uint32_t row = set * R + sub;
+                if constexpr (NM == 1) {
+                    if (row < a.rows) {
+#pragma unroll
+                        for (int tt = 0; tt < TT; ++tt)
+                            if (t0 + tt < a.tokens)
+                                store_plain<MODE>(a, (size_t)(t0 + tt) * a.out_stride + row,
+                                                  acc[0][tt]);
+                    }
+                } else {
+                    const uint32_t slot = (wave + j * kWaves) * R + sub;
+#pragma unroll
+                    for (int tt = 0; tt < TT; ++tt)
+                        res[(m * TT + tt) * res_per + slot] = acc[0][tt] * a.tensor_scale[m];
+                }
+            }
         }
-        for (; set < nsets; set += wave_stride) {
-            const uint32_t row = set * R + sub;
-            const uint32_t next = set + wave_stride;
-            if (next < nsets) {
-                const uint32_t nrow = next * R + sub;
-#pragma unroll
-                for (int m = 0; m < NMAT; ++m)
-                    load_row<SLOTS, G>(nxt[m], a.codes[m], a.scales[m], nrow, nrow < a.rows,
-                                       gl, nchunks, a.K);
+    epilogue:
+        if constexpr (NM == 2) {
+            // gelu(gate) * up for every row this workgroup owns
+            __syncthreads();
+            for (uint32_t q = threadIdx.x; q < TT * res_per; q += kThreads) {
+                const uint32_t tt = q / res_per;
+                const uint32_t slot = q - tt * res_per;
+                const uint32_t jj = slot / (kWaves * R);
+                const uint32_t w = (slot / R) % kWaves;
+                const uint32_t row = (blockIdx.x * kWaves + w + jj * step) * R + slot % R;
+                if (row >= a.rows || t0 + tt >= a.tokens)
+                    continue;
+                const float g = res[tt * res_per + slot];
+                const float u = res[(TT + tt) * res_per + slot];
+                const float h = gelu_tanh(g) * u;
+                const size_t o = (size_t)(t0 + tt) * a.out_stride + row;
+                if constexpr (MODE == 2)
+                    static_cast<uint16_t *>(a.out)[o] = f32_to_bf16_bits(h);
+                else
+                    static_cast<float *>(a.out)[o] = h;
             }
-            float acc[NMAT][TT];
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-                for (int tt = 0; tt < TT; ++tt)
-                    acc[m][tt] = 0.0f;
-#pragma unroll
-            for (int s = 0; s < SLOTS; ++s) {
-                const int c = gl + s * G;
-                if (c < nchunks) {
-#pragma unroll
-                    for (int tt = 0; tt < TT; ++tt) {
-                        const uint4 *xl = lds_x + tt * plane;
-#pragma unroll
-                        for (int m = 0; m < NMAT; ++m)
-                            acc[m][tt] += chunk_dot(cur[m].codes[s], cur[m].scales[s], xl,
-                                                    nchunks, c, XT());
-                    }
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-                for (int tt = 0; tt < TT; ++tt)
-                    acc[m][tt] = group_sum<G>(acc[m][tt]);
-            if (gl == 0 && row < a.rows) {
-#pragma unroll
-                for (int tt = 0; tt < TT; ++tt) {
-                    const uint32_t t = t0 + tt;
-                    if (t >= a.tokens)
-                        break;
-                    const size_t o = (size_t)t * a.out_stride + row;
-                    if constexpr (MODE == 0) {
-                        static_cast<float *>(a.out)[o] = acc[0][tt] * a.tensor_scale[0];
-                    } else if constexpr (MODE == 1) {
-                        static_cast<uint16_t *>(a.out)[o] =
-                            f32_to_bf16_bits(acc[0][tt] * a.tensor_scale[0]);
-                    } else {
-                        const float g = acc[0][tt] * a.tensor_scale[0];
-                        const float u = acc[1][tt] * a.tensor_scale[1];
-                        const float h = gelu_tanh(g) * u;
-                        if constexpr (MODE == 2)
-                            static_cast<uint16_t *>(a.out)[o] = f32_to_bf16_bits(h);
-                        else
-                            static_cast<float *>(a.out)[o] = h;
-                    }
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-                cur[m] = nxt[m];
         }
     }
 }
@@ -313,18 +460,31 @@ inline Shape pick_shape(int nchunks) {
 }
 
 template <typename XT, int MODE, int G, int SLOTS, int TT>
-hipError_t launch_fast(const GemvArgs &a, int nchunks, hipStream_t stream) {
+hipError_t launch_fast(const GemvArgs &args, int nchunks, hipStream_t stream) {
     constexpr int R = 64 / G;
-    const uint32_t nsets = (a.rows + R - 1) / R;
-    // Balanced persistent grid: about kTargetWaves waves, each with the same count of
-    // row sets (the last wave may have fewer).
+    constexpr int NM = (MODE >= 2) ? 2 : 1;
+    const uint32_t nsets = (args.rows + R - 1) / R;
+    // Persistent grid of about kTargetWavesPerCU waves per CU; every wave gets the
+    // same count of row sets per matrix (the last ones may get one fewer).
     const uint32_t target = (uint32_t)kTargetWavesPerCU * (uint32_t)kNumCUs;
     const uint32_t per_wave = (nsets + target - 1) / target;
     const uint32_t waves = (nsets + per_wave - 1) / per_wave;
     const uint32_t grid = (waves + kWaves - 1) / kWaves;
-    const size_t lds = (size_t)TT * XTraits<XT>::kPieces * nchunks * 16;
-    hipLaunchKernelGGL((nvfp4_gemv_kernel<XT, MODE, G, SLOTS, TT>), dim3(grid), dim3(kThreads),
-                       lds, stream, a);
+    const uint32_t kmax = (nsets + grid * kWaves - 1) / (grid * kWaves);
+    size_t lds = (size_t)TT * XTraits<XT>::kPieces * (nchunks + 1) * 16;
+    if (NM == 2)
+        lds += (size_t)NM * TT * kWaves * kmax * R * sizeof(float);
+    if (lds > 65536)
+        return hipErrorInvalidValue;
+    GemvArgs a = args;
+    a.sets_per_wave = kmax;
+    a.mapping = 0;
+    if (kGemvDepth >= 3)
+        hipLaunchKernelGGL((nvfp4_gemv_kernel<XT, MODE, G, SLOTS, TT, 3>), dim3(grid),
+                           dim3(kThreads), lds, stream, a);
+    else
+        hipLaunchKernelGGL((nvfp4_gemv_kernel<XT, MODE, G, SLOTS, TT, 2>), dim3(grid),
+                           dim3(kThreads), lds, stream, a);
     return hipGetLastError();
 }
 
@@ -345,7 +505,8 @@ hipError_t dispatch_shape(const GemvArgs &a, int nchunks, hipStream_t stream) {
 template <typename XT, int MODE>
 hipError_t gemv_dispatch(const GemvArgs &a, hipStream_t stream) {
     const int nchunks = (int)(a.K / 32);
-    bool fast = (a.K % 32 == 0) && nchunks <= 4 * 64;
+    // buffer descriptors address at most 2^31 bytes per matrix
+    bool fast = (a.K % 32 == 0) && nchunks <= 4 * 64 && (uint64_t)a.rows * (a.K / 2) < (1ull << 31);
     for (int m = 0; m < ((MODE >= 2) ? 2 : 1); ++m)
         fast = fast && ((uintptr_t)a.codes[m] % 16 == 0) && ((uintptr_t)a.scales[m] % 2 == 0);
     fast = fast && ((uintptr_t)a.x % 16 == 0);

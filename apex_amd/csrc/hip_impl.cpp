@@ -683,6 +683,17 @@ int apex_hip_event_elapsed_ms(void *start, void *stop, float *ms) {
     });
 }
 
+int apex_hip_read_probe(const void *ptr, size_t bytes, uint32_t *sink, void *stream) {
+    return guard([&] {
+        require(ptr && sink, "null pointer");
+        require(bytes >= 16 && bytes < (1ull << 31), "bytes must be in [16, 2 GiB)");
+        init_device_tuning();
+        hip_check(apex_hip::read_probe_launch(ptr, bytes, sink, as_stream(stream)), "read probe");
+    });
+}
+
+int apex_hip_read_probe_sink_words(void) { return 8 * apex_hip::kNumCUs; }
+
 int apex_hip_set_gemv_waves_per_cu(int waves) {
     return guard([&] {
         require(waves >= 1 && waves <= 32, "waves per CU must be in [1, 32]");

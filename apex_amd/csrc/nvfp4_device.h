@@ -26,6 +26,29 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Buffer resource over [base, base + bytes): raw buffer loads through it are range
+// checked by the hardware -- a lane whose offset falls outside returns 0 and never
+// faults -- so tails need no branches.  Word 3 is the gfx9 default descriptor format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// Cache-policy bits of the weight-stream loads (the buffer instruction's aux field).
+#ifndef APEX_WEIGHT_CPOL
+#define APEX_WEIGHT_CPOL 2 // nt: the weights are streamed once
+#endif
+
+template <int CPOL = 0>
+__device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CPOL));
+}
+
+template <int CPOL = 0>
+__device__ __forceinline__ uint32_t load_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, CPOL);
+}
+
 // E4M3 byte (in the low 8 bits of `b`) -> fp32, reference semantics.
 // Magnitude bits 0eeeemmm placed at float bits 20..26 give 2^(e-127) * (1 + m/8) for
 // e > 0 and the fp32 denormal m * 2^-129 for e == 0; multiplying by 2^120 (exact)

@@ -91,6 +91,8 @@ _PROTOS = {
     "apex_hip_event_record": (_I, [_P, _P]),
     "apex_hip_event_synchronize": (_I, [_P]),
     "apex_hip_event_elapsed_ms": (_I, [_P, _P, C.POINTER(_F)]),
+    "apex_hip_read_probe": (_I, [_P, _SZ, _P, _P]),
+    "apex_hip_read_probe_sink_words": (_I, []),
     "apex_hip_set_gemv_waves_per_cu": (_I, [_I]),
 }
 
@@ -252,6 +254,14 @@ def geglu_f32(gate, up, out, count, stream=None):
 def nvfp4_dequant(codes, scales, out, rows, K, tensor_scale=1.0, stream=None):
     f = lib().apex_nvfp4_dequant_bf16 if out.dtype == np.uint16 else lib().apex_nvfp4_dequant_f32
     check(f(codes.ptr, scales.ptr, tensor_scale, out.ptr, rows, K, _s(stream)))
+
+
+def read_probe(buf, sink, stream=None) -> None:
+    check(lib().apex_hip_read_probe(buf.ptr, buf.nbytes, sink.ptr, _s(stream)))
+
+
+def read_probe_sink_words() -> int:
+    return lib().apex_hip_read_probe_sink_words()
 
 
 def set_gemv_waves_per_cu(waves: int) -> None:

@@ -202,7 +202,13 @@ int apex_hip_event_record(void *event, void *stream);
 int apex_hip_event_synchronize(void *event);
 int apex_hip_event_elapsed_ms(void *start, void *stop, float *ms);
 
-/* Launch tuning of the GEMV kernels: target resident waves per CU (default 8). */
+/* Streaming-read probe: reads [ptr, ptr+bytes) once with 16-byte buffer loads
+ * (bytes < 2 GiB); `sink` must hold apex_hip_read_probe_sink_words() words.  Used by
+ * the benchmark to measure the achievable HBM read rate beside the spec peak. */
+int apex_hip_read_probe(const void *ptr, size_t bytes, uint32_t *sink, void *stream);
+int apex_hip_read_probe_sink_words(void);
+
+/* Launch tuning of the GEMV kernels: target resident waves per CU (default 12). */
 int apex_hip_set_gemv_waves_per_cu(int waves);
 
 #ifdef __cplusplus

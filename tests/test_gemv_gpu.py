@@ -142,3 +142,45 @@ def test_standalone_geglu_f32_in_place():
     hip.geglu_f32(dg, du, dg, g.size)  # in place, as src/ops.h:67 does
     hip.synchronize()
     assert rel_l2(dg.numpy(), oracle.geglu(g, u)) < 1e-6
+
+
+@pytest.mark.parametrize("bf16_io", [False, True])
+def test_gemv_every_scale_code(bf16_io):
+    """Every row holds every E4M3 scale code, including 0x7F/0xFF (+-480 in the
+    reference, NaN in the hardware fp8 conversion): the kernel's exact fallback must
+    reproduce the reference decode."""
+    w = all_codes_weights(rows_per_code=2)
+    rng = np.random.default_rng(11)
+    x = synth.normal_bf16(rng, (1, w.K))
+    got = run_matmul(x if bf16_io else bf16(x), w, bf16_io=bf16_io)
+    got = bf16(got) if bf16_io else got
+    want = oracle.matvec(w.codes, w.scales, bf16(x))
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) < (TOL_BF16 if bf16_io else TOL_REF_GATE)
+
+
+def test_gemv_some_rows_with_480_scales():
+    """Random weights where a few rows carry 0x7F / 0xFF scales among ordinary ones."""
+    rng = np.random.default_rng(12)
+    w = synth.nvfp4_weights(rng, 300, 5376)
+    for r, col, code in [(3, 0, 0x7F), (77, 335, 0xFF), (150, 100, 0x7F), (299, 7, 0xFF)]:
+        w.scales[r, col] = code
+    x = synth.normal_bf16(rng, (1, w.K))
+    want = oracle.matvec(w.codes, w.scales, bf16(x))
+    got = run_matmul(bf16(x), w, bf16_io=False)
+    assert rel_l2(got, want) < TOL_REF_GATE
+    gotb = bf16(run_matmul(x, w, bf16_io=True))
+    assert rel_l2(gotb, want) < TOL_BF16
+    for r in (3, 77, 150, 299):
+        assert abs(gotb[0, r] - want[0, r]) <= 1e-2 * abs(want[0, r]) + 1e-3
+
+
+def test_fused_geglu_every_scale_code():
+    gate = all_codes_weights()
+    up = synth.Nvfp4Weights(gate.codes[::-1].copy(), gate.scales[:, ::-1].copy())
+    rng = np.random.default_rng(13)
+    x = synth.normal_bf16(rng, (1, gate.K)) * 0 + synth.bf16_from_f32(
+        rng.standard_normal((1, gate.K), dtype=np.float32) * 0.01)
+    want = geglu_oracle(bf16(x), gate, up)
+    got = run_geglu(bf16(x), gate, up, False)
+    assert rel_l2(got, want) < TOL_REF_GATE
