@@ -10,6 +10,7 @@
 #include <stdexcept>
 #include <string>
 
+#include "gemm.h"
 #include "gemv.h"
 
 namespace {
@@ -71,6 +72,23 @@ void check_nvfp4_shape(uint32_t rows, uint32_t K) {
 // Direct-entry implementations (shared by the registry launchers)
 // ------------------------------------------------------------------------------------
 
+// Tokens from which a bf16 product runs as an MFMA GEMM instead of a GEMV: below it
+// the weights dominate the traffic and the GEMV streams them at the HBM rate.
+constexpr uint32_t kGemmMinTokens = 64;
+
+void gemm_impl(const uint16_t *A, const uint32_t *codes, const uint8_t *scales, float ts,
+               uint16_t *C, uint32_t M, uint32_t N, uint32_t K, hipStream_t stream) {
+    check_nvfp4_shape(N, K);
+    if (M == 0 || N == 0)
+        return;
+    require(A && codes && scales && C, "null pointer");
+    require(apex_hip::gemm_supported(M, N, K),
+            "gemm: K must be a multiple of 64 and operands below 2 GiB");
+    init_device_tuning();
+    apex_hip::GemmArgs g{A, codes, scales, C, M, N, K, N, ts};
+    hip_check(apex_hip::gemm_launch(g, stream), "gemm_nvfp4 launch");
+}
+
 void matmul_impl(const void *x, bool bf16, const uint32_t *codes, const uint8_t *scales,
                  float ts, void *out, uint32_t tokens, uint32_t rows, uint32_t K,
                  hipStream_t stream) {
@@ -79,6 +97,11 @@ void matmul_impl(const void *x, bool bf16, const uint32_t *codes, const uint8_t 
         return;
     require(x && codes && scales && out, "null pointer");
     init_device_tuning();
+    if (bf16 && tokens >= kGemmMinTokens && apex_hip::gemm_supported(tokens, rows, K)) {
+        gemm_impl(static_cast<const uint16_t *>(x), codes, scales, ts, static_cast<uint16_t *>(out),
+                  tokens, rows, K, stream);
+        return;
+    }
     apex_hip::GemvArgs a{};
     a.x = x;
     a.codes[0] = a.codes[1] = codes;
@@ -252,6 +275,17 @@ template <bool BF16> void launch_geglu_nvfp4(const LaunchCtx &c) {
                rows, K, c.stream);
 }
 
+void launch_gemm_nvfp4_bf16(const LaunchCtx &c) {
+    const uint32_t M = c.u[4], N = c.u[5], K = c.u[6];
+    check_nvfp4_shape(N, K);
+    need(c, 0, (uint64_t)M * K * 2, "gemm_nvfp4_bf16 A");
+    need(c, 1, (uint64_t)N * K / 2, "gemm_nvfp4_bf16 weights");
+    need(c, 2, (uint64_t)N * K / 16, "gemm_nvfp4_bf16 scales");
+    need(c, 3, (uint64_t)M * N * 2, "gemm_nvfp4_bf16 output");
+    gemm_impl((const uint16_t *)c.ptr[0], (const uint32_t *)c.ptr[1], (const uint8_t *)c.ptr[2],
+              c.f[7], (uint16_t *)c.ptr[3], M, N, K, c.stream);
+}
+
 template <bool BF16> void launch_dequant(const LaunchCtx &c) {
     const uint32_t K = c.u[3], rows = c.u[4];
     check_nvfp4_shape(rows, K);
@@ -269,6 +303,7 @@ const KernelSpec kKernels[] = {
     {"matmul_nvfp4_bf16", "BBBBUUUF", 1u << 3, launch_matmul_nvfp4_bf16},
     {"geglu_nvfp4_f32", "BBBBBBUUUFF", 1u << 5, launch_geglu_nvfp4<false>},
     {"geglu_nvfp4_bf16", "BBBBBBUUUFF", 1u << 5, launch_geglu_nvfp4<true>},
+    {"gemm_nvfp4_bf16", "BBBBUUUF", 1u << 3, launch_gemm_nvfp4_bf16},
     {"dequant_nvfp4_f32", "BBBUUF", 1u << 2, launch_dequant<false>},
     {"dequant_nvfp4_bf16", "BBBUUF", 1u << 2, launch_dequant<true>},
 };
@@ -525,6 +560,12 @@ int apex_nvfp4_matmul_bf16(const uint16_t *x, const uint32_t *codes, const uint8
     return guard([&] {
         matmul_impl(x, true, codes, scales, tensor_scale, out, tokens, rows, K, as_stream(stream));
     });
+}
+
+int apex_nvfp4_gemm_bf16(const uint16_t *A, const uint32_t *codes, const uint8_t *scales,
+                         float tensor_scale, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
+                         void *stream) {
+    return guard([&] { gemm_impl(A, codes, scales, tensor_scale, C, M, N, K, as_stream(stream)); });
 }
 
 int apex_nvfp4_geglu_f32(const float *x, const uint32_t *gate_codes, const uint8_t *gate_scales,

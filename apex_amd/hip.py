@@ -69,6 +69,7 @@ _PROTOS = {
     "apex_hip_validate_run": (_I, [C.c_char_p, C.POINTER(Arg), _SZ, Dim3, Dim3]),
     "apex_nvfp4_matmul_f32": (_I, [_P, _P, _P, _F, _P, _U32, _U32, _U32, _P]),
     "apex_nvfp4_matmul_bf16": (_I, [_P, _P, _P, _F, _P, _U32, _U32, _U32, _P]),
+    "apex_nvfp4_gemm_bf16": (_I, [_P, _P, _P, _F, _P, _U32, _U32, _U32, _P]),
     "apex_nvfp4_geglu_f32": (_I, [_P, _P, _P, _F, _P, _P, _F, _P, _U32, _U32, _U32, _P]),
     "apex_nvfp4_geglu_bf16": (_I, [_P, _P, _P, _F, _P, _P, _F, _P, _U32, _U32, _U32, _P]),
     "apex_geglu_f32": (_I, [_P, _P, _P, _U32, _P]),
@@ -233,6 +234,11 @@ def nvfp4_matmul_f32(x, codes, scales, out, tokens, rows, K, tensor_scale=1.0, s
 def nvfp4_matmul_bf16(x, codes, scales, out, tokens, rows, K, tensor_scale=1.0, stream=None):
     check(lib().apex_nvfp4_matmul_bf16(x.ptr, codes.ptr, scales.ptr, tensor_scale, out.ptr,
                                        tokens, rows, K, _s(stream)))
+
+
+def nvfp4_gemm_bf16(A, codes, scales, C, M, N, K, tensor_scale=1.0, stream=None):
+    check(lib().apex_nvfp4_gemm_bf16(A.ptr, codes.ptr, scales.ptr, tensor_scale, C.ptr, M, N, K,
+                                     _s(stream)))
 
 
 def nvfp4_geglu_f32(x, gc, gs, uc, us, out, tokens, rows, K, gate_scale=1.0, up_scale=1.0,

@@ -117,6 +117,8 @@ int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
  *   geglu_nvfp4_bf16  B up scales, B output [T,rows], U hidden_dim, U w_rows,
  *                     U tokens, F gate tensor_scale, F up tensor_scale:
  *                     gelu_tanh(gate.x) * (up.x) in one pass (src/ops.h:65-67 fused).
+ *   gemm_nvfp4_bf16   B A bf16 [M,K], B weights [N,K/8], B scales [N,K/16], B C bf16
+ *                     [M,N], U M, U N, U K, F tensor_scale (apex_nvfp4_gemm_bf16).
  *   dequant_nvfp4_f32 B weights, B scales, B output [rows,K], U hidden_dim,
  *   dequant_nvfp4_bf16 U w_rows, F tensor_scale (src/nvfp4.h:27-43 on the device).
  * For the kernels after geglu_f32 the launch shape is chosen by the backend; the
@@ -155,10 +157,19 @@ int apex_nvfp4_matmul_f32(const float *x, const uint32_t *codes, const uint8_t *
                           float tensor_scale, float *out, uint32_t tokens, uint32_t rows,
                           uint32_t K, void *stream);
 
-/* Same product with bf16 activations and bf16 outputs (fp32 accumulation). */
+/* Same product with bf16 activations and bf16 outputs (fp32 accumulation): a GEMV
+ * for few tokens, the MFMA GEMM below from 64 tokens (when K % 64 == 0). */
 int apex_nvfp4_matmul_bf16(const uint16_t *x, const uint32_t *codes, const uint8_t *scales,
                            float tensor_scale, uint16_t *out, uint32_t tokens, uint32_t rows,
                            uint32_t K, void *stream);
+
+/* Prefill GEMM (no reference counterpart: the reference runs prefill as one GEMV per
+ * token, src/ops.h:44): C[M, N] = tensor_scale * A[M, K] . W[N, K]^T with A, C bf16
+ * row-major (C row stride N), W NVFP4, bf16 MFMA on W dequantised exactly to bf16.
+ * Requires K % 64 == 0. */
+int apex_nvfp4_gemm_bf16(const uint16_t *A, const uint32_t *codes, const uint8_t *scales,
+                         float tensor_scale, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
+                         void *stream);
 
 /* src/ops.h:65-67 fused: out[t, r] = gelu_tanh(Wg[r].x_t) * (Wu[r].x_t). */
 int apex_nvfp4_geglu_f32(const float *x, const uint32_t *gate_codes, const uint8_t *gate_scales,
