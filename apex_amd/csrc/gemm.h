@@ -17,6 +17,7 @@ struct GemmArgs {
 
 // K % 64 == 0 and operands within the 2 GiB buffer-descriptor range.
 bool gemm_supported(uint32_t M, uint32_t N, uint32_t K);
+
 hipError_t gemm_launch(const GemmArgs &a, hipStream_t stream);
 
 } // namespace apex_hip
