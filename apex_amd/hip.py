@@ -128,6 +128,10 @@ def device_count() -> int:
     return n.value
 
 
+def set_device(device: int) -> None:
+    check(lib().apex_hip_set_device(device))
+
+
 # ---------------------------------------------------------------------------------
 # Device memory and timing plumbing
 # ---------------------------------------------------------------------------------

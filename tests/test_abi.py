@@ -1,0 +1,167 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/apex_hip.h
+declares, and its kernel registry rejects malformed runs (src/backend/metal_backend.cpp
+error behaviour) before anything touches a GPU."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from apex_amd import hip
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "apex_hip.h"
+
+E_OK, E_INVALID, E_UNKNOWN_KERNEL, E_ARGS = 0, 1, 2, 3
+E_THREADGROUP = 7
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w \*]*?\b(apex_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def header_constant(name):
+    m = re.search(rf"(?:#define\s+{name}\s+|\b{name}\s*=\s*)(-?\d+)", HEADER.read_text())
+    return int(m.group(1))
+
+
+def test_library_exports_every_declared_function():
+    lib = C.CDLL(str(hip.LIB_PATH))
+    names = header_functions()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the Python binding declares a prototype for each of them
+    assert sorted(hip.exported_symbols()) == names
+
+
+def test_error_codes_match_header():
+    assert header_constant("APEX_HIP_OK") == E_OK
+    assert header_constant("APEX_HIP_E_INVALID") == E_INVALID
+    assert header_constant("APEX_HIP_E_UNKNOWN_KERNEL") == E_UNKNOWN_KERNEL
+    assert header_constant("APEX_HIP_E_ARGS") == E_ARGS
+    assert header_constant("APEX_HIP_E_THREADGROUP") == E_THREADGROUP
+
+
+def test_abi_version():
+    assert hip.lib().apex_hip_abi_version() == header_constant("APEX_HIP_ABI_VERSION")
+
+
+EXPECTED = {
+    "matmul_nvfp4": "BBBBUU",
+    "geglu_f32": "BBBU",
+    "matmul_nvfp4_bf16": "BBBBUUUF",
+    "geglu_nvfp4_f32": "BBBBBBUUUFF",
+    "geglu_nvfp4_bf16": "BBBBBBUUUFF",
+    "gemm_nvfp4_bf16": "BBBBUUUF",
+    "dequant_nvfp4_f32": "BBBUUF",
+    "dequant_nvfp4_bf16": "BBBUUF",
+}
+
+
+def test_registry_names_and_signatures():
+    names = hip.kernel_names()
+    for k, sig in EXPECTED.items():
+        assert k in names
+        assert hip.kernel_signature(k) == sig
+    assert hip.kernel_signature("no_such_kernel") is None
+    # every registered name is documented in the header
+    text = HEADER.read_text()
+    for k in names:
+        assert f"`{k}`" in text or f" {k} " in text or f"{k}:" in text or k in text
+
+
+class FakeBuffer:
+    """validate_run never dereferences a buffer handle: any non-null value works."""
+    handle = 0x1000
+
+
+def buf(off=0):
+    return ("buf", FakeBuffer(), off)
+
+
+def u32(v):
+    return ("val", C.c_uint32(v))
+
+
+def f32(v):
+    return ("val", C.c_float(v))
+
+
+def matmul_args():
+    return [buf(), buf(), buf(), buf(), u32(2048), u32(2048)]
+
+
+def rc_of(fn):
+    try:
+        fn()
+        return E_OK
+    except hip.ApexHipError as e:
+        return e.code
+
+
+def test_validate_accepts_the_reference_launch():
+    # src/ops.h:36-45: grid {ceil(rows/8), tokens}, 256 threads
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", matmul_args(), (256, 1), (256,))) == 0
+    assert rc_of(lambda: hip.validate_run("geglu_f32", [buf(), buf(), buf(), u32(10)],
+                                          (1,), (256,))) == 0
+
+
+def test_validate_unknown_kernel():
+    rc = rc_of(lambda: hip.validate_run("rms_norm_f32", matmul_args()))
+    assert rc == E_UNKNOWN_KERNEL
+    assert "rms_norm_f32" in hip.lib().apex_hip_last_error().decode()
+
+
+def test_validate_wrong_arg_count():
+    rc = rc_of(lambda: hip.validate_run("matmul_nvfp4", matmul_args()[:5]))
+    assert rc == E_ARGS
+    assert "expected 6" in hip.lib().apex_hip_last_error().decode()
+
+
+def test_validate_wrong_arg_kind():
+    a = matmul_args()
+    a[1] = u32(3)  # a value where a buffer belongs
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", a)) == E_ARGS
+    a = matmul_args()
+    a[4] = buf()  # a buffer where a value belongs
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", a)) == E_ARGS
+    a = matmul_args()
+    a[5] = ("val", C.c_uint64(3))  # an 8-byte value
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", a)) == E_ARGS
+    a = matmul_args()
+    a[0] = ("buf", None, 0)  # a null buffer
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", a)) == E_ARGS
+
+
+def test_validate_threadgroup_limits():
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", matmul_args(), (1,), (2048,))) == \
+        E_THREADGROUP
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", matmul_args(), (1,), (32, 32, 2))) == \
+        E_THREADGROUP
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", matmul_args(), (0,), (256,))) == \
+        E_INVALID
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4", matmul_args(), (1,), (32, 32))) == 0
+
+
+def test_validate_bf16_signature():
+    a = [buf(), buf(), buf(), buf(), u32(1), u32(64), u32(64), f32(1.0)]
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4_bf16", a)) == 0
+    a[7] = u32(1)  # U and F are both 4-byte values: the kind check is on size only
+    assert rc_of(lambda: hip.validate_run("matmul_nvfp4_bf16", a)) == 0
+
+
+def test_null_out_pointers_are_rejected():
+    L = hip.lib()
+    assert L.apex_hip_backend_create(0, None) != 0
+    assert L.apex_hip_device_count(None) != 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """The product path has no fallback: without the built library every op raises."""
+    monkeypatch.setattr(hip, "LIB_PATH", tmp_path / "libapex_hip.so")
+    monkeypatch.setattr(hip, "_lib", None)
+    with pytest.raises(ImportError):
+        hip.lib()

@@ -1,0 +1,382 @@
+"""CPU checks that pin the oracle (oracle/nvfp4_oracle.c) before it is trusted.
+
+Each function of the oracle is checked against something other than its own formula:
+the reference's own CPU code (golden vectors under tests/golden/, written by
+tests/golden/make_golden.py from the compiled src/nvfp4.h + src/tests/cpu_ref.h, and
+the live compiled library where it was built), closed forms, torch's FP8 decoder,
+brute force on tiny inputs and algebraic invariants.
+"""
+import hashlib
+import json
+import math
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from apex_amd import synth
+from tests.helpers import all_codes_weights
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def load(name):
+    return np.load(GOLDEN / name, allow_pickle=False)
+
+
+def e2m1_closed_form(c: int) -> float:
+    """E2M1: 1 sign, 2 exponent (bias 1), 1 mantissa bit; exponent 0 is subnormal."""
+    e, m = (c >> 1) & 3, c & 1
+    v = m * 0.5 if e == 0 else (1 + m / 2) * 2.0 ** (e - 1)
+    return -v if c & 8 else v
+
+
+def e4m3_closed_form(b: int) -> float:
+    """E4M3 (fn) without NaN: bias 7, exponent 0 subnormal m/512."""
+    e, m = (b >> 3) & 15, b & 7
+    v = m / 512 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)
+    return -v if b & 0x80 else v
+
+
+# ---- a1 / a2: the two decoders ------------------------------------------------------
+
+def test_e2m1_closed_form_and_reference_table():
+    ref = load("nvfp4_tables.npz")["e2m1"]
+    got = np.array([oracle.e2m1(c) for c in range(16)], np.float32)
+    want = np.array([e2m1_closed_form(c) for c in range(16)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert math.copysign(1.0, got[8]) == -1.0 and got[8] == 0.0  # code 8 is -0.0
+    assert list(got[:8]) == [0, 0.5, 1, 1.5, 2, 3, 4, 6]
+
+
+def test_e4m3_closed_form_and_reference_table():
+    ref = load("nvfp4_tables.npz")["e4m3"]
+    got = np.array([oracle.e4m3(b) for b in range(256)], np.float32)
+    want = np.array([e4m3_closed_form(b) for b in range(256)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # known answers of the reference decoder
+    for b, v in [(0x01, 0.001953125), (0x07, 0.013671875), (0x08, 0.015625), (0x38, 1.0),
+                 (0x39, 1.125), (0x7E, 448.0), (0xFE, -448.0), (0x7F, 480.0), (0xFF, -480.0)]:
+        assert got[b] == v
+    assert got[0x80] == 0.0 and math.copysign(1.0, got[0x80]) == -1.0
+
+
+def test_e4m3_matches_torch_except_the_nan_codes():
+    torch = pytest.importorskip("torch")
+    codes = torch.arange(256, dtype=torch.uint8)
+    t = codes.view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    got = np.array([oracle.e4m3(b) for b in range(256)], np.float32)
+    same = np.ones(256, bool)
+    same[[0x7F, 0xFF]] = False
+    assert np.array_equal(t[same].view(np.uint32), got[same].view(np.uint32))
+    assert np.isnan(t[0x7F]) and np.isnan(t[0xFF])  # the reference decodes +-480 instead
+
+
+def test_synth_decoder_matches_oracle():
+    got = synth.e4m3_to_f32(np.arange(256, dtype=np.uint8))
+    want = np.array([oracle.e4m3(b) for b in range(256)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---- a3: row dequantisation --------------------------------------------------------
+
+def test_decode_row_every_pair_is_the_exact_product():
+    w = all_codes_weights()
+    got = oracle.decode(w.codes, w.scales)
+    e2 = np.array([e2m1_closed_form(c) for c in range(16)])
+    e4 = np.array([e4m3_closed_form(b) for b in range(256)])
+    want = (e2[:, None] * e4[None, :]).astype(np.float32)  # float64 product, exact
+    assert np.array_equal(np.repeat(want, 16, axis=1).view(np.uint32), got.view(np.uint32))
+    # every product has <= 6 significant bits: exactly representable in fp32 and bf16
+    assert np.array_equal(synth.bf16_to_f32(synth.bf16_from_f32(got)).view(np.uint32),
+                          got.view(np.uint32))
+
+
+def test_decode_nibble_order_is_lsb_first():
+    codes = np.array([[0x76543210, 0xFEDCBA98]], np.uint32)
+    scales = np.array([[0x38]], np.uint8)  # 1.0
+    got = oracle.decode(codes, scales)[0]
+    want = np.array([e2m1_closed_form(c) for c in range(16)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the scale applies to 16 consecutive elements
+    codes2 = np.full((1, 4), 0x22222222, np.uint32)
+    got2 = oracle.decode(codes2, np.array([[0x38, 0x40]], np.uint8))[0]
+    assert np.all(got2[:16] == 1.0) and np.all(got2[16:] == 2.0)
+
+
+def test_decode_matches_compiled_reference():
+    if not oracle.ref_available():
+        pytest.skip("reference CPU code not built")
+    rng = np.random.default_rng(7)
+    w = synth.nvfp4_weights(rng, 33, 704)
+    w.scales[0, :] = np.arange(44, dtype=np.uint8) + 0x60  # include 0x7F
+    assert np.array_equal(oracle.decode(w.codes, w.scales).view(np.uint32),
+                          oracle.ref_decode(w.codes, w.scales).view(np.uint32))
+
+
+def test_synth_dequant_matches_oracle():
+    rng = np.random.default_rng(8)
+    w = synth.nvfp4_weights(rng, 17, 256)
+    assert np.array_equal(w.dequant().view(np.uint32),
+                          oracle.decode(w.codes, w.scales).view(np.uint32))
+
+
+# ---- a4: the fp64 matvec -----------------------------------------------------------
+
+def test_matvec_golden_tiny():
+    g = load("matvec_tiny.npz")
+    n = len([k for k in g.files if k.endswith("_y")])
+    assert n >= 8
+    seen = set()
+    for i in range(n):
+        codes, scales, x, y = (g[f"c{i}_{s}"] for s in ("codes", "scales", "x", "y"))
+        got = oracle.matvec(codes, scales, x)
+        assert np.array_equal(got.view(np.uint32), y.view(np.uint32)), f"case {i}"
+        b = codes.view(np.uint8)
+        seen |= set(np.unique(b & 15)) | set(np.unique(b >> 4))
+    assert seen == set(range(16))
+
+
+def test_matvec_golden_2048():
+    """The 2048x2048 single GEMV on seed-0 inputs, against the reference's output."""
+    x, w = synth.gemv_case(seed=0)
+    got = oracle.matvec(w.codes, w.scales, synth.bf16_to_f32(x))
+    want = load("matvec_2048.npz")["y"]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_matvec_matches_compiled_reference_live():
+    if not oracle.ref_available():
+        pytest.skip("reference CPU code not built")
+    rng = np.random.default_rng(9)
+    for rows, K, T in [(37, 2112, 2), (5, 5376, 1), (100, 704, 4)]:
+        w = synth.nvfp4_weights(rng, rows, K)
+        x = rng.standard_normal((T, K), dtype=np.float32)
+        a = oracle.matvec(w.codes, w.scales, x)
+        b = oracle.ref_matvec(w.codes, w.scales, x)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_matvec_brute_force_exact_rational():
+    """Exact rational dot products, rounded once: the fp64 accumulation in index order
+    may differ from the exact sum by double rounding only, far below one float ulp."""
+    rng = np.random.default_rng(10)
+    w = synth.nvfp4_weights(rng, 6, 48)
+    x = rng.standard_normal((2, 48), dtype=np.float32)
+    W = oracle.decode(w.codes, w.scales)
+    got = oracle.matvec(w.codes, w.scales, x)
+    for t in range(2):
+        for r in range(6):
+            exact = sum(Fraction(float(W[r, i])) * Fraction(float(x[t, i])) for i in range(48))
+            want = np.float32(float(exact))
+            assert abs(float(got[t, r]) - float(want)) <= np.spacing(np.abs(want)) , (t, r)
+
+
+def test_matvec_output_layout_is_token_major():
+    rng = np.random.default_rng(11)
+    w = synth.nvfp4_weights(rng, 4, 32)
+    x = rng.standard_normal((3, 32), dtype=np.float32)
+    got = oracle.matvec(w.codes, w.scales, x)
+    W = oracle.decode(w.codes, w.scales).astype(np.float64)
+    want = (x.astype(np.float64) @ W.T).astype(np.float32)
+    assert got.shape == (3, 4)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-7)
+
+
+def test_matvec_linearity_and_symmetry():
+    rng = np.random.default_rng(12)
+    w = synth.nvfp4_weights(rng, 40, 512)
+    x1 = rng.standard_normal((1, 512), dtype=np.float32)
+    x2 = rng.standard_normal((1, 512), dtype=np.float32)
+    y1, y2 = oracle.matvec(w.codes, w.scales, x1), oracle.matvec(w.codes, w.scales, x2)
+    y12 = oracle.matvec(w.codes, w.scales, x1 + x2)
+    np.testing.assert_allclose(y12, y1 + y2, rtol=1e-5, atol=1e-5)
+    # negating x or every scale's sign bit negates the output exactly
+    assert np.array_equal(oracle.matvec(w.codes, w.scales, -x1), -y1)
+    assert np.array_equal(oracle.matvec(w.codes, w.scales ^ np.uint8(0x80), x1), -y1)
+    # flipping every code's sign bit (bit 3 of each nibble) also negates
+    flipped = w.codes ^ np.uint32(0x88888888)
+    assert np.array_equal(oracle.matvec(flipped, w.scales, x1), -y1)
+    # doubling x is exact
+    assert np.array_equal(oracle.matvec(w.codes, w.scales, 2 * x1), 2 * y1)
+
+
+def test_matvec_tensor_scale():
+    rng = np.random.default_rng(13)
+    w = synth.nvfp4_weights(rng, 16, 256)
+    x = rng.standard_normal((2, 256), dtype=np.float32)
+    y = oracle.matvec(w.codes, w.scales, x)
+    assert np.array_equal(oracle.matvec(w.codes, w.scales, x, tensor_scale=0.5), y * 0.5)
+    y3 = oracle.matvec(w.codes, w.scales, x, tensor_scale=0.3)
+    np.testing.assert_allclose(y3, y * np.float32(0.3), rtol=1e-6)
+
+
+def test_matvec_rows_subset():
+    rng = np.random.default_rng(14)
+    w = synth.nvfp4_weights(rng, 50, 128)
+    x = rng.standard_normal((3, 128), dtype=np.float32)
+    ids = np.array([49, 0, 7, 7, 20])
+    assert np.array_equal(oracle.matvec_rows(w.codes, w.scales, x, ids),
+                          oracle.matvec(w.codes, w.scales, x)[:, ids])
+
+
+# ---- a7: GeLU-tanh ----------------------------------------------------------------
+
+def test_gelu_golden_and_closed_form():
+    g = load("gelu.npz")
+    got = np.array([oracle.gelu(float(v)) for v in g["x"]], np.float32)
+    assert np.array_equal(got.view(np.uint32), g["y"].view(np.uint32))
+    for v, y in zip(g["x"], got):
+        v = float(v)
+        want = 0.5 * v * (1 + math.tanh(0.7978845608028654 * (v + 0.044715 * v ** 3)))
+        assert abs(y - want) <= 4e-7 * max(1.0, abs(want)) + 1e-30
+    assert abs(oracle.gelu(1.0) - 0.841192007) < 1e-8
+
+
+def test_geglu_is_gelu_times_up():
+    rng = np.random.default_rng(15)
+    g = rng.standard_normal(1000, dtype=np.float32) * 3
+    u = rng.standard_normal(1000, dtype=np.float32)
+    got = oracle.geglu(g, u)
+    want = np.array([np.float32(oracle.gelu(float(a))) * b for a, b in zip(g, u)], np.float32)
+    assert np.array_equal(got, want)
+
+
+# ---- a8: dense FFN composition -----------------------------------------------------
+
+def test_dense_mlp_is_the_composition():
+    rng = np.random.default_rng(16)
+    H, I = 128, 64
+    gate = synth.nvfp4_weights(rng, I, H)
+    up = synth.nvfp4_weights(rng, I, H)
+    down = synth.nvfp4_weights(rng, H, I)
+    x = rng.standard_normal((2, H), dtype=np.float32)
+    y = oracle.dense_mlp((gate.codes, gate.scales), (up.codes, up.scales),
+                         (down.codes, down.scales), x)
+    h = oracle.geglu(oracle.matvec(gate.codes, gate.scales, x),
+                     oracle.matvec(up.codes, up.scales, x))
+    assert np.array_equal(y, oracle.matvec(down.codes, down.scales, h))
+
+
+# ---- a10: diff metric --------------------------------------------------------------
+
+def test_diff_metric():
+    a = np.array([1.0, 2.0, 3.0], np.float32)
+    b = np.array([1.0, 2.5, 3.0], np.float32)
+    mx, rel = oracle.diff(a, b)
+    assert mx == 0.5
+    assert abs(rel - 0.5 / math.sqrt(1 + 6.25 + 9)) < 1e-12
+    mx, rel = oracle.diff(np.array([np.nan], np.float32), np.array([1.0], np.float32))
+    assert math.isinf(rel)
+
+
+# ---- a9: MoE routing and expert FFN (no reference code; parity vs mlx-lm unpinned) ----
+
+def test_moe_route_brute_force():
+    rng = np.random.default_rng(17)
+    logits = synth.bf16_to_f32(synth.normal_bf16(rng, (20, 16)))
+    logits[3, :] = 0.5  # all tied: lowest ids win
+    logits[4, [2, 9]] = 10.0  # a tie at the top
+    ids, w = oracle.moe_route(logits, 4)
+    for t in range(20):
+        order = sorted(range(16), key=lambda e: (-float(logits[t, e]), e))[:4]
+        assert list(ids[t]) == order
+        sel = np.array([logits[t, e] for e in order], np.float64)
+        p = np.exp(sel - sel.max())
+        np.testing.assert_allclose(w[t], p / p.sum(), rtol=1e-6)
+    assert list(ids[3]) == [0, 1, 2, 3]
+    assert list(ids[4][:2]) == [2, 9]
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-6)
+
+
+def test_moe_route_skips_empty_experts():
+    rng = np.random.default_rng(18)
+    logits = synth.bf16_to_f32(synth.zipf_logits(rng, 64, 32, n_empty=4))
+    empty = np.where(np.all(np.isinf(logits), axis=0))[0]
+    assert empty.size == 4
+    ids, w = oracle.moe_route(logits, 8)
+    assert not np.isin(ids, empty).any()
+    assert np.all(np.isfinite(w))
+
+
+def test_moe_ffn_is_the_weighted_sum_of_dense_ffns():
+    rng = np.random.default_rng(19)
+    E, H, I, T, k = 6, 64, 32, 3, 2
+    slots = synth.expert_slots(rng, E, H, I)
+    x = synth.bf16_to_f32(synth.normal_bf16(rng, (T, H)))
+    logits = synth.bf16_to_f32(synth.normal_bf16(rng, (T, E)))
+    ids, w = oracle.moe_route(logits, k)
+    y = oracle.moe_ffn(slots, x, ids, w)
+    for t in range(T):
+        acc = np.zeros(H, np.float64)
+        for j in range(k):
+            e = ids[t, j]
+            d = oracle.dense_mlp((slots.piece(e, "gate_w"), slots.piece(e, "gate_s")),
+                                 (slots.piece(e, "up_w"), slots.piece(e, "up_s")),
+                                 (slots.piece(e, "down_w"), slots.piece(e, "down_s")), x[t])
+            acc += np.float64(w[t, j]) * d[0].astype(np.float64)
+        assert np.array_equal(y[t], acc.astype(np.float32))
+    # linear in the routing weights
+    y2 = oracle.moe_ffn(slots, x, ids, 2 * w)
+    assert np.array_equal(y2, 2 * y)
+
+
+def test_expert_slot_layout():
+    offsets, stride, used = synth.slot_layout(2816, 704)
+    assert used == 3_345_408 and stride == 3_358_720 and stride % 16384 == 0
+    assert [offsets[p] for p in synth.PIECES] == sorted(offsets.values())
+
+
+# ---- the generator ---------------------------------------------------------------
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def test_generator_digests():
+    d = json.loads((GOLDEN / "digests.json").read_text())
+    x, w = synth.gemv_case(seed=0)
+    assert sha(w.codes, w.scales, x) == d["gemv_case_seed0"]
+    xg, gate, up = synth.geglu_case(seed=0, rows=64, K=512)
+    assert sha(xg, gate.codes, gate.scales, up.codes, up.scales) == d["geglu_case_seed0_64x512"]
+    a, wg = synth.gemm_case(seed=0, M=16, N=32, K=128)
+    assert sha(wg.codes, wg.scales, a) == d["gemm_case_seed0_16x32x128"]
+    xm, lm, slots = synth.moe_decode_case(seed=0, tokens=2, H=64, I=32, E=4)
+    assert sha(xm, lm, slots.data) == d["moe_decode_case_seed0_tiny"]
+    xp, lp, sp = synth.moe_prefill_case(seed=0, tokens=8, H=64, I=32, E=16)
+    assert sha(xp, lp, sp.data) == d["moe_prefill_case_seed0_tiny"]
+
+
+def test_e4m3_rounding_matches_oracle_and_torch():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(20)
+    v = np.concatenate([np.abs(rng.standard_normal(20000, dtype=np.float32)) * 0.05,
+                        rng.standard_normal(2000, dtype=np.float32) * 100,
+                        np.array([0.0, -0.0, 2 ** -10, 3 * 2 ** -10, 448.0, -448.0,
+                                  0.015625, 0.0146484375], np.float32)])
+    got = synth.e4m3_from_f32(v)
+    want = np.array([oracle.e4m3_from_float(float(a)) for a in v], np.uint8)
+    assert np.array_equal(got, want)
+    t = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, t)
+    # saturation: the generator never emits the +-480 codes
+    big = synth.e4m3_from_f32(np.array([470.0, 1e6, -1e6], np.float32))
+    assert list(big) == [0x7E, 0x7E, 0xFE]
+
+
+def test_bf16_rounding():
+    rng = np.random.default_rng(21)
+    v = rng.standard_normal(5000, dtype=np.float32)
+    got = synth.bf16_from_f32(v)
+    want = np.array([oracle.float_to_bf16(float(a)) for a in v], np.uint16)
+    assert np.array_equal(got, want)
+    torch = pytest.importorskip("torch")
+    t = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, t)
