@@ -1,0 +1,246 @@
+// Tile core of the NVFP4 x bf16 MFMA GEMMs (dense prefill GEMM and the grouped MoE
+// expert GEMMs), gfx950.
+//
+// One workgroup of 4 waves computes a (32*MT) x 256 tile of C = A . W^T:
+//   A   bf16 rows (activations), K contiguous, 2*K bytes per row;
+//   W   NVFP4 rows (codes: K/2 bytes, E4M3 scales: K/16 bytes per row);
+//   C   fp32 accumulators, handed to the caller's epilogue.
+// Row addressing is the caller's: `a_row(r)` gives the byte offset of tile row r of A
+// inside the A descriptor, `w_code(r)` / `w_scale(r)` the byte offsets of W tile row r
+// inside the code / scale descriptors, each 0x80000000 (out of range: reads zeros)
+// for rows that do not exist.  That is how the grouped GEMMs gather token rows and
+// place gate and up rows side by side.
+//
+// gfx950's scaled-FP4 MFMA uses MXFP4 (32-element blocks, E8M0 scales), which cannot
+// express NVFP4's 16-element E4M3 blocks, so W is dequantised to bf16 -- exactly:
+// every e2m1 x e4m3 product has at most 6 significant bits -- and fed to
+// v_mfma_f32_32x32x16_bf16 (measured: sustains ~90% of the bf16 peak with one wave per
+// SIMD; 16x16x32 only ~55%).
+//
+//  * 1 x 4 waves: wave w owns all 32*MT rows and W columns [64w, 64w+64) as MT x 2
+//    MFMA tiles, so every W element is dequantised exactly once per tile.
+//  * A streams HBM/L2 -> LDS with buffer_load ... lds (no VGPR round trip) through a
+//    ring of kStages stage buffers, kStages-1 stages ahead of the MFMAs.  A rows are
+//    128 bytes per stage with 16-byte pieces XOR-swizzled by (row / 2) % 8, so the 32
+//    lanes reading one piece of 32 consecutive rows spread over all banks.
+//  * W's packed codes (32 bytes per row per stage) and scales (4 bytes) ride the same
+//    ring with the same DMA loads; each wave reads its B fragments' code words from
+//    LDS and dequantises them in registers right before its MFMAs
+//    (cvt_scalef32_pk_f32_fp4, x E4M3 scale, keep the exact high halves as bf16).
+//    The packed form keeps W's LDS traffic 4x smaller than a bf16 copy.
+//  * K order: within a 64-wide stage, MFMA step q (0..3) and lane half h = lane/32
+//    take the 8 k values of piece 4h + q (a permutation of k applied to A and W alike,
+//    which leaves the dot products unchanged), so a lane's four code words of a stage
+//    are one 16-byte LDS read and span scale blocks 2h, 2h+1.
+//  * Software pipeline: the MFMAs of step q run while step q+1's A fragments are read
+//    and its B fragments dequantised; one barrier per stage.
+#pragma once
+#include "nvfp4_device.h"
+
+namespace apex_hip {
+namespace gemm_core {
+
+constexpr int kThreads = 256;
+constexpr int BK = 64;
+constexpr int BN = 256;
+constexpr int kARow = BK * 2;              // bytes per A row per stage
+constexpr int kStages = 3;                 // ring depth
+constexpr int kWCode = BN * (BK / 2);      // 8 KiB of W codes per stage
+constexpr int kWScale = BN * (BK / 16);    // 1 KiB of W scales per stage
+constexpr uint32_t kOut = 0x80000000u;     // an offset no descriptor covers
+
+template <int MT> struct Layout {
+    static constexpr int kAStage = MT * 32 * kARow;
+    static constexpr int kStage = kAStage + kWCode + kWScale;
+    static constexpr size_t kLds = (size_t)kStages * kStage;
+};
+constexpr size_t kMaxLds = Layout<8>::kLds;
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ uint32_t pack_bf16_hi(float lo, float hi) {
+    // e2m1 x e4m3 products are exact in bf16: the low 16 bits of the fp32 are zero,
+    // so taking the high halves (bytes 2,3 of lo, then of hi) is exact.
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// Accumulator element e of MFMA tile (i, j) of wave `wave`, lane `lane` sits at tile
+// row 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4 and tile column 64 wave + 32 j + lane % 32.
+template <int MT> using Acc = f32x16_t[MT][2];
+
+template <int MT, typename ARow, typename WCode, typename WScale>
+__device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t ra,
+                                          __amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rs,
+                                          uint32_t K, ARow a_row, WCode w_code, WScale w_scale,
+                                          Acc<MT> &acc) {
+    constexpr int NT = 2;
+    constexpr int kAStage = Layout<MT>::kAStage;
+    constexpr int kStage = Layout<MT>::kStage;
+    constexpr int kALoads = MT;               // DMA loads of 8 A rows per wave per stage
+    constexpr int kLoadsPerStage = kALoads + 2 + 1;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave * 64;       // wave's column offset in the tile
+    const int frow = lane & 31;     // fragment row (A) / column (B) within a 32-wide tile
+    const int h = lane >> 5;        // lane half: k pieces 4h .. 4h+3 of each stage
+
+    // A: wave w copies rows [8 MT w, 8 MT (w+1)) with MT DMA loads of 8 rows; lane l
+    // lands at row 8i + l/8, physical piece l%8, so it fetches logical piece
+    // (l%8) ^ ((row/2)%8) of that row.
+    uint32_t a_off[kALoads];
+#pragma unroll
+    for (int i = 0; i < kALoads; ++i) {
+        const int trow = wave * 8 * MT + 8 * i + (lane >> 3);
+        const uint32_t ro = a_row(trow);
+        a_off[i] = ro == kOut ? kOut : ro + (((lane & 7) ^ ((trow >> 1) & 7)) * 16);
+    }
+    // W codes: 16-byte slot q of the stage holds half (q%2) ^ ((q/16)%2) of tile row
+    // q/2 -- rows 8..15 of every 16 swap halves, so the 16 lanes reading one half of 16
+    // consecutive rows hit distinct bank groups; wave w copies slots [128w, 128w+128)
+    // with 2 DMA loads.  Scales: wave w copies rows [64w, 64w+64), 4 bytes each.
+    uint32_t wc_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = wave * 128 + i * 64 + lane;
+        const int trow = q / 2;
+        const int half = (q & 1) ^ ((trow >> 3) & 1);
+        const uint32_t ro = w_code(trow);
+        wc_off[i] = ro == kOut ? kOut : ro + half * 16;
+    }
+    const uint32_t ws_off = w_scale(wave * 64 + lane);
+
+    auto load_stage = [&](int buf, uint32_t k0) {
+        uint8_t *base = lds + buf * kStage;
+#pragma unroll
+        for (int i = 0; i < kALoads; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (lds_void_t *)(base + (wave * 8 * MT + 8 * i) * kARow), 16, a_off[i] + k0 * 2,
+                0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rc, (lds_void_t *)(base + kAStage + (wave * 128 + i * 64) * 16), 16,
+                wc_off[i] + k0 / 2, 0, 0, APEX_WEIGHT_CPOL);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (lds_void_t *)(base + kAStage + kWCode + wave * 64 * 4), 4, ws_off + k0 / 16, 0, 0,
+            APEX_WEIGHT_CPOL);
+    };
+
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                acc[i][j][e] = 0.0f;
+
+    const uint32_t nk = K / BK;
+    auto kofs = [&](uint32_t st) { return st < nk ? st * BK : 0u; }; // past the end: harmless re-read
+
+    u32x4_t wcode[NT];
+    f32x2_t wsc[NT];
+    bf16x8_v af[2][MT], bf[2][NT];
+    auto read_w = [&](int buf) {
+        const uint8_t *lwc = lds + buf * kStage + kAStage;
+        const uint8_t *lws = lwc + kWCode;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            // rows wn + 32 j + frow, half h (code words 4h .. 4h+3 = scale blocks 2h,
+            // 2h+1), slot 2r + (h ^ ((r/8)%2))
+            const int r = wn + 32 * j + frow;
+            wcode[j] = *reinterpret_cast<const u32x4_t *>(lwc + (2 * r + (h ^ ((r >> 3) & 1))) * 16);
+            const uint32_t sb = *reinterpret_cast<const uint16_t *>(lws + r * 4 + 2 * h);
+            wsc[j] = f32x2_t{e4m3_to_f32(sb), e4m3_to_f32(sb >> 8)};
+        }
+    };
+    // A fragments of step q: rows 32 i + frow, logical piece 4h + q.
+    auto read_a = [&](bf16x8_v (&dst)[MT], int buf, int q) {
+        const uint8_t *la = lds + buf * kStage;
+        const int piece = 4 * h + q;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            const int r = i * 32 + frow;
+            dst[i] = *reinterpret_cast<const bf16x8_v *>(la + r * kARow + ((piece ^ ((r >> 1) & 7)) * 16));
+        }
+    };
+    // B fragments of step q: word q of each tile's codes (8 weights), scale block 2h + q/2.
+    auto dequant_b = [&](bf16x8_v (&dst)[NT], int q) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            f32x2_t v[4];
+            e2m1x8_to_f32(wcode[j][q], v);
+            const float sc = wsc[j][q >> 1];
+            u32x4_t bw;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                bw[e] = pack_bf16_hi(v[e][0] * sc, v[e][1] * sc);
+            dst[j] = __builtin_bit_cast(bf16x8_v, bw);
+        }
+    };
+    auto mfmas = [&](const bf16x8_v (&A)[MT], const bf16x8_v (&B)[NT]) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[i], B[j], acc[i][j], 0, 0, 0);
+    };
+    // One MFMA, then up to two VALU ops and one LDS read, for the MT*NT MFMAs of a step.
+    auto interleave = [&]() {
+#pragma unroll
+        for (int m = 0; m < MT * NT; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0); // VALU
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+        }
+    };
+
+    // Prologue: stages 0 .. kStages-1 in flight; stage 0 visible; step 0 prepared.
+#pragma unroll
+    for (int st = 0; st < kStages; ++st)
+        load_stage(st, kofs(st));
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerStage * (kStages - 1)) : "memory");
+    __syncthreads();
+    read_w(0);
+    read_a(af[0], 0, 0);
+    dequant_b(bf[0], 0);
+
+    // Stage s (buffer s % kStages): after step 2 every read of the buffer has been
+    // issued: the wave waits for them and for its part of stage s+1, meets the barrier
+    // (stage s+1 visible everywhere, buffer s retired) and refills buffer s with stage
+    // s + kStages; step 3 then hides stage s+1's first reads and dequantisation.
+    for (uint32_t s = 0; s < nk; ++s) {
+        const int buf = s % kStages;
+        const int nbuf = (s + 1) % kStages;
+        read_a(af[1], buf, 1);
+        dequant_b(bf[1], 1);
+        mfmas(af[0], bf[0]);
+        interleave();
+        read_a(af[0], buf, 2);
+        dequant_b(bf[0], 2);
+        mfmas(af[1], bf[1]);
+        interleave();
+        read_a(af[1], buf, 3);
+        dequant_b(bf[1], 3);
+        mfmas(af[0], bf[0]);
+        interleave();
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kLoadsPerStage * (kStages - 2))
+                     : "memory");
+        __syncthreads();
+        load_stage(buf, kofs(s + kStages));
+        read_w(nbuf);
+        read_a(af[0], nbuf, 0);
+        dequant_b(bf[0], 0);
+        mfmas(af[1], bf[1]);
+        interleave();
+    }
+    // Drain the DMA loads of the stages past the end, so the LDS is free for the
+    // caller (epilogue staging or the next tile).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+}
+
+} // namespace gemm_core
+} // namespace apex_hip

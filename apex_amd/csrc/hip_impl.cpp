@@ -12,6 +12,7 @@
 
 #include "gemm.h"
 #include "gemv.h"
+#include "moe.h"
 
 namespace {
 
@@ -145,6 +146,60 @@ void geglu_impl(const void *x, bool bf16, const uint32_t *gc, const uint8_t *gs,
               "geglu_nvfp4 launch");
 }
 
+bool moe_use_gemm(uint32_t T, uint32_t k, uint32_t H, uint32_t I) {
+    if (apex_hip::kMoePath == 1)
+        return false;
+    if (apex_hip::kMoePath == 2)
+        return true;
+    return !(T <= apex_hip::kMoeGemvMaxTokens && (uint64_t)T * k <= apex_hip::kMoeGemvMaxPairs &&
+             H <= 3072 && I <= 1024);
+}
+
+void moe_impl(const uint16_t *x, const uint16_t *logits, const apex_moe_slots *slots, uint16_t *y,
+              uint32_t T, uint32_t E, uint32_t k, uint32_t H, uint32_t I, void *ws,
+              size_t ws_bytes, hipStream_t stream) {
+    require(slots != nullptr, "moe_ffn: slots is null");
+    if (T == 0)
+        return;
+    require(x && logits && slots->base && y && ws, "moe_ffn: null pointer");
+    init_device_tuning();
+    const bool gemm = moe_use_gemm(T, k, H, I);
+    apex_hip::MoeArgs a{};
+    a.x = x;
+    a.logits = logits;
+    a.slots = {static_cast<const uint8_t *>(slots->base), slots->stride, slots->gate_w,
+               slots->gate_s, slots->up_w, slots->up_s, slots->down_w, slots->down_s};
+    a.y = y;
+    a.T = T, a.E = E, a.k = k, a.H = H, a.I = I;
+    const char *why = nullptr;
+    if (!apex_hip::moe_supported(a, gemm, &why))
+        fail(APEX_HIP_E_INVALID, std::string("moe_ffn: ") + why);
+    const apex_hip::MoeWorkspace w = apex_hip::moe_workspace(T, E, k, H, I, gemm);
+    require((uintptr_t)ws % 256 == 0, "moe_ffn: workspace must be 256-byte aligned");
+    if (ws_bytes < w.total)
+        fail(APEX_HIP_E_INVALID, "moe_ffn: workspace too small (need " + std::to_string(w.total) +
+                                     " bytes, have " + std::to_string(ws_bytes) + ")");
+    uint8_t *base = static_cast<uint8_t *>(ws);
+    a.ids = reinterpret_cast<int32_t *>(base + w.ids);
+    a.w = reinterpret_cast<float *>(base + w.w);
+    a.plan = reinterpret_cast<int32_t *>(base + w.plan);
+    a.h = reinterpret_cast<uint16_t *>(base + w.h);
+    a.d = reinterpret_cast<uint16_t *>(base + w.d);
+    a.max_tiles = w.max_tiles;
+    hip_check(apex_hip::moe_ffn_launch(a, gemm, stream), "moe_ffn launch");
+}
+
+void moe_route_impl(const uint16_t *logits, uint32_t T, uint32_t E, uint32_t k, int32_t *ids,
+                    float *w, hipStream_t stream) {
+    if (T == 0)
+        return;
+    require(logits && ids && w, "moe_route: null pointer");
+    require(E >= 1 && E <= apex_hip::kMoeMaxExperts, "moe_route: experts must be in [1, 256]");
+    require(k >= 1 && k <= apex_hip::kMoeMaxTopK && k <= E,
+            "moe_route: top_k must be in [1, min(16, experts)]");
+    hip_check(apex_hip::moe_route_launch(logits, T, E, k, ids, w, stream), "moe_route launch");
+}
+
 } // namespace
 
 // ------------------------------------------------------------------------------------
@@ -181,11 +236,13 @@ void ensure_device_current(apex_hip_backend *b, apex_hip_buffer *buf) {
 
 // ---- registry ---------------------------------------------------------------------
 
+constexpr int kMaxArgs = 24;
+
 struct LaunchCtx {
-    void *ptr[16];
-    size_t avail[16]; // bytes from the offset to the end of the buffer
-    uint32_t u[16];
-    float f[16];
+    void *ptr[kMaxArgs];
+    size_t avail[kMaxArgs]; // bytes from the offset to the end of the buffer
+    uint32_t u[kMaxArgs];
+    float f[kMaxArgs];
     apex_hip_dim3 grid, block;
     hipStream_t stream;
 };
@@ -297,6 +354,28 @@ template <bool BF16> void launch_dequant(const LaunchCtx &c) {
               "dequant launch");
 }
 
+// moe_ffn_nvfp4_bf16: x, logits, expert slots, y, workspace; T, E, k, H, I; slot stride
+// and the six piece offsets.
+void launch_moe_ffn(const LaunchCtx &c) {
+    const uint32_t T = c.u[5], E = c.u[6], k = c.u[7], H = c.u[8], I = c.u[9];
+    apex_moe_slots s{c.ptr[2], c.u[10], c.u[11], c.u[12], c.u[13], c.u[14], c.u[15], c.u[16]};
+    need(c, 0, (uint64_t)T * H * 2, "moe_ffn x");
+    need(c, 1, (uint64_t)T * E * 2, "moe_ffn logits");
+    need(c, 2, (uint64_t)E * s.stride, "moe_ffn expert slots");
+    need(c, 3, (uint64_t)T * H * 2, "moe_ffn output");
+    moe_impl((const uint16_t *)c.ptr[0], (const uint16_t *)c.ptr[1], &s, (uint16_t *)c.ptr[3], T, E,
+             k, H, I, c.ptr[4], c.avail[4], c.stream);
+}
+
+void launch_moe_route(const LaunchCtx &c) {
+    const uint32_t T = c.u[3], E = c.u[4], k = c.u[5];
+    need(c, 0, (uint64_t)T * E * 2, "moe_route logits");
+    need(c, 1, (uint64_t)T * k * 4, "moe_route ids");
+    need(c, 2, (uint64_t)T * k * 4, "moe_route weights");
+    moe_route_impl((const uint16_t *)c.ptr[0], T, E, k, (int32_t *)c.ptr[1], (float *)c.ptr[2],
+                   c.stream);
+}
+
 const KernelSpec kKernels[] = {
     {"matmul_nvfp4", "BBBBUU", 1u << 3, launch_matmul_nvfp4},
     {"geglu_f32", "BBBU", 1u << 2, launch_geglu_f32},
@@ -306,6 +385,8 @@ const KernelSpec kKernels[] = {
     {"gemm_nvfp4_bf16", "BBBBUUUF", 1u << 3, launch_gemm_nvfp4_bf16},
     {"dequant_nvfp4_f32", "BBBUUF", 1u << 2, launch_dequant<false>},
     {"dequant_nvfp4_bf16", "BBBUUF", 1u << 2, launch_dequant<true>},
+    {"moe_ffn_nvfp4_bf16", "BBBBBUUUUUUUUUUUU", (1u << 3) | (1u << 4), launch_moe_ffn},
+    {"moe_route_bf16", "BBBUUU", (1u << 1) | (1u << 2), launch_moe_route},
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -739,6 +820,33 @@ int apex_hip_set_gemv_waves_per_cu(int waves) {
     return guard([&] {
         require(waves >= 1 && waves <= 32, "waves per CU must be in [1, 32]");
         apex_hip::kTargetWavesPerCU = waves;
+    });
+}
+
+size_t apex_moe_workspace_bytes(uint32_t tokens, uint32_t experts, uint32_t top_k, uint32_t hidden,
+                                uint32_t inter) {
+    return apex_hip::moe_workspace(tokens, experts, top_k, hidden, inter, true).total;
+}
+
+int apex_moe_route_bf16(const uint16_t *logits, uint32_t tokens, uint32_t experts, uint32_t top_k,
+                        int32_t *ids, float *weights, void *stream) {
+    return guard([&] { moe_route_impl(logits, tokens, experts, top_k, ids, weights, as_stream(stream)); });
+}
+
+int apex_moe_ffn_bf16(const uint16_t *x, const uint16_t *logits, const apex_moe_slots *slots,
+                      uint16_t *y, uint32_t tokens, uint32_t experts, uint32_t top_k,
+                      uint32_t hidden, uint32_t inter, void *workspace, size_t workspace_bytes,
+                      void *stream) {
+    return guard([&] {
+        moe_impl(x, logits, slots, y, tokens, experts, top_k, hidden, inter, workspace,
+                 workspace_bytes, as_stream(stream));
+    });
+}
+
+int apex_hip_set_moe_path(int path) {
+    return guard([&] {
+        require(path >= 0 && path <= 2, "moe path must be 0 (by size), 1 (grouped GEMV) or 2 (grouped GEMM)");
+        apex_hip::kMoePath = path;
     });
 }
 

@@ -95,6 +95,10 @@ _PROTOS = {
     "apex_hip_read_probe": (_I, [_P, _SZ, _P, _P]),
     "apex_hip_read_probe_sink_words": (_I, []),
     "apex_hip_set_gemv_waves_per_cu": (_I, [_I]),
+    "apex_moe_route_bf16": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
+    "apex_moe_workspace_bytes": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
+    "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
+    "apex_hip_set_moe_path": (_I, [_I]),
 }
 
 
@@ -276,6 +280,56 @@ def read_probe_sink_words() -> int:
 
 def set_gemv_waves_per_cu(waves: int) -> None:
     check(lib().apex_hip_set_gemv_waves_per_cu(waves))
+
+
+# ---- MoE expert FFN --------------------------------------------------------------
+
+class MoeSlots(C.Structure):
+    """apex_moe_slots: expert e's pieces at base + e * stride + offset."""
+    _fields_ = [("base", C.c_void_p), ("stride", C.c_uint64), ("gate_w", C.c_uint64),
+                ("gate_s", C.c_uint64), ("up_w", C.c_uint64), ("up_s", C.c_uint64),
+                ("down_w", C.c_uint64), ("down_s", C.c_uint64)]
+
+
+def moe_slots(base: DeviceArray, stride: int, offsets: dict) -> MoeSlots:
+    o = offsets
+    return MoeSlots(base.ptr, stride, o["gate_w"], o["gate_s"], o["up_w"], o["up_s"],
+                    o["down_w"], o["down_s"])
+
+
+def moe_route_bf16(logits, ids, weights, tokens, experts, top_k, stream=None):
+    check(lib().apex_moe_route_bf16(logits.ptr, tokens, experts, top_k, ids.ptr, weights.ptr,
+                                    _s(stream)))
+
+
+def moe_workspace_bytes(tokens, experts, top_k, hidden, inter) -> int:
+    return lib().apex_moe_workspace_bytes(tokens, experts, top_k, hidden, inter)
+
+
+def moe_ffn_bf16(x, logits, slots: MoeSlots, y, tokens, experts, top_k, hidden, inter, workspace,
+                 stream=None):
+    check(lib().apex_moe_ffn_bf16(x.ptr, logits.ptr, C.byref(slots), y.ptr, tokens, experts,
+                                  top_k, hidden, inter, workspace.ptr, workspace.nbytes,
+                                  _s(stream)))
+
+
+def set_moe_path(path: int) -> None:
+    """0 by size (default), 1 grouped GEMV, 2 grouped GEMM."""
+    check(lib().apex_hip_set_moe_path(path))
+
+
+def moe_forward(x, logits, slots, top_k=8):
+    """Host convenience: numpy bf16 x [T,H], logits [T,E], apex_amd.synth.ExpertSlots ->
+    numpy bf16 y [T,H], computed by apex_moe_ffn_bf16 on the current device."""
+    T, H = x.shape
+    E = logits.shape[1]
+    dx, dl = DeviceArray.from_numpy(x), DeviceArray.from_numpy(logits)
+    ds = DeviceArray.from_numpy(slots.data)
+    y = DeviceArray((T, H), np.uint16)
+    ws = DeviceArray((moe_workspace_bytes(T, E, top_k, H, slots.I),), np.uint8)
+    moe_ffn_bf16(dx, dl, moe_slots(ds, slots.stride, slots.offsets), y, T, E, top_k, H, slots.I, ws)
+    synchronize()
+    return y.numpy()
 
 
 # ---------------------------------------------------------------------------------

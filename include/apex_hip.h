@@ -121,6 +121,12 @@ int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
  *                     [M,N], U M, U N, U K, F tensor_scale (apex_nvfp4_gemm_bf16).
  *   dequant_nvfp4_f32 B weights, B scales, B output [rows,K], U hidden_dim,
  *   dequant_nvfp4_bf16 U w_rows, F tensor_scale (src/nvfp4.h:27-43 on the device).
+ *   moe_ffn_nvfp4_bf16 B x bf16 [T,H], B logits bf16 [T,E], B expert slots, B y bf16
+ *                     [T,H], B workspace (apex_moe_workspace_bytes), U T, U E, U top_k,
+ *                     U H, U I, U slot stride, U gate_w, U gate_s, U up_w, U up_s,
+ *                     U down_w, U down_s (apex_moe_ffn_bf16).
+ *   moe_route_bf16    B logits bf16 [T,E], B ids i32 [T,k], B weights f32 [T,k], U T,
+ *                     U E, U top_k (apex_moe_route_bf16).
  * For the kernels after geglu_f32 the launch shape is chosen by the backend; the
  * caller's threadgroups/threads must only be nonzero. */
 int apex_hip_run(apex_hip_backend *backend, const char *kernel, const apex_hip_arg *args,
@@ -221,6 +227,46 @@ int apex_hip_read_probe_sink_words(void);
 
 /* Launch tuning of the GEMV kernels: target resident waves per CU (default 12). */
 int apex_hip_set_gemv_waves_per_cu(int waves);
+
+/* ---- MoE expert FFN (no reference kernel) ------------------------------------------
+ * Semantics: tools/dump_reference.py:208-219 (router top-k, experts combined with the
+ * router weights) with each expert the dense GeGLU FFN of src/ops.h:57-69
+ * (gate/up [I, H], down [H, I], all NVFP4), stored in the fixed-stride slot format of
+ * tools/repack.py:180-213 / src/model_info.h:189-204.  These entry points extend the
+ * ops.h surface for the MoE layer the reference plans (docs/B6_3_attention.md:721-725). */
+
+/* One expert slot layout: expert e's pieces start at base + e * stride + offset. */
+typedef struct {
+    const void *base;   /* device pointer to expert 0's slot (16-byte aligned) */
+    uint64_t stride;    /* bytes between consecutive slots (multiple of 16, < 2 GiB) */
+    uint64_t gate_w, gate_s, up_w, up_s, down_w, down_s; /* piece offsets in a slot */
+} apex_moe_slots;
+
+/* Router: per token the top_k of `experts` bf16 logits (ties to the lower expert id),
+ * in descending order, and softmax weights over those k (fp32).  ids/weights are
+ * [tokens, top_k].  experts <= 256, top_k <= 16. */
+int apex_moe_route_bf16(const uint16_t *logits, uint32_t tokens, uint32_t experts, uint32_t top_k,
+                        int32_t *ids, float *weights, void *stream);
+
+/* Device workspace (bytes) apex_moe_ffn_bf16 needs for these sizes (either path). */
+size_t apex_moe_workspace_bytes(uint32_t tokens, uint32_t experts, uint32_t top_k, uint32_t hidden,
+                                uint32_t inter);
+
+/* y[t] = sum_j w[t,j] * down_e(gelu_tanh(gate_e x_t) * up_e x_t), e = ids[t,j], for
+ * x, y bf16 [tokens, hidden] and logits bf16 [tokens, experts].  Up to 32 tokens (and
+ * 256 token-expert pairs, hidden <= 3072, inter <= 1024) run as grouped GEMVs, the
+ * rest as grouped bf16-MFMA GEMMs; the
+ * combine is deterministic (fixed summation order, no float atomics).  hidden and
+ * inter must be multiples of 64.  `workspace` is device memory of at least
+ * apex_moe_workspace_bytes(), 256-byte aligned; calls sharing one workspace must not
+ * overlap. */
+int apex_moe_ffn_bf16(const uint16_t *x, const uint16_t *logits, const apex_moe_slots *slots,
+                      uint16_t *y, uint32_t tokens, uint32_t experts, uint32_t top_k,
+                      uint32_t hidden, uint32_t inter, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* Path selection of apex_moe_ffn_bf16: 0 by size (default), 1 grouped GEMV, 2 grouped GEMM. */
+int apex_hip_set_moe_path(int path);
 
 #ifdef __cplusplus
 }

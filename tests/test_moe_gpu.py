@@ -1,0 +1,164 @@
+"""GPU parity of the MoE expert FFN (router, grouped GEMV decode path, grouped MFMA GEMM
+prefill path) against the CPU oracle: orc_moe_route (top-k with ties to the lower id,
+softmax over the k) and orc_moe_ffn (per (token, expert) the fp64 dense GeGLU FFN of
+src/tests/dense_mlp.cpp:148-182, combined with the router weights in slot order).
+Parity vs mlx-lm's MoE numerics is unpinned (not importable); the oracle's own
+composition is pinned by tests/test_oracle.py."""
+import numpy as np
+import pytest
+
+import oracle
+from apex_amd import hip, synth
+from tests.helpers import TOL_BF16, bf16, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def default_path():
+    yield
+    hip.set_moe_path(0)
+
+
+def dev(a):
+    return hip.DeviceArray.from_numpy(a)
+
+
+def route(logits, k):
+    T, E = logits.shape
+    ids = hip.DeviceArray((T, k), np.int32)
+    w = hip.DeviceArray((T, k), np.float32)
+    hip.moe_route_bf16(dev(logits), ids, w, T, E, k)
+    hip.synchronize()
+    return ids.numpy(), w.numpy()
+
+
+def check_route(logits, k):
+    ids, w = route(logits, k)
+    want_ids, want_w = oracle.moe_route(bf16(logits), k)
+    assert np.array_equal(ids, want_ids)
+    np.testing.assert_allclose(w, want_w, rtol=2e-6, atol=1e-7)
+
+
+def test_route_decode_shape():
+    rng = np.random.default_rng(0)
+    check_route(synth.normal_bf16(rng, (16, 128)), 8)
+
+
+def test_route_ties_and_odd_sizes():
+    rng = np.random.default_rng(1)
+    lg = synth.normal_bf16(rng, (37, 100))
+    lg[0, :] = synth.bf16_from_f32(np.float32(0.25))      # all tied: ids 0..k-1
+    lg[1, [3, 50, 99]] = synth.bf16_from_f32(np.float32(9.0))  # tie at the top
+    lg[2, :] = synth.bf16_from_f32(-np.arange(100, dtype=np.float32))
+    check_route(lg, 8)
+    check_route(lg, 1)
+    check_route(synth.normal_bf16(rng, (5, 256)), 16)
+    check_route(synth.normal_bf16(rng, (3, 8)), 8)        # k == E
+
+
+def test_route_zipf_prefill_with_empty_experts():
+    rng = np.random.default_rng(2)
+    lg = synth.zipf_logits(rng, 4096, 128)
+    check_route(lg, 8)
+
+
+def moe_ref(x, logits, slots, k, rows=None):
+    xf, lf = bf16(x), bf16(logits)
+    if rows is not None:
+        xf, lf = xf[rows], lf[rows]
+    ids, w = oracle.moe_route(lf, k)
+    return oracle.moe_ffn(slots, xf, ids, w)
+
+
+def run_moe(x, logits, slots, k, path=0):
+    hip.set_moe_path(path)
+    return bf16(hip.moe_forward(x, logits, slots, top_k=k))
+
+
+@pytest.mark.parametrize("path", [1, 2])
+def test_moe_small(path):
+    rng = np.random.default_rng(3)
+    T, E, H, I, k = 6, 16, 256, 128, 4
+    x = synth.normal_bf16(rng, (T, H))
+    logits = synth.normal_bf16(rng, (T, E))
+    slots = synth.expert_slots(rng, E, H, I)
+    got = run_moe(x, logits, slots, k, path)
+    assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16
+
+
+@pytest.mark.parametrize("path", [1, 2])
+def test_moe_odd_shapes(path):
+    """H not a multiple of 256, I not a multiple of 128, E not a multiple of 64, k = 1."""
+    rng = np.random.default_rng(4)
+    for T, E, H, I, k in [(3, 10, 320, 192, 1), (9, 100, 448, 64, 3), (1, 7, 64, 704, 7)]:
+        x = synth.normal_bf16(rng, (T, H))
+        logits = synth.normal_bf16(rng, (T, E))
+        slots = synth.expert_slots(rng, E, H, I)
+        got = run_moe(x, logits, slots, k, path)
+        assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16, (T, E, H, I, k)
+
+
+def test_moe_decode_full_size_both_paths():
+    """MoE decode: 16 tokens, hidden 2816, 128 experts, top-8, intermediate 704, seed 0."""
+    x, logits, slots = synth.moe_decode_case(seed=0)
+    want = moe_ref(x, logits, slots, 8)
+    got_gemv = run_moe(x, logits, slots, 8, 0)  # 16 tokens: the grouped-GEMV path
+    assert rel_l2(got_gemv, want) < TOL_BF16
+    got_gemm = run_moe(x, logits, slots, 8, 2)
+    assert rel_l2(got_gemm, want) < TOL_BF16
+    # deterministic: a second run is bit-identical
+    assert np.array_equal(run_moe(x, logits, slots, 8, 0), got_gemv)
+
+
+def test_moe_hot_experts_span_many_tiles():
+    """All tokens prefer the same 8 experts: each holds 600 rows (two full 256-row
+    tiles plus a tail), the others none."""
+    rng = np.random.default_rng(5)
+    T, E, H, I, k = 600, 32, 256, 128, 8
+    x = synth.normal_bf16(rng, (T, H))
+    lg = rng.standard_normal((T, E), dtype=np.float32)
+    lg[:, [1, 4, 9, 16, 17, 20, 30, 31]] += 20.0
+    logits = synth.bf16_from_f32(lg)
+    slots = synth.expert_slots(rng, E, H, I)
+    got = run_moe(x, logits, slots, k)
+    assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16
+
+
+def test_moe_tile_classes():
+    """Expert sizes hitting every tile class boundary (64, 65, 128, 129, 256, 257 rows)."""
+    rng = np.random.default_rng(6)
+    sizes = [1, 63, 64, 65, 127, 128, 129, 255, 256, 257, 300]
+    E, H, I, k = len(sizes), 128, 64, 1
+    T = sum(sizes)
+    experts = np.repeat(np.arange(E), sizes)
+    lg = np.full((T, E), -5.0, np.float32)
+    lg[np.arange(T), experts] = 5.0
+    logits = synth.bf16_from_f32(lg)
+    x = synth.normal_bf16(rng, (T, H))
+    slots = synth.expert_slots(rng, E, H, I)
+    got = run_moe(x, logits, slots, k)
+    assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16
+
+
+def test_moe_prefill_full_size_sampled():
+    """MoE prefill: 4096 tokens, Zipf(1.1) routing with empty experts, hidden 2816,
+    intermediate 704, top-8.  The oracle checks a 48-token sample (routing is per
+    token); the whole output is checked for determinism and finiteness."""
+    x, logits, slots = synth.moe_prefill_case(seed=0)
+    got = run_moe(x, logits, slots, 8)
+    assert np.all(np.isfinite(got))
+    rows = np.random.default_rng(7).choice(4096, 48, replace=False)
+    rows.sort()
+    assert rel_l2(got[rows], moe_ref(x, logits, slots, 8, rows=rows)) < TOL_BF16
+    assert np.array_equal(run_moe(x, logits, slots, 8), got)
+
+
+def test_moe_rejects_bad_layout():
+    rng = np.random.default_rng(8)
+    T, E, H, I = 2, 4, 96, 64  # hidden not a multiple of 64
+    x = synth.normal_bf16(rng, (T, H))
+    logits = synth.normal_bf16(rng, (T, E))
+    slots = synth.expert_slots(rng, E, H, I)
+    with pytest.raises(hip.ApexHipError, match="multiples of 64"):
+        hip.moe_forward(x, logits, slots, top_k=2)
