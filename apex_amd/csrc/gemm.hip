@@ -45,20 +45,7 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a) {
     Acc<MT> acc;
     gemm_tile<MT>(lds, ra, rc, rs, K, a_row, w_code, w_scale, acc);
 
-    const int lane = threadIdx.x & 63;
-    const uint32_t cn = n0 + (threadIdx.x >> 6) * 64 + (lane & 31);
-    const uint32_t cm = m0 + 4 * (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t m = cm + 32 * i + 8 * (e >> 2) + (e & 3);
-                const uint32_t n = cn + 32 * j;
-                if (m < M && n < N)
-                    a.C[(size_t)m * a.ldc + n] = f32_to_bf16_bits(acc[i][j][e] * a.tensor_scale);
-            }
+    store_tile_bf16<MT>(acc, a.C, a.ldc, m0, n0, M, N, a.tensor_scale);
 }
 
 hipError_t launch(const GemmArgs &a, hipStream_t stream) {

@@ -35,6 +35,8 @@
 //  * Software pipeline: the MFMAs of step q run while step q+1's A fragments are read
 //    and its B fragments dequantised; one barrier per stage.
 #pragma once
+#include <type_traits>
+
 #include "nvfp4_device.h"
 
 namespace apex_hip {
@@ -195,6 +197,9 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
             __builtin_amdgcn_sched_group_barrier(0x002, 2, 0); // VALU
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
         }
+        // Close the region: the next step's MFMAs must not be pulled into this one's
+        // slots, or their fragment reads end up right before them (exposed latency).
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     // Prologue: stages 0 .. kStages-1 in flight; stage 0 visible; step 0 prepared.
@@ -240,6 +245,36 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     // caller (epilogue staging or the next tile).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+}
+
+// Store a tile's accumulators (times `scale`) as bf16 into C (row stride ldc
+// elements): tile row r, column c go to C[(m0 + r) * ldc + n0 + c] for m0 + r < M and
+// n0 + c < N.  Branch-free: the stores go through a buffer descriptor that ends at row
+// M (the hardware drops stores past it) and columns past N get an out-of-range offset.
+template <int MT>
+__device__ __forceinline__ void store_tile_bf16(const Acc<MT> &acc, uint16_t *C, uint32_t ldc,
+                                                uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
+                                                float scale) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t cn = 64 * (threadIdx.x >> 6) + (lane & 31); // column within the tile
+    const uint32_t cm = 4 * (lane >> 5);                       // row within the tile
+    const uint64_t rows = M - m0;
+    const uint64_t bytes = rows * ldc * 2;
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(C + (size_t)m0 * ldc + n0, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const bool col_ok = n0 + cn + 32 * j < N;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t r = cm + 32 * i + 8 * (e >> 2) + (e & 3);
+                const uint32_t off = col_ok ? (r * ldc + cn + 32 * j) * 2 : kOut;
+                __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(acc[i][j][e] * scale), rc,
+                                                      (int)off, 0, 0);
+            }
+    }
 }
 
 } // namespace gemm_core

@@ -18,13 +18,12 @@
 //           neighbours, so outputs do not depend on that order.
 //
 // Decode regime (T <= 32 tokens, T*k <= 256 pairs): bandwidth-bound grouped GEMVs.
-//   gate/up  persistent waves over (active expert, row pair) units: both gate and up
-//            rows of the unit stream once and serve every token routed to the
-//            expert; GeGLU in registers -> h[pos] (bf16).
-//   down     one workgroup per 8 output rows; its 8 waves split the active experts,
-//            stream the experts' 8 down rows and dot them with h of each routed
-//            token; router-weighted partial sums meet in LDS and are added in a fixed
-//            wave order (no float atomics): a deterministic combine.
+//   gate/up  persistent waves over (active expert, 2 rows) units: the unit's gate and
+//            up rows stream once and serve every token routed to the expert; GeGLU in
+//            registers -> h[pos] (bf16).
+//   down     the same over (active expert, 16 rows) units of the down matrices, x =
+//            h[pos] -> d[pos] (bf16).
+//   combine  as in the prefill regime.
 // Prefill regime: MFMA grouped GEMMs on the gemm_core tile (bf16 MFMA on exactly
 // dequantised weights).
 //   m-tiles  per expert, 256-row tiles plus one tail tile of 256, 128 or 64 rows, big
@@ -34,7 +33,10 @@
 //            so that a lane's two accumulator sets are gate and up of one h column:
 //            GeGLU epilogue in registers -> h[pos] (bf16).
 //   down     h rows are contiguous per expert -> d[pos] (bf16).
-//   combine  y[t] = sum_j w[t,j] d[pos(t,j)] in slot order j, fp32 -> bf16.
+//   combine  y[t] = sum_j w[t,j] d[pos(t,j)] in slot order j, fp32 -> bf16: a fixed
+//            summation order, no float atomics, so results are deterministic.
+#include <type_traits>
+
 #include "gemm_core.h"
 #include "gemv_kernels.h"
 #include "moe.h"
@@ -52,6 +54,15 @@ using gemv_detail::RowRegs;
 using gemv_detail::XChunk;
 
 constexpr uint32_t kOutOfRange = 0x80000000u;
+
+// A value the whole wave holds alike, moved to a scalar register.  Values read from
+// memory land in vector registers, and a buffer descriptor or loop bound built from a
+// vector register makes the compiler wrap every load in a per-lane (waterfall) loop.
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int uniform(int v) { return (int)__builtin_amdgcn_readfirstlane((uint32_t)v); }
+__device__ __forceinline__ float uniform_f(float v) {
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v)));
+}
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -74,6 +85,31 @@ __host__ __device__ inline PlanView plan_view(int32_t *plan, uint32_t E, uint32_
 // ---------------------------------------------------------------------------------
 // Routing
 // ---------------------------------------------------------------------------------
+
+// Maximum of a 64-bit key over the wave: DPP within rows of 16 lanes (quad swaps, then
+// half-row and row mirrors pair every lane with one of the other half), then the two
+// cross-row steps by lane shuffles.
+template <int CTRL> __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    uint64_t o;
+    o = dpp_u64<0xB1>(v);  v = o > v ? o : v;  // quad_perm [1,0,3,2]
+    o = dpp_u64<0x4E>(v);  v = o > v ? o : v;  // quad_perm [2,3,0,1]
+    o = dpp_u64<0x141>(v); v = o > v ? o : v;  // row_half_mirror
+    o = dpp_u64<0x140>(v); v = o > v ? o : v;  // row_mirror
+#pragma unroll
+    for (int x = 16; x <= 32; x <<= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)v, x, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), x, 64);
+        o = ((uint64_t)hi << 32) | lo;
+        v = o > v ? o : v;
+    }
+    return v;
+}
 
 // Top-k of one token's E logits (E <= 256) by wave 0..63 lanes, then softmax over the
 // k; lane j < k returns slot j's expert id and weight.  Keys order by logit, then by
@@ -99,13 +135,7 @@ __device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, 
 #pragma unroll
         for (int q = 1; q < 4; ++q)
             best = key[q] > best ? key[q] : best;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const uint32_t lo = __shfl_xor((uint32_t)best, o, 64);
-            const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), o, 64);
-            const uint64_t other = ((uint64_t)hi << 32) | lo;
-            best = other > best ? other : best;
-        }
+        best = wave_max_u64(best);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             if (key[q] == best)
@@ -143,60 +173,87 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *logits, 
 
 // Grouping of the P = T*k pairs by expert (one workgroup of 1024 threads).  With
 // `tiles`, also the m-tile list of the grouped GEMMs: entries (expert, first pos,
-// rows, class) with class 0/1/2 = 256/128/64-row tiles, all class-0 tiles first.
+// rows, class) with class 0/1/2 = 256/128/64-row tiles -- per expert, full 256-row
+// tiles and a tail tile of the smallest class that holds the remainder -- all class-0
+// tiles first.  Counts, offsets and tile slots come from exclusive scans over the
+// experts, so every expert's entries are written in parallel.
+constexpr int kPlanScans = 5; // pair counts, active flags, class 0/1/2 tile counts
+
 __device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
-    __shared__ int cnt[kMoeMaxExperts], cur[kMoeMaxExperts + 1];
+    __shared__ int cnt[kMoeMaxExperts], cur[kMoeMaxExperts];
+    __shared__ int scan[kPlanScans][kMoeMaxExperts];
     const uint32_t E = a.E, P = a.T * a.k;
-    PlanView v = plan_view(a.plan, E, P);
+    const PlanView v = plan_view(a.plan, E, P);
     const int tid = threadIdx.x;
-    for (uint32_t e = tid; e < E; e += blockDim.x)
-        cnt[e] = 0;
+    if (tid < (int)kMoeMaxExperts)
+        cnt[tid] = 0;
     __syncthreads();
     for (uint32_t p = tid; p < P; p += blockDim.x)
         atomicAdd(&cnt[ids[p]], 1);
     __syncthreads();
-    if (tid == 0) {
-        int off = 0, U = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            cur[e] = off;
-            v.off[e] = off;
-            v.cnt[e] = cnt[e];
-            off += cnt[e];
-            if (cnt[e] > 0)
-                v.act[U++] = (int32_t)e;
-        }
-        v.off[E] = off;
-        v.hdr[0] = U;
+    // inclusive Hillis-Steele scans over the 256 expert slots (experts >= E count 0)
+    int val[kPlanScans] = {};
+    const int c = tid < (int)E ? cnt[tid] : 0;
+    const int rem = c % 256;
+    if (tid < (int)kMoeMaxExperts) {
+        val[0] = c;
+        val[1] = c > 0;
+        val[2] = c / 256 + (rem > 128);
+        val[3] = rem > 64 && rem <= 128;
+        val[4] = rem > 0 && rem <= 64;
+#pragma unroll
+        for (int q = 0; q < kPlanScans; ++q)
+            scan[q][tid] = val[q];
+    }
+    __syncthreads();
+    for (int d = 1; d < (int)kMoeMaxExperts; d <<= 1) {
+        int add[kPlanScans] = {};
+        if (tid < (int)kMoeMaxExperts && tid >= d)
+#pragma unroll
+            for (int q = 0; q < kPlanScans; ++q)
+                add[q] = scan[q][tid - d];
+        __syncthreads();
+        if (tid < (int)kMoeMaxExperts)
+#pragma unroll
+            for (int q = 0; q < kPlanScans; ++q)
+                scan[q][tid] += add[q];
+        __syncthreads();
+    }
+    const int last = kMoeMaxExperts - 1;
+    const int n0 = scan[2][last], n1 = scan[3][last], n2 = scan[4][last];
+    if (tid < (int)E) {
+        const int e = tid;
+        const int off = scan[0][e] - val[0]; // exclusive
+        cur[e] = off;
+        v.off[e] = off;
+        v.cnt[e] = c;
+        if (c > 0)
+            v.act[scan[1][e] - 1] = e;
         if (tiles) {
-            int n = 0, big = 0;
-            for (int cls = 0; cls < 3; ++cls) {
-                for (int i = 0; i < U; ++i) {
-                    const int e = v.act[i];
-                    const int c = cnt[e], full = c / 256, rem = c % 256;
-                    int rows = 0, tile_cls = -1;
-                    if (cls == 0) {
-                        for (int f = 0; f < full; ++f) {
-                            int32_t *t = v.tiles + 4 * n++;
-                            t[0] = e, t[1] = cur[e] + 256 * f, t[2] = 256, t[3] = 0;
-                        }
-                        if (rem > 128)
-                            rows = rem, tile_cls = 0;
-                    } else if (cls == 1 && rem > 64 && rem <= 128) {
-                        rows = rem, tile_cls = 1;
-                    } else if (cls == 2 && rem > 0 && rem <= 64) {
-                        rows = rem, tile_cls = 2;
-                    }
-                    if (tile_cls >= 0) {
-                        int32_t *t = v.tiles + 4 * n++;
-                        t[0] = e, t[1] = cur[e] + 256 * full, t[2] = rows, t[3] = tile_cls;
-                    }
-                }
-                if (cls == 0)
-                    big = n;
+            int slot = -1, cls = 0;
+            const int full = c / 256;
+            int t0 = scan[2][e] - val[2];
+            for (int f = 0; f < full; ++f) {
+                int32_t *t = v.tiles + 4 * (t0 + f);
+                t[0] = e, t[1] = off + 256 * f, t[2] = 256, t[3] = 0;
             }
-            v.hdr[1] = n;
-            v.hdr[2] = big;
+            if (rem > 128)
+                slot = t0 + full, cls = 0;
+            else if (rem > 64)
+                slot = n0 + scan[3][e] - 1, cls = 1;
+            else if (rem > 0)
+                slot = n0 + n1 + scan[4][e] - 1, cls = 2;
+            if (slot >= 0) {
+                int32_t *t = v.tiles + 4 * slot;
+                t[0] = e, t[1] = off + 256 * full, t[2] = rem, t[3] = cls;
+            }
         }
+    }
+    if (tid == 0) {
+        v.off[E] = scan[0][last];
+        v.hdr[0] = scan[1][last];
+        v.hdr[1] = n0 + n1 + n2;
+        v.hdr[2] = n0;
     }
     __syncthreads();
     for (uint32_t p = tid; p < P; p += blockDim.x) {
@@ -230,151 +287,198 @@ __global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
 // Decode: grouped GEMVs
 // ---------------------------------------------------------------------------------
 
-// x chunks c = gl + s*G of one bf16 row at byte offset `row_off` (chunks past the row
-// read zeros).
-template <int G, int SLOTS>
-__device__ __forceinline__ void load_x(XChunk<uint16_t> (&xc)[SLOTS], __amdgpu_buffer_rsrc_t r,
-                                       uint32_t row_off, int gl, int nchunks) {
+// x pieces of chunk c = gl + s*G of one bf16 row at byte offset `row_off` (chunks past
+// the row read zeros).
+template <int G>
+__device__ __forceinline__ XChunk<uint16_t> load_x_slot(__amdgpu_buffer_rsrc_t r, uint32_t row_off,
+                                                       int gl, int s, int nchunks) {
+    const int c = gl + s * G;
+    const uint32_t off = c < nchunks ? row_off + (uint32_t)c * 64 : kOutOfRange;
+    XChunk<uint16_t> xc;
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const int c = gl + s * G;
-        const uint32_t off = c < nchunks ? row_off + (uint32_t)c * 64 : kOutOfRange;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            xc[s].p[q] = load_b128(r, off + q * 16);
-    }
+    for (int q = 0; q < 4; ++q)
+        xc.p[q] = load_b128(r, off + q * 16);
+    return xc;
 }
 
-template <int SLOTS>
-__device__ __forceinline__ float row_dot(const RowRegs<SLOTS> &r, const XChunk<uint16_t> (&xc)[SLOTS]) {
-    float acc = 0.0f;
+// Dots of NR weight rows (row sets whose loads are in `w`) with one activation row
+// whose slot-s chunk `xslot(s)` returns, reduced over the G-lane groups.  The fast
+// E4M3 conversion maps 0x7F/0xFF to NaN (the reference decodes +-480): a NaN result
+// is recomputed with the exact decode.
+template <int G, int SLOTS, int NR, bool SERIAL_X, typename XSlot>
+__device__ __forceinline__ void rows_dot(float (&out)[NR], const RowRegs<SLOTS> (&w)[NR],
+                                         XSlot xslot) {
+    auto pass = [&](auto exact) {
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s)
-        chunk_dot(r.codes[s], chunk_scales<true>(r.scales[s]), xc[s], acc);
-    return acc;
+        for (int r = 0; r < NR; ++r)
+            out[r] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const XChunk<uint16_t> xc = xslot(s);
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                // Tie the weight words to x's arrival: the compiler would otherwise decode
+                // every row and slot ahead of the x wait and exceed the register budget.
+                u32x4_t cw = w[r].codes[s];
+                asm volatile("" : "+v"(cw) : "v"(xc.p[3]));
+                chunk_dot(cw, chunk_scales<decltype(exact)::value>(w[r].scales[s]), xc, out[r]);
+            }
+            // SERIAL_X (x read from LDS): the next slot's reads wait for this slot's
+            // dots instead of being hoisted, keeping one slot of x in registers.
+            if constexpr (SERIAL_X)
+                asm volatile("" ::"v"(out[NR - 1]) : "memory");
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            out[r] = group_sum<G>(out[r]);
+    };
+    pass(std::false_type{});
+    bool nan = false;
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+        nan |= __builtin_isnan(out[r]);
+    if (nan)
+        pass(std::true_type{});
 }
 
-// Gate/up: G = 32 lanes per row, two rows per wave and unit; a persistent grid of
-// kGateUpBlocksPerCU workgroups (one wave per SIMD each) per CU.
-constexpr int kGateUpBlocksPerCU = 3;
+// Grouped GEMV over the active experts' row blocks.  A unit is (active expert, NB
+// row sets of 64/G rows); persistent waves walk the units, and each unit's weight rows
+// stream once for every token routed to its expert.
+//   GATE_UP: K = H, gate and up rows side by side, GeGLU -> h[pos][row] (bf16).
+//   else:    K = I, down rows, x = h[pos] -> d[pos][row] (bf16).
+// XLDS: all T activation rows are staged in LDS once per workgroup (piece-major, so
+// a wave's 16-byte reads of one piece of consecutive chunks are conflict-free) and
+// read from there; otherwise each token's row is loaded from global memory (L2).
+constexpr int kGemvBlocksPerCU = 4; // 256-thread workgroups per CU (global x)
+constexpr int kXLdsThreads = 768;   // one workgroup per CU (x in LDS): 3 waves per SIMD
+constexpr uint32_t kXLdsBytes = 120 * 1024;
 
-template <int SLOTS>
-__global__ __launch_bounds__(256, kGateUpBlocksPerCU) void moe_gateup_gemv_kernel(MoeArgs a) {
-    constexpr int G = 32;
+template <bool GATE_UP, int G, int SLOTS, int NB, bool XLDS>
+__global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 256 : 4) void moe_gemv_kernel(MoeArgs a) {
+    constexpr int R = 64 / G;          // rows per row set
+    constexpr int NM = GATE_UP ? 2 : 1;
+    // The plan (at most 256 experts and 256 pairs here) is staged in LDS once, so the
+    // per-unit lookups are LDS reads that never wait behind the weight stream.
+    __shared__ int s_act[kMoeMaxExperts], s_cnt[kMoeMaxExperts], s_off[kMoeMaxExperts];
+    __shared__ uint32_t s_xrow[kMoeGemvMaxPairs]; // activation row of pos (token or pos)
+    extern __shared__ uint4 xl[];                 // XLDS: [T][4 pieces][nchunks]
     const int lane = threadIdx.x & 63;
     const int sub = lane / G, gl = lane % G;
     const uint32_t E = a.E, P = a.T * a.k, H = a.H, I = a.I;
+    const uint32_t K = GATE_UP ? H : I, rows = GATE_UP ? I : H;
+    const int nchunks = (int)(K / 32);
     const PlanView v = plan_view(a.plan, E, P);
-    const uint32_t U = v.hdr[0];
-    const uint32_t rpe = (I + 1) / 2;
-    const uint32_t units = U * rpe;
-    const int nchunks = (int)(H / 32);
+    const __amdgpu_buffer_rsrc_t rx =
+        GATE_UP ? make_rsrc(a.x, a.T * H * 2) : make_rsrc(a.h, P * I * 2);
+    for (uint32_t i = threadIdx.x; i < E; i += blockDim.x) {
+        s_act[i] = v.act[i];
+        s_cnt[i] = v.cnt[i];
+        s_off[i] = v.off[i];
+    }
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x)
+        s_xrow[i] = GATE_UP ? (uint32_t)v.pair_of_pos[i] / a.k : i;
+    if constexpr (XLDS) {
+        // entry (t, piece q, chunk c) = bytes [64 c + 16 q, +16) of row t
+        const uint32_t n = a.T * 4 * nchunks;
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+            const uint32_t t = i / (4 * nchunks), rem = i % (4 * nchunks);
+            const uint32_t c = rem / 4, q = rem % 4;
+            xl[(t * 4 + q) * nchunks + c] =
+                __builtin_bit_cast(uint4, load_b128(rx, t * K * 2 + c * 64 + q * 16));
+        }
+    }
+    const uint32_t U = uniform(v.hdr[0]);
+    __syncthreads();
+    const uint32_t wave = uniform(threadIdx.x >> 6);
+    const uint32_t waves_per_block = blockDim.x / 64;
+    const uint32_t per_e = (rows + R * NB - 1) / (R * NB);
+    const uint32_t units = U * per_e;
     const bool last_ok = gl + (SLOTS - 1) * G < nchunks;
     const uint32_t last_c = last_ok ? (SLOTS - 1) * G * 16 : kOutOfRange;
     const uint32_t last_s = last_ok ? (SLOTS - 1) * G * 2 : kOutOfRange;
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.T * H * 2);
-    const uint32_t nw = gridDim.x * 4;
-    for (uint32_t u = blockIdx.x * 4 + (threadIdx.x >> 6); u < units; u += nw) {
-        const uint32_t ai = u / rpe;
-        const uint32_t row = 2 * (u - ai * rpe) + sub;
-        const int e = v.act[ai];
-        const uint8_t *slot = a.slots.base + (size_t)e * a.slots.stride;
-        const uint32_t lrow = row < I ? row : I;
-        RowRegs<SLOTS> rg, ru;
-        load_row<SLOTS, G>(rg, make_rsrc(slot + a.slots.gate_w, I * H / 2),
-                           make_rsrc(slot + a.slots.gate_s, I * H / 16), lrow, gl, H, last_c, last_s);
-        load_row<SLOTS, G>(ru, make_rsrc(slot + a.slots.up_w, I * H / 2),
-                           make_rsrc(slot + a.slots.up_s, I * H / 16), lrow, gl, H, last_c, last_s);
-        const int n = v.cnt[e], p0 = v.off[e];
+    const uint64_t off_w[2] = {GATE_UP ? a.slots.gate_w : a.slots.down_w, a.slots.up_w};
+    const uint64_t off_s[2] = {GATE_UP ? a.slots.gate_s : a.slots.down_s, a.slots.up_s};
+    const uint32_t wbytes = rows * K / 2, sbytes = rows * K / 16;
+    const uint32_t nw = gridDim.x * waves_per_block;
+
+    // Loads of unit u into `w` (a unit past the end loads nothing).
+    auto issue = [&](RowRegs<SLOTS> (&w)[NM * NB], uint32_t u) {
+        if (u >= units)
+            return;
+        const uint32_t ai = u / per_e;
+        const uint32_t r0 = (u - ai * per_e) * R * NB;
+        const uint8_t *slot = a.slots.base + (size_t)uniform(s_act[ai]) * a.slots.stride;
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const uint32_t row = r0 + b * R + sub;
+                load_row<SLOTS, G>(w[m * NB + b], make_rsrc(slot + off_w[m], wbytes),
+                                   make_rsrc(slot + off_s[m], sbytes), row < rows ? row : rows, gl,
+                                   K, last_c, last_s);
+            }
+    };
+    // Every token of unit u's expert against the rows in `w`.
+    auto compute = [&](const RowRegs<SLOTS> (&w)[NM * NB], uint32_t u) {
+        const uint32_t ai = u / per_e;
+        const uint32_t r0 = (u - ai * per_e) * R * NB;
+        const int e = uniform(s_act[ai]);
+        const int n = uniform(s_cnt[e]), p0 = uniform(s_off[e]);
         for (int i = 0; i < n; ++i) {
             const int pos = p0 + i;
-            const uint32_t t = (uint32_t)v.pair_of_pos[pos] / a.k;
-            // one slot of x at a time keeps the register footprint at 4 waves per SIMD
-            float g = 0.0f, up = 0.0f;
+            const uint32_t xr = uniform(s_xrow[pos]);
+            float dots[NM * NB];
+            if constexpr (XLDS) {
+                rows_dot<G, SLOTS, NM * NB, true>(dots, w, [&](int s) {
+                    const int c = gl + s * G;
+                    XChunk<uint16_t> xc;
 #pragma unroll
-            for (int s = 0; s < SLOTS; ++s) {
-                const int c = gl + s * G;
-                const uint32_t off = c < nchunks ? t * H * 2 + (uint32_t)c * 64 : kOutOfRange;
-                XChunk<uint16_t> xc;
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    xc.p[q] = load_b128(rx, off + q * 16);
-                chunk_dot(rg.codes[s], chunk_scales<true>(rg.scales[s]), xc, g);
-                chunk_dot(ru.codes[s], chunk_scales<true>(ru.scales[s]), xc, up);
+                    for (int q = 0; q < 4; ++q)
+                        xc.p[q] = c < nchunks ? __builtin_bit_cast(u32x4_t, xl[(xr * 4 + q) * nchunks + c])
+                                              : u32x4_t{0, 0, 0, 0};
+                    return xc;
+                });
+            } else {
+                rows_dot<G, SLOTS, NM * NB, false>(dots, w, [&](int s) {
+                    return load_x_slot<G>(rx, xr * K * 2, gl, s, nchunks);
+                });
             }
-            g = group_sum<G>(g);
-            up = group_sum<G>(up);
-            if (gl == 0 && row < I)
-                a.h[(size_t)pos * I + row] = f32_to_bf16_bits(gelu_tanh(g) * up);
-        }
-    }
-}
-
-// Down + combine: workgroup b owns output rows [8b, 8b+8); G = 8 lanes per row.
-constexpr int kDownWaves = 8;
-
-template <int SLOTS>
-__global__ __launch_bounds__(kDownWaves * 64) void moe_down_gemv_kernel(MoeArgs a) {
-    constexpr int G = 8, R = 8;
-    __shared__ float part[kDownWaves][kMoeGemvMaxTokens][R];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int sub = lane / G, gl = lane % G;
-    const uint32_t E = a.E, P = a.T * a.k, H = a.H, I = a.I;
-    const PlanView v = plan_view(a.plan, E, P);
-    for (uint32_t q = threadIdx.x; q < kDownWaves * kMoeGemvMaxTokens * R; q += blockDim.x)
-        (&part[0][0][0])[q] = 0.0f;
-    __syncthreads();
-    const uint32_t U = v.hdr[0];
-    const uint32_t row = blockIdx.x * R + sub;
-    const uint32_t lrow = row < H ? row : H;
-    const int nchunks = (int)(I / 32);
-    const bool last_ok = gl + (SLOTS - 1) * G < nchunks;
-    const uint32_t last_c = last_ok ? (SLOTS - 1) * G * 16 : kOutOfRange;
-    const uint32_t last_s = last_ok ? (SLOTS - 1) * G * 2 : kOutOfRange;
-    const __amdgpu_buffer_rsrc_t rh = make_rsrc(a.h, P * I * 2);
-    // Two experts per step: both experts' rows are in flight before the first dot.
-    for (uint32_t ai = wave; ai < U; ai += 2 * kDownWaves) {
-        const uint32_t bi = ai + kDownWaves;
-        const int e0 = v.act[ai];
-        const int e1 = bi < U ? v.act[bi] : e0;
-        RowRegs<SLOTS> r[2];
-        const int es[2] = {e0, e1};
+            if (gl != 0)
+                continue;
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const uint8_t *slot = a.slots.base + (size_t)es[b] * a.slots.stride;
-            load_row<SLOTS, G>(r[b], make_rsrc(slot + a.slots.down_w, H * I / 2),
-                               make_rsrc(slot + a.slots.down_s, H * I / 16),
-                               (b == 1 && bi >= U) ? H : lrow, gl, I, last_c, last_s);
+            for (int b = 0; b < NB; ++b) {
+                const uint32_t row = r0 + b * R + sub;
+                if (row >= rows)
+                    continue;
+                if constexpr (GATE_UP)
+                    a.h[(size_t)pos * I + row] = f32_to_bf16_bits(gelu_tanh(dots[b]) * dots[NB + b]);
+                else
+                    a.d[(size_t)pos * H + row] = f32_to_bf16_bits(dots[b]);
+            }
         }
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            if (b == 1 && bi >= U)
+    };
+
+    const uint32_t u0 = blockIdx.x * waves_per_block + wave;
+    if constexpr (XLDS) {
+        // Activations come from LDS, so the next unit's weight loads can be in flight
+        // while this unit computes (two register sets, body unrolled twice so the
+        // buffer indices are constants).
+        RowRegs<SLOTS> wa[NM * NB], wb[NM * NB];
+        issue(wa, u0);
+        for (uint32_t u = u0; u < units; u += 2 * nw) {
+            issue(wb, u + nw);
+            compute(wa, u);
+            if (u + nw >= units)
                 break;
-            const int e = es[b];
-            const int n = v.cnt[e], p0 = v.off[e];
-            for (int i = 0; i < n; ++i) {
-                const int pos = p0 + i;
-                const uint32_t pair = (uint32_t)v.pair_of_pos[pos];
-                const uint32_t t = pair / a.k;
-                XChunk<uint16_t> xc[SLOTS];
-                load_x<G, SLOTS>(xc, rh, (uint32_t)pos * I * 2, gl, nchunks);
-                const float d = group_sum<G>(row_dot(r[b], xc));
-                if (gl == 0)
-                    part[wave][t][sub] += a.w[pair] * d;
-            }
+            issue(wa, u + 2 * nw);
+            compute(wb, u + nw);
         }
-    }
-    __syncthreads();
-    for (uint32_t q = threadIdx.x; q < a.T * R; q += blockDim.x) {
-        const uint32_t t = q / R, rr = q % R;
-        const uint32_t orow = blockIdx.x * R + rr;
-        if (orow >= H)
-            continue;
-        float s = 0.0f;
-        for (int w = 0; w < kDownWaves; ++w)
-            s += part[w][t][rr];
-        a.y[(size_t)t * H + orow] = f32_to_bf16_bits(s);
+    } else {
+        for (uint32_t u = u0; u < units; u += nw) {
+            RowRegs<SLOTS> w[NM * NB];
+            issue(w, u);
+            compute(w, u);
+        }
     }
 }
 
@@ -408,19 +512,20 @@ __device__ __forceinline__ void gateup_tile(const MoeArgs &a, uint8_t *lds, cons
     };
     Acc<MT> acc;
     gemm_tile<MT>(lds, ra, rw, rw, H, a_row, w_code, w_scale, acc);
+    // h[row0 + r][col] = gelu(gate) * up, branch-free: the store descriptor ends at
+    // row nrows, columns past I get an out-of-range offset.
     const int lane = threadIdx.x & 63;
     const uint32_t col = c0 + 32 * (threadIdx.x >> 6) + (lane & 31);
     const uint32_t rb = 4 * (lane >> 5);
-    if (col >= I)
-        return;
+    const __amdgpu_buffer_rsrc_t rh = make_rsrc(a.h + (size_t)row0 * I, nrows * I * 2);
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
             const uint32_t r = rb + 32 * i + 8 * (q >> 2) + (q & 3);
-            if (r < nrows)
-                a.h[(size_t)(row0 + r) * I + col] =
-                    f32_to_bf16_bits(gelu_tanh(acc[i][0][q]) * acc[i][1][q]);
+            const uint32_t off = col < I ? (r * I + col) * 2 : kOut;
+            __builtin_amdgcn_raw_buffer_store_b16(
+                f32_to_bf16_bits(gelu_tanh(acc[i][0][q]) * acc[i][1][q]), rh, (int)off, 0, 0);
         }
 }
 
@@ -430,11 +535,11 @@ __global__ __launch_bounds__(kThreads) void moe_gateup_gemm_kernel(MoeArgs a) {
     const PlanView v = plan_view(a.plan, E, P);
     const uint32_t nn = (a.I + kGateUpCols - 1) / kGateUpCols;
     const uint32_t mt = blockIdx.x / nn, nt = blockIdx.x % nn;
-    if (mt >= (uint32_t)v.hdr[1])
+    if (mt >= uniform(v.hdr[1]))
         return;
     const int32_t *t = v.tiles + 4 * mt;
-    const int e = t[0], cls = t[3];
-    const uint32_t row0 = t[1], nrows = t[2], c0 = nt * kGateUpCols;
+    const int e = uniform(t[0]), cls = uniform(t[3]);
+    const uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]), c0 = nt * kGateUpCols;
     if (cls == 0)
         gateup_tile<8>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
     else if (cls == 1)
@@ -456,20 +561,7 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
     auto w_scale = [=](int r) { return n0 + r < H ? ds + (n0 + r) * (I / 16) : kOut; };
     Acc<MT> acc;
     gemm_tile<MT>(lds, ra, rw, rw, I, a_row, w_code, w_scale, acc);
-    const int lane = threadIdx.x & 63;
-    const uint32_t cn = n0 + 64 * (threadIdx.x >> 6) + (lane & 31);
-    const uint32_t rb = 4 * (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const uint32_t r = rb + 32 * i + 8 * (q >> 2) + (q & 3);
-                const uint32_t n = cn + 32 * j;
-                if (r < nrows && n < H)
-                    a.d[(size_t)(row0 + r) * H + n] = f32_to_bf16_bits(acc[i][j][q]);
-            }
+    store_tile_bf16<MT>(acc, a.d + (size_t)row0 * H, H, 0, n0, nrows, H, 1.0f);
 }
 
 __global__ __launch_bounds__(kThreads) void moe_down_gemm_kernel(MoeArgs a) {
@@ -478,11 +570,11 @@ __global__ __launch_bounds__(kThreads) void moe_down_gemm_kernel(MoeArgs a) {
     const PlanView v = plan_view(a.plan, E, P);
     const uint32_t nn = (a.H + BN - 1) / BN;
     const uint32_t mt = blockIdx.x / nn, nt = blockIdx.x % nn;
-    if (mt >= (uint32_t)v.hdr[1])
+    if (mt >= uniform(v.hdr[1]))
         return;
     const int32_t *t = v.tiles + 4 * mt;
-    const int e = t[0], cls = t[3];
-    const uint32_t row0 = t[1], nrows = t[2], n0 = nt * BN;
+    const int e = uniform(t[0]), cls = uniform(t[3]);
+    const uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]), n0 = nt * BN;
     if (cls == 0)
         down_tile<8>(a, lds, e, row0, nrows, n0);
     else if (cls == 1)
@@ -491,32 +583,46 @@ __global__ __launch_bounds__(kThreads) void moe_down_gemm_kernel(MoeArgs a) {
         down_tile<2>(a, lds, e, row0, nrows, n0);
 }
 
-// y[t] = sum_j w[t,j] d[pos(t,j)], slot order, fp32; 8 columns per thread.
+// y[t] = sum_j w[t,j] d[pos(t,j)], slot order, fp32; 8 columns per thread.  Workgroup
+// (t, c) covers columns [2048 c, 2048 c + 2048) of token t; the k pairs' rows are
+// loaded 8 at a time (slots past k read zeros with weight 0) so the loads overlap.
+constexpr uint32_t kCombineCols = 256 * 8;
+
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
     const uint32_t t = blockIdx.x;
     const uint32_t E = a.E, P = a.T * a.k, H = a.H, k = a.k;
     const PlanView v = plan_view(a.plan, E, P);
     const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.d, P * H * 2);
-    for (uint32_t c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
-        float acc[8] = {};
-        for (uint32_t j = 0; j < k; ++j) {
-            const uint32_t pair = t * k + j;
-            const uint32_t pos = (uint32_t)v.pos_of_pair[pair];
-            const float wt = a.w[pair];
-            const u32x4_t dv = load_b128(rd, (pos * H + c) * 2);
+    const uint32_t c = blockIdx.y * kCombineCols + threadIdx.x * 8;
+    if (c >= H)
+        return;
+    float acc[8] = {};
+    for (uint32_t j0 = 0; j0 < k; j0 += 8) {
+        u32x4_t dv[8];
+        float wt[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const uint32_t j = j0 + jj;
+            const bool ok = j < k;
+            const uint32_t pair = t * k + (ok ? j : 0);
+            wt[jj] = ok ? uniform_f(a.w[pair]) : 0.0f;
+            const uint32_t pos = uniform(v.pos_of_pair[pair]);
+            dv[jj] = load_b128(rd, ok ? (pos * H + c) * 2 : kOutOfRange);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                acc[2 * q] += wt * bf16_bits_to_f32(dv[q] & 0xFFFFu);
-                acc[2 * q + 1] += wt * bf16_bits_to_f32(dv[q] >> 16);
+                acc[2 * q] += wt[jj] * bf16_bits_to_f32(dv[jj][q] & 0xFFFFu);
+                acc[2 * q + 1] += wt[jj] * bf16_bits_to_f32(dv[jj][q] >> 16);
             }
-        }
-        u32x4_t o;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            o[q] = (uint32_t)f32_to_bf16_bits(acc[2 * q]) |
-                   ((uint32_t)f32_to_bf16_bits(acc[2 * q + 1]) << 16);
-        *reinterpret_cast<u32x4_t *>(a.y + (size_t)t * H + c) = o;
     }
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        o[q] = (uint32_t)f32_to_bf16_bits(acc[2 * q]) |
+               ((uint32_t)f32_to_bf16_bits(acc[2 * q + 1]) << 16);
+    *reinterpret_cast<u32x4_t *>(a.y + (size_t)t * H + c) = o;
 }
 
 template <typename F> hipError_t set_lds(F *kernel, size_t bytes, bool &done) {
@@ -547,8 +653,7 @@ MoeWorkspace moe_workspace(uint32_t T, uint32_t E, uint32_t k, uint32_t H, uint3
     w.h = off;
     off = align256(off + P * I * 2);
     w.d = off;
-    if (gemm)
-        off = align256(off + P * H * 2);
+    off = align256(off + P * H * 2);
     w.total = off;
     return w;
 }
@@ -582,7 +687,7 @@ bool moe_supported(const MoeArgs &a, bool gemm, const char **why) {
     if (!gemm) {
         if (a.T > kMoeGemvMaxTokens || P > kMoeGemvMaxPairs)
             return no("the grouped-GEMV path takes at most 32 tokens and 256 (token, expert) pairs");
-        if (gemv_slots(a.H, 32) > 3 || gemv_slots(a.I, 8) > 4)
+        if (gemv_slots(a.H, 32) > 3 || gemv_slots(a.I, 32) > 1)
             return no("the grouped-GEMV path takes hidden <= 3072 and intermediate <= 1024");
     }
     return true;
@@ -602,19 +707,41 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
         return hipSuccess;
     if (!gemm) {
         hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(1024), 0, stream, a);
-        const uint32_t grid = (uint32_t)kNumCUs * kGateUpBlocksPerCU;
-        switch (gemv_slots(a.H, 32)) {
-        case 1: hipLaunchKernelGGL(moe_gateup_gemv_kernel<1>, dim3(grid), dim3(256), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL(moe_gateup_gemv_kernel<2>, dim3(grid), dim3(256), 0, stream, a); break;
-        default: hipLaunchKernelGGL(moe_gateup_gemv_kernel<3>, dim3(grid), dim3(256), 0, stream, a); break;
+        const dim3 grid((uint32_t)kNumCUs * kGemvBlocksPerCU), block(256);
+        // gate/up: 32 lanes per row; x staged in LDS when it fits (one workgroup per
+        // CU, next unit's weights prefetched), else read per token from global memory
+        const uint32_t xbytes = a.T * (a.H / 32) * 64;
+        if (xbytes <= kXLdsBytes) {
+            static bool attr[3] = {};
+            const dim3 lgrid((uint32_t)kNumCUs), lblock(kXLdsThreads);
+            hipError_t err = hipSuccess;
+            switch (gemv_slots(a.H, 32)) {
+            case 1:
+                err = set_lds(moe_gemv_kernel<true, 32, 1, 2, true>, kXLdsBytes, attr[0]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, true>), lgrid, lblock, xbytes, stream, a);
+                break;
+            case 2:
+                err = set_lds(moe_gemv_kernel<true, 32, 2, 1, true>, kXLdsBytes, attr[1]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 1, true>), lgrid, lblock, xbytes, stream, a);
+                break;
+            default:
+                err = set_lds(moe_gemv_kernel<true, 32, 3, 1, true>, kXLdsBytes, attr[2]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, true>), lgrid, lblock, xbytes, stream, a);
+                break;
+            }
+            if (err != hipSuccess)
+                return err;
+        } else {
+            switch (gemv_slots(a.H, 32)) {
+            case 1: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, false>), grid, block, 0, stream, a); break;
+            case 2: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 2, false>), grid, block, 0, stream, a); break;
+            default: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, false>), grid, block, 0, stream, a); break;
+            }
         }
-        const dim3 dgrid((a.H + 7) / 8), dblock(kDownWaves * 64);
-        switch (gemv_slots(a.I, 8)) {
-        case 1: hipLaunchKernelGGL(moe_down_gemv_kernel<1>, dgrid, dblock, 0, stream, a); break;
-        case 2: hipLaunchKernelGGL(moe_down_gemv_kernel<2>, dgrid, dblock, 0, stream, a); break;
-        case 3: hipLaunchKernelGGL(moe_down_gemv_kernel<3>, dgrid, dblock, 0, stream, a); break;
-        default: hipLaunchKernelGGL(moe_down_gemv_kernel<4>, dgrid, dblock, 0, stream, a); break;
-        }
+        // down: 32 lanes per row (one slot for I <= 1024), 8 row sets (16 rows) per unit
+        hipLaunchKernelGGL((moe_gemv_kernel<false, 32, 1, 8, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL(moe_combine_kernel, dim3(a.T, (a.H + kCombineCols - 1) / kCombineCols),
+                           dim3(256), 0, stream, a);
         return hipGetLastError();
     }
     static bool lds_gateup = false, lds_down = false;
@@ -632,7 +759,8 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     const uint32_t nn_d = (a.H + BN - 1) / BN;
     hipLaunchKernelGGL(moe_down_gemm_kernel, dim3(a.max_tiles * nn_d), dim3(kThreads), kMaxLds,
                        stream, a);
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(a.T), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(a.T, (a.H + kCombineCols - 1) / kCombineCols),
+                       dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

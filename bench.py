@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the NVFP4 matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extra]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+                    [--calibrate]
 
 A step is one launch of the hot-path kernel over one batch of synthetic input with
 every operand already resident in HBM.  The headline workload is the decode fused
@@ -14,6 +15,18 @@ The roofline object prices the same kernel against MI355X's 8 TB/s HBM peak; the
 cpu_baseline object times the reference's own CPU implementation of the op
 (src/tests/cpu_ref.h matvecNvfp4Cpu + geluTanh, compiled from its sources) on a
 bounded sample, single-threaded like the reference.
+
+The "secondary" object carries the metric's second half and the other workloads of
+the path, each timed the same way (HIP events around back-to-back steps):
+  moe_prefill   MoE layer prefill: 4096 tokens, hidden 2816, 128 experts, top-8,
+                intermediate 704, Zipf(1.1) routing -> TFLOP/s vs the 2.5 PFLOP/s
+                dense bf16 MFMA peak (flops of the routed pairs only);
+  gemm_prefill  dense prefill GEMM bf16 [2048,5376] x NVFP4 [21504x5376]^T -> TFLOP/s;
+  moe_decode    MoE decode: 16 tokens, same experts -> GB/s of the distinct experts'
+                weights + activations (expert slots rotated over copies > MALL).
+--calibrate runs, before the timed steps, one streaming read of 1 GiB and one 256 MiB
+device copy, the known-size kernels the HBM counters (FETCH_SIZE / WRITE_SIZE) of a
+rocprofv3 --pmc pass are scaled by.
 """
 from __future__ import annotations
 
@@ -101,19 +114,143 @@ def cpu_baseline_geglu(budget_s: float = 10.0, rows=21504, K=5376):
     mv(gate.codes[:256], gate.scales[:256], xf)
     per_row = (time.perf_counter() - t) / 256
     n = int(min(rows, max(256, budget_s / (2 * per_row))))
+    reps = 0
     t = time.perf_counter()
-    g = mv(gate.codes[:n], gate.scales[:n], xf)
-    u = mv(up.codes[:n], up.scales[:n], xf)
-    h = np.array([gelu(float(a)) for a in g.ravel()], np.float32) * u.ravel()
+    while True:
+        g = mv(gate.codes[:n], gate.scales[:n], xf)
+        u = mv(up.codes[:n], up.scales[:n], xf)
+        h = np.array([gelu(float(a)) for a in g.ravel()], np.float32) * u.ravel()
+        reps += 1
+        if time.perf_counter() - t >= budget_s:
+            break
     dt = time.perf_counter() - t
     bytes_per_row = (algo_bytes - xf.size * 2 - rows * 2) / rows
-    sample_bytes = n * bytes_per_row + x.nbytes + n * 2
+    sample_bytes = reps * (n * bytes_per_row + x.nbytes + n * 2)
     return {
         "value": round(sample_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
         "sample": f"decode GeGLU, gate+up rows 0..{n - 1} of {rows} (K={K}), batch 1, "
-                  f"{dt:.1f} s single-threaded, host nproc={os.cpu_count()}",
+                  f"{reps} pass(es) in {dt:.1f} s single-threaded, host nproc={os.cpu_count()}",
         "_h": h,
     }
+
+
+def time_steps(step, steps, warmup, stream):
+    """Average seconds per step of `step(i)` launched back to back on `stream`."""
+    for i in range(warmup):
+        step(i)
+    stream.synchronize()
+    hip.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / 1e3 / steps
+
+
+def moe_setup(case, copies):
+    x, logits, slots = case
+    T, H = x.shape
+    E = logits.shape[1]
+    dx, dl = hip.DeviceArray.from_numpy(x), hip.DeviceArray.from_numpy(logits)
+    base = hip.DeviceArray.from_numpy(slots.data)
+    sl = [base]
+    for _ in range(copies - 1):
+        c = hip.DeviceArray(base.shape, base.dtype)
+        c.copy_from(base)
+        sl.append(c)
+    y = hip.DeviceArray((T, H), np.uint16)
+    ws = hip.DeviceArray((hip.moe_workspace_bytes(T, E, 8, H, slots.I),), np.uint8)
+    ms = [hip.moe_slots(b, slots.stride, slots.offsets) for b in sl]
+    return dx, dl, sl, ms, y, ws
+
+
+def time_moe_decode(steps, warmup):
+    case = synth.moe_decode_case(seed=0)
+    x, logits, slots = case
+    T, H, E, I = x.shape[0], x.shape[1], logits.shape[1], slots.I
+    # distinct experts the step streams: from the library's own router
+    ids = hip.DeviceArray((T, 8), np.int32)
+    wts = hip.DeviceArray((T, 8), np.float32)
+    hip.moe_route_bf16(hip.DeviceArray.from_numpy(logits), ids, wts, T, E, 8)
+    hip.synchronize()
+    U = len(np.unique(ids.numpy()))
+    piece_bytes = 3 * (I * H // 2 + I * H // 16)
+    algo = U * piece_bytes + x.nbytes + logits.nbytes + T * H * 2
+    copies = max(2, int(np.ceil(2.5 * MALL_BYTES / (U * piece_bytes))))
+    dx, dl, sl, ms, y, ws = moe_setup(case, copies)
+    stream = hip.Stream()
+
+    def step(i):
+        hip.moe_ffn_bf16(dx, dl, ms[i % copies], y, T, E, 8, H, I, ws, stream=stream)
+
+    sec = time_steps(step, steps, warmup, stream)
+    stream.close()
+    gbs = algo / sec / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(sec * 1e3, 6),
+            "roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(algo),
+            "distinct_experts": int(U), "slot_copies_rotated": copies,
+            "workload": "MoE decode: x bf16 [16,2816], logits bf16 [16,128], top-8, 128 "
+                        "experts NVFP4 gate/up [704x2816], down [2816x704], y bf16 [16,2816]",
+            "path": "route+plan, grouped GEMV gate/up with GeGLU, grouped GEMV down with "
+                    "deterministic combine (3 launches)"}
+
+
+def time_moe_prefill(steps, warmup):
+    case = synth.moe_prefill_case(seed=0)
+    x, logits, slots = case
+    T, H, E, I = x.shape[0], x.shape[1], logits.shape[1], slots.I
+    flops = 2.0 * T * 8 * 3 * H * I
+    dx, dl, sl, ms, y, ws = moe_setup(case, 1)
+    stream = hip.Stream()
+
+    def step(i):
+        hip.moe_ffn_bf16(dx, dl, ms[0], y, T, E, 8, H, I, ws, stream=stream)
+
+    sec = time_steps(step, steps, warmup, stream)
+    stream.close()
+    tf = flops / sec / 1e12
+    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
+            "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(flops),
+            "workload": "MoE prefill: x bf16 [4096,2816], Zipf(1.1) routing over 128 experts "
+                        "(8 empty), top-8, NVFP4 gate/up [704x2816], down [2816x704], y bf16",
+            "path": "route, plan, grouped MFMA GEMM gate/up with GeGLU epilogue, grouped "
+                    "MFMA GEMM down, weighted combine (5 launches)"}
+
+
+def time_gemm_prefill(steps, warmup, M=2048, N=21504, K=5376):
+    A, w = synth.gemm_case(seed=0, M=M, N=N, K=K)
+    dA = hip.DeviceArray.from_numpy(A)
+    dc, ds = hip.DeviceArray.from_numpy(w.codes), hip.DeviceArray.from_numpy(w.scales)
+    C = hip.DeviceArray((M, N), np.uint16)
+    stream = hip.Stream()
+
+    def step(i):
+        hip.nvfp4_gemm_bf16(dA, dc, ds, C, M, N, K, stream=stream)
+
+    sec = time_steps(step, steps, warmup, stream)
+    stream.close()
+    tf = 2.0 * M * N * K / sec / 1e12
+    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
+            "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(2 * M * N * K),
+            "workload": f"prefill GEMM: A bf16 [{M},{K}] x NVFP4 W [{N}x{K}]^T -> C bf16 [{M},{N}]"}
+
+
+def calibrate():
+    """Known-size kernels for scaling rocprofv3 HBM counters: a 1 GiB streaming read
+    and a 256 MiB device-to-device copy."""
+    big = hip.DeviceArray((1 << 30,), np.uint8)
+    big.fill_bytes(1)
+    sink = hip.DeviceArray((hip.read_probe_sink_words(),), np.uint32)
+    hip.read_probe(big, sink)
+    src = hip.DeviceArray((256 << 20,), np.uint8)
+    dst = hip.DeviceArray((256 << 20,), np.uint8)
+    src.fill_bytes(2)
+    dst.copy_from(src)
+    hip.synchronize()
+    for a in (big, sink, src, dst):
+        a.close()
 
 
 def load_traffic(kernel: str):
@@ -130,12 +267,18 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="time only the headline fused-GeGLU workload")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="run the known-size read and copy kernels first (counter scaling)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
         return 2
 
+    if args.calibrate:
+        calibrate()
     r = time_geglu(args.steps, args.warmup)
     gbs = r["algo_bytes"] / r["per_step_s"] / 1e9
     line = {
@@ -168,6 +311,14 @@ def main(argv=None):
             "traffic": load_traffic("geglu_decode"),
         },
     }
+    if not args.no_secondary:
+        sec_steps = max(1, args.steps // 100)
+        sec_warm = max(1, args.warmup // 100)
+        line["secondary"] = {
+            "moe_prefill": time_moe_prefill(sec_steps, sec_warm),
+            "gemm_prefill": time_gemm_prefill(sec_steps, sec_warm),
+            "moe_decode": time_moe_decode(max(1, args.steps // 10), max(1, args.warmup // 10)),
+        }
     if not args.no_cpu:
         cb = cpu_baseline_geglu(args.cpu_budget)
         cb.pop("_h")
