@@ -6,7 +6,7 @@
 Outputs (git-ignored, shipped with the tree):
     apex_amd/lib/libapex_hip.so    HIP kernels + the C ABI of include/apex_hip.h
     apex_amd/lib/libapex_host.so   C++ apex::HipBackend over that C ABI
-    apex_amd/lib/apex-hip          C++ host self-check CLI (src/main.cpp-style subcommands)
+    tests/host/test_host           C++ checks of the host layer (test infrastructure)
     oracle/liboracle.so            CPU oracle (test infrastructure)
     oracle/_ref/libapexref.so      reference CPU code, only where the reference is mounted
 """
@@ -88,19 +88,24 @@ def build_hip(changed_only: bool = False, jobs: int | None = None) -> Path:
 
 
 def build_host() -> None:
-    """C++ host layer: apex::HipBackend (links only the C ABI) and the self-check CLI."""
-    if not (HOST / "hip_backend.cpp").exists():
-        return
+    """C++ host layer: apex::HipBackend (links only the C ABI)."""
     LIB.mkdir(parents=True, exist_ok=True)
     cxx = os.environ.get("CXX", "g++")
-    rpath = "-Wl,-rpath,$ORIGIN"
     _run([cxx] + CXX_FLAGS + ["-shared", "-o", str(LIB / "libapex_host.so")] +
-         [str(HOST / u) for u in HOST_UNITS] + ["-L", str(LIB), "-lapex_hip", rpath])
-    main = HOST / "main.cpp"
-    if main.exists():
-        _run([cxx] + CXX_FLAGS + ["-o", str(LIB / "apex-hip"), str(main)] +
-             sorted(str(p) for p in (HOST / "tests").glob("*.cpp")) +
-             ["-L", str(LIB), "-lapex_host", "-lapex_hip", rpath])
+         [str(HOST / u) for u in HOST_UNITS] + ["-L", str(LIB), "-lapex_hip",
+                                                "-Wl,-rpath,$ORIGIN"])
+
+
+def build_host_tests() -> None:
+    """tests/host/test_host: the C++ checks of the host layer (links the oracle)."""
+    src = ROOT / "tests" / "host" / "test_host.cpp"
+    if not src.exists():
+        return
+    cxx = os.environ.get("CXX", "g++")
+    _run([cxx] + CXX_FLAGS + ["-I", str(ORACLE), "-o", str(src.with_suffix("")), str(src),
+                              "-L", str(LIB), "-lapex_host", "-lapex_hip", "-L", str(ORACLE),
+                              "-loracle", f"-Wl,-rpath,{LIB}:{ORACLE}",
+                              "-Wl,-rpath,$ORIGIN/../../apex_amd/lib:$ORIGIN/../../oracle"])
 
 
 def build_oracle() -> None:
@@ -119,6 +124,7 @@ def build(changed_only: bool = False) -> None:
     build_oracle()
     build_hip(changed_only)
     build_host()
+    build_host_tests()
 
 
 if __name__ == "__main__":

@@ -1,0 +1,129 @@
+// Kernel-launch helpers over the Backend interface, as src/ops.h provides them for the
+// engine: the reference's NVFP4 ops under their reference names and argument order
+// (matmulNvfp4, geglu, denseMlp: src/ops.h:7-16, 28-69), plus the HIP backend's
+// additional ops -- bf16 activations, the fused GeGLU projection, the MFMA prefill
+// GEMM and the MoE expert FFN.  Every helper only queues work (Backend::run); results
+// are visible after Backend::sync().
+#pragma once
+#include <cstdint>
+
+#include "apex_hip.h"
+#include "backend.h"
+
+namespace apex {
+
+// An NVFP4 matrix [w_rows, hidden_dim] in GPU memory; codes and scales may share one
+// buffer at different offsets (src/ops.h:7-16).
+struct Nvfp4Matrix {
+    Buffer *weights;
+    size_t weights_offset; // uint32 [w_rows, hidden_dim / 8]
+    Buffer *scales;
+    size_t scales_offset;  // uint8  [w_rows, hidden_dim / 16]
+    uint32_t w_rows;
+    uint32_t hidden_dim;
+};
+
+// fp32 [tokens, hidden_dim] -> fp32 [tokens, w_rows] (src/ops.h:34-46): the reference
+// launch shape, rows in groups of 8 and tokens on the grid's y axis.
+inline void matmulNvfp4(Backend &backend, Buffer *input, const Nvfp4Matrix &W, Buffer *output,
+                        uint32_t tokens) {
+    constexpr uint32_t kRowsPerGroup = 8, kThreads = 256;
+    const uint32_t row_groups = (W.w_rows + kRowsPerGroup - 1) / kRowsPerGroup;
+    backend.run("matmul_nvfp4",
+                {Arg::buf(input), Arg::buf(W.weights, W.weights_offset),
+                 Arg::buf(W.scales, W.scales_offset), Arg::buf(output), Arg::val(W.hidden_dim),
+                 Arg::val(W.w_rows)},
+                Dim3{row_groups, tokens}, Dim3{kThreads});
+}
+
+// output[i] = gelu_tanh(gate[i]) * up[i], fp32, in place allowed (src/ops.h:48-55).
+inline void geglu(Backend &backend, Buffer *gate, Buffer *up, Buffer *output, uint32_t count) {
+    constexpr uint32_t kThreads = 256;
+    backend.run("geglu_f32", {Arg::buf(gate), Arg::buf(up), Arg::buf(output), Arg::val(count)},
+                Dim3{(count + kThreads - 1) / kThreads}, Dim3{kThreads});
+}
+
+// GeGLU FFN with fp32 intermediates, four launches (src/ops.h:57-69).
+inline void denseMlp(Backend &backend, Buffer *input, const Nvfp4Matrix &gate_weights,
+                     const Nvfp4Matrix &up_weights, const Nvfp4Matrix &down_weights,
+                     Buffer *gate_tmp, Buffer *up_tmp, Buffer *output, uint32_t tokens) {
+    matmulNvfp4(backend, input, gate_weights, gate_tmp, tokens);
+    matmulNvfp4(backend, input, up_weights, up_tmp, tokens);
+    geglu(backend, gate_tmp, up_tmp, gate_tmp, tokens * gate_weights.w_rows);
+    matmulNvfp4(backend, gate_tmp, down_weights, output, tokens);
+}
+
+// ---- additional ops of the HIP backend ------------------------------------------------
+
+// bf16 [tokens, hidden_dim] -> bf16 [tokens, w_rows], fp32 accumulation.  From 64
+// tokens it runs as the MFMA GEMM, below as the bandwidth-bound GEMV.
+inline void matmulNvfp4Bf16(Backend &backend, Buffer *input, const Nvfp4Matrix &W, Buffer *output,
+                            uint32_t tokens, float tensor_scale = 1.0f) {
+    backend.run("matmul_nvfp4_bf16",
+                {Arg::buf(input), Arg::buf(W.weights, W.weights_offset),
+                 Arg::buf(W.scales, W.scales_offset), Arg::buf(output), Arg::val(W.hidden_dim),
+                 Arg::val(W.w_rows), Arg::val(tokens), Arg::val(tensor_scale)},
+                Dim3{1}, Dim3{256});
+}
+
+// gelu_tanh(gate . x) * (up . x) in one pass over both weight matrices: the gate/up
+// half of denseMlp fused (no fp32 round trip).  x and output are bf16 if `bf16`,
+// else fp32.
+inline void gegluNvfp4(Backend &backend, Buffer *input, const Nvfp4Matrix &gate,
+                       const Nvfp4Matrix &up, Buffer *output, uint32_t tokens, bool bf16,
+                       float gate_scale = 1.0f, float up_scale = 1.0f) {
+    backend.run(bf16 ? "geglu_nvfp4_bf16" : "geglu_nvfp4_f32",
+                {Arg::buf(input), Arg::buf(gate.weights, gate.weights_offset),
+                 Arg::buf(gate.scales, gate.scales_offset), Arg::buf(up.weights, up.weights_offset),
+                 Arg::buf(up.scales, up.scales_offset), Arg::buf(output), Arg::val(gate.hidden_dim),
+                 Arg::val(gate.w_rows), Arg::val(tokens), Arg::val(gate_scale),
+                 Arg::val(up_scale)},
+                Dim3{1}, Dim3{256});
+}
+
+// Prefill GEMM: bf16 A [M, K] x NVFP4 W [N, K]^T -> bf16 C [M, N] on bf16 MFMA.
+inline void gemmNvfp4Bf16(Backend &backend, Buffer *A, const Nvfp4Matrix &W, Buffer *C, uint32_t M,
+                          float tensor_scale = 1.0f) {
+    backend.run("gemm_nvfp4_bf16",
+                {Arg::buf(A), Arg::buf(W.weights, W.weights_offset),
+                 Arg::buf(W.scales, W.scales_offset), Arg::buf(C), Arg::val(M), Arg::val(W.w_rows),
+                 Arg::val(W.hidden_dim), Arg::val(tensor_scale)},
+                Dim3{1}, Dim3{256});
+}
+
+// Dense GeGLU FFN with the fused gate/up projection: two launches instead of four.
+inline void denseMlpFused(Backend &backend, Buffer *input, const Nvfp4Matrix &gate_weights,
+                          const Nvfp4Matrix &up_weights, const Nvfp4Matrix &down_weights,
+                          Buffer *h_tmp, Buffer *output, uint32_t tokens) {
+    gegluNvfp4(backend, input, gate_weights, up_weights, h_tmp, tokens, false);
+    matmulNvfp4(backend, h_tmp, down_weights, output, tokens);
+}
+
+// Expert slots: expert e's six pieces at slots + e * stride + offset
+// (tools/repack.py:180-213 slot format).
+struct ExpertSlots {
+    Buffer *slots;
+    uint32_t stride;
+    uint32_t gate_w, gate_s, up_w, up_s, down_w, down_s;
+};
+
+// Device workspace the MoE op needs for these sizes.
+inline size_t moeWorkspaceBytes(uint32_t tokens, uint32_t experts, uint32_t top_k, uint32_t hidden,
+                                uint32_t inter) {
+    return apex_moe_workspace_bytes(tokens, experts, top_k, hidden, inter);
+}
+
+// MoE expert FFN: router top-k + softmax over bf16 logits [tokens, experts], then
+// y = sum_j w_j * down_e(gelu(gate_e x) * up_e x) for bf16 x, y [tokens, hidden].
+inline void moeFfn(Backend &backend, Buffer *x, Buffer *logits, const ExpertSlots &E, Buffer *y,
+                   Buffer *workspace, uint32_t tokens, uint32_t experts, uint32_t top_k,
+                   uint32_t hidden, uint32_t inter) {
+    backend.run("moe_ffn_nvfp4_bf16",
+                {Arg::buf(x), Arg::buf(logits), Arg::buf(E.slots), Arg::buf(y), Arg::buf(workspace),
+                 Arg::val(tokens), Arg::val(experts), Arg::val(top_k), Arg::val(hidden),
+                 Arg::val(inter), Arg::val(E.stride), Arg::val(E.gate_w), Arg::val(E.gate_s),
+                 Arg::val(E.up_w), Arg::val(E.up_s), Arg::val(E.down_w), Arg::val(E.down_s)},
+                Dim3{1}, Dim3{256});
+}
+
+} // namespace apex

@@ -271,6 +271,8 @@ def main(argv=None):
                     help="time only the headline fused-GeGLU workload")
     ap.add_argument("--calibrate", action="store_true",
                     help="run the known-size read and copy kernels first (counter scaling)")
+    ap.add_argument("--only", choices=["moe_prefill", "gemm_prefill", "moe_decode"],
+                    help="profiling aid: time one secondary workload and print its record only")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -279,6 +281,11 @@ def main(argv=None):
 
     if args.calibrate:
         calibrate()
+    if args.only:
+        fn = {"moe_prefill": time_moe_prefill, "gemm_prefill": time_gemm_prefill,
+              "moe_decode": time_moe_decode}[args.only]
+        print(json.dumps({args.only: fn(args.steps, args.warmup)}), flush=True)
+        return 0
     r = time_geglu(args.steps, args.warmup)
     gbs = r["algo_bytes"] / r["per_step_s"] / 1e9
     line = {

@@ -1,0 +1,286 @@
+// C++ checks of apex::HipBackend and the ops.h helpers against the CPU oracle, in the
+// style of the reference's own harness (src/tests/dense_mlp.cpp: fill buffers through
+// contents(), queue ops, sync(), compare with the CPU result by rel L2).
+//
+//   test_host            run every check on device 0 (needs a GPU)
+//   test_host --no-gpu   checks that need no GPU (constructor error path)
+//
+// Test infrastructure: links the oracle (oracle/liboracle.so).
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "hip_backend.h"
+#include "nvfp4_oracle.h"
+#include "ops.h"
+#include "profiling.h"
+
+using namespace apex;
+
+namespace {
+
+int g_failures = 0;
+
+void report(const std::string &name, bool ok, const std::string &detail = "") {
+    std::printf("%s %s%s%s\n", ok ? "PASS" : "FAIL", name.c_str(), detail.empty() ? "" : ": ",
+                detail.c_str());
+    std::fflush(stdout);
+    if (!ok)
+        ++g_failures;
+}
+
+// splitmix64: the test's own deterministic generator.
+struct Rng {
+    uint64_t s;
+    uint64_t next() {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    float normal() { // Box-Muller
+        const double u1 = ((next() >> 11) + 1.0) / 9007199254740993.0;
+        const double u2 = (next() >> 11) / 9007199254740992.0;
+        return (float)(std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+    }
+};
+
+struct HostMatrix {
+    std::vector<uint32_t> codes;
+    std::vector<uint8_t> scales;
+    uint32_t rows, K;
+};
+
+HostMatrix random_matrix(Rng &rng, uint32_t rows, uint32_t K) {
+    HostMatrix m{std::vector<uint32_t>((size_t)rows * K / 8), std::vector<uint8_t>((size_t)rows * K / 16),
+                 rows, K};
+    for (auto &c : m.codes)
+        c = (uint32_t)rng.next();
+    for (auto &s : m.scales)
+        s = orc_e4m3_from_float(std::fabs(rng.normal()) * 0.05f);
+    return m;
+}
+
+double rel_l2(const float *a, const float *b, size_t n) {
+    double mx, rel;
+    orc_diff(a, b, n, &mx, &rel);
+    return rel;
+}
+
+// Copy host bytes into a fresh backend buffer through contents().
+Buffer *upload(HipBackend &be, const void *src, size_t bytes, const char *cat) {
+    Buffer *b = be.allocate(bytes, cat);
+    std::memcpy(be.contents(b), src, bytes);
+    return b;
+}
+
+// Weights for one matrix in one buffer: codes then scales (as core.bin places them).
+struct DevMatrix {
+    Buffer *buf;
+    Nvfp4Matrix m;
+};
+
+DevMatrix upload_matrix(HipBackend &be, const HostMatrix &h) {
+    const size_t cb = h.codes.size() * 4, sb = h.scales.size();
+    Buffer *b = be.allocate(cb + sb, "core_weights");
+    auto *p = static_cast<uint8_t *>(be.contents(b));
+    std::memcpy(p, h.codes.data(), cb);
+    std::memcpy(p + cb, h.scales.data(), sb);
+    return {b, Nvfp4Matrix{b, 0, b, cb, h.rows, h.K}};
+}
+
+uint16_t to_bf16(float f) { return orc_float_to_bf16(f); }
+float from_bf16(uint16_t b) { return orc_bf16_to_float(b); }
+
+void test_dense_mlp(HipBackend &be) {
+    // src/tests/dense_mlp.cpp:148-182 composition at a small dense shape, fp32 contract.
+    Rng rng{1};
+    const uint32_t H = 512, I = 256, T = 3;
+    HostMatrix g = random_matrix(rng, I, H), u = random_matrix(rng, I, H), d = random_matrix(rng, H, I);
+    std::vector<float> x((size_t)T * H);
+    for (auto &v : x)
+        v = rng.normal();
+    std::vector<float> want((size_t)T * H);
+    orc_dense_mlp(g.codes.data(), g.scales.data(), u.codes.data(), u.scales.data(), d.codes.data(),
+                  d.scales.data(), x.data(), want.data(), T, H, I);
+
+    DevMatrix dg = upload_matrix(be, g), du = upload_matrix(be, u), dd = upload_matrix(be, d);
+    Buffer *in = upload(be, x.data(), x.size() * 4, "scratch");
+    Buffer *gate_tmp = be.allocate((size_t)T * I * 4, "scratch");
+    Buffer *up_tmp = be.allocate((size_t)T * I * 4, "scratch");
+    Buffer *out = be.allocate((size_t)T * H * 4, "scratch");
+    denseMlp(be, in, dg.m, du.m, dd.m, gate_tmp, up_tmp, out, T);
+    be.sync();
+    const double r = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
+    // the reference harness's gate for fp32 outputs (src/tests/dense_mlp.cpp:113)
+    report("denseMlp fp32 (4 launches) vs oracle", r < 1e-5, "rel_l2 " + std::to_string(r));
+
+    // fused gate/up + down
+    Buffer *h_tmp = be.allocate((size_t)T * I * 4, "scratch");
+    Buffer *out2 = be.allocate((size_t)T * H * 4, "scratch");
+    denseMlpFused(be, in, dg.m, du.m, dd.m, h_tmp, out2, T);
+    be.sync();
+    const double r2 = rel_l2(static_cast<float *>(be.contents(out2)), want.data(), want.size());
+    report("denseMlpFused fp32 (2 launches) vs oracle", r2 < 1e-5, "rel_l2 " + std::to_string(r2));
+
+    // re-run after rewriting the input through contents(): the mirror must be uploaded
+    for (auto &v : x)
+        v = -v;
+    std::memcpy(be.contents(in), x.data(), x.size() * 4);
+    denseMlp(be, in, dg.m, du.m, dd.m, gate_tmp, up_tmp, out, T);
+    be.sync();
+    orc_dense_mlp(g.codes.data(), g.scales.data(), u.codes.data(), u.scales.data(), d.codes.data(),
+                  d.scales.data(), x.data(), want.data(), T, H, I);
+    const double r3 = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
+    report("contents() write before run is uploaded", r3 < 1e-5, "rel_l2 " + std::to_string(r3));
+
+    for (Buffer *b : {dg.buf, du.buf, dd.buf, in, gate_tmp, up_tmp, out, h_tmp, out2})
+        be.release(b);
+}
+
+void test_bf16_ops(HipBackend &be) {
+    Rng rng{2};
+    const uint32_t K = 1024, N = 384;
+    HostMatrix w = random_matrix(rng, N, K);
+    DevMatrix dw = upload_matrix(be, w);
+    for (uint32_t T : {1u, 5u, 96u}) { // GEMV below 64 tokens, MFMA GEMM from 64
+        std::vector<uint16_t> xb((size_t)T * K);
+        std::vector<float> xf((size_t)T * K);
+        for (size_t i = 0; i < xb.size(); ++i) {
+            xb[i] = to_bf16(rng.normal());
+            xf[i] = from_bf16(xb[i]);
+        }
+        std::vector<float> want((size_t)T * N);
+        orc_matvec_nvfp4(w.codes.data(), w.scales.data(), xf.data(), want.data(), T, N, K, 1.0f);
+        Buffer *in = upload(be, xb.data(), xb.size() * 2, "scratch");
+        Buffer *out = be.allocate((size_t)T * N * 2, "scratch");
+        matmulNvfp4Bf16(be, in, dw.m, out, T);
+        be.sync();
+        const auto *ob = static_cast<const uint16_t *>(be.contents(out));
+        std::vector<float> got((size_t)T * N);
+        for (size_t i = 0; i < got.size(); ++i)
+            got[i] = from_bf16(ob[i]);
+        const double r = rel_l2(got.data(), want.data(), want.size());
+        report("matmulNvfp4Bf16 T=" + std::to_string(T), r < 1e-2, "rel_l2 " + std::to_string(r));
+        be.release(in);
+        be.release(out);
+    }
+    be.release(dw.buf);
+}
+
+void test_moe(HipBackend &be) {
+    Rng rng{3};
+    const uint32_t T = 5, E = 12, k = 3, H = 256, I = 128;
+    orc_expert_layout L{};
+    L.gate_w = 0;
+    L.gate_s = L.gate_w + (size_t)I * H / 2;
+    L.up_w = L.gate_s + (size_t)I * H / 16;
+    L.up_s = L.up_w + (size_t)I * H / 2;
+    L.down_w = L.up_s + (size_t)I * H / 16;
+    L.down_s = L.down_w + (size_t)H * I / 2;
+    L.slot_stride = (L.down_s + (size_t)H * I / 16 + 16383) / 16384 * 16384;
+    std::vector<uint8_t> slots((size_t)E * L.slot_stride, 0);
+    for (uint32_t e = 0; e < E; ++e) {
+        uint8_t *s = slots.data() + (size_t)e * L.slot_stride;
+        struct P {
+            size_t w, s;
+            uint32_t rows, K;
+        } pieces[3] = {{L.gate_w, L.gate_s, I, H}, {L.up_w, L.up_s, I, H}, {L.down_w, L.down_s, H, I}};
+        for (const P &p : pieces) {
+            HostMatrix m = random_matrix(rng, p.rows, p.K);
+            std::memcpy(s + p.w, m.codes.data(), m.codes.size() * 4);
+            std::memcpy(s + p.s, m.scales.data(), m.scales.size());
+        }
+    }
+    std::vector<uint16_t> xb((size_t)T * H), lb((size_t)T * E);
+    std::vector<float> xf(xb.size()), lf(lb.size());
+    for (size_t i = 0; i < xb.size(); ++i)
+        xf[i] = from_bf16(xb[i] = to_bf16(rng.normal()));
+    for (size_t i = 0; i < lb.size(); ++i)
+        lf[i] = from_bf16(lb[i] = to_bf16(rng.normal()));
+    std::vector<int32_t> ids((size_t)T * k);
+    std::vector<float> w((size_t)T * k), want((size_t)T * H);
+    orc_moe_route(lf.data(), T, E, k, ids.data(), w.data());
+    orc_moe_ffn(slots.data(), &L, xf.data(), ids.data(), w.data(), want.data(), T, k, H, I);
+
+    Buffer *dx = upload(be, xb.data(), xb.size() * 2, "scratch");
+    Buffer *dl = upload(be, lb.data(), lb.size() * 2, "scratch");
+    Buffer *ds = upload(be, slots.data(), slots.size(), "expert_slots");
+    Buffer *dy = be.allocate((size_t)T * H * 2, "scratch");
+    Buffer *ws = be.allocate(moeWorkspaceBytes(T, E, k, H, I), "scratch");
+    ExpertSlots es{ds, (uint32_t)L.slot_stride, (uint32_t)L.gate_w, (uint32_t)L.gate_s, (uint32_t)L.up_w,
+                   (uint32_t)L.up_s, (uint32_t)L.down_w, (uint32_t)L.down_s};
+    moeFfn(be, dx, dl, es, dy, ws, T, E, k, H, I);
+    be.sync();
+    const auto *yb = static_cast<const uint16_t *>(be.contents(dy));
+    std::vector<float> got((size_t)T * H);
+    for (size_t i = 0; i < got.size(); ++i)
+        got[i] = from_bf16(yb[i]);
+    const double r = rel_l2(got.data(), want.data(), want.size());
+    report("moeFfn vs oracle", r < 1e-2, "rel_l2 " + std::to_string(r));
+    for (Buffer *b : {dx, dl, ds, dy, ws})
+        be.release(b);
+}
+
+bool throws(const std::function<void()> &f, const char *needle) {
+    try {
+        f();
+    } catch (const std::runtime_error &e) {
+        return std::strstr(e.what(), needle) != nullptr;
+    }
+    return false;
+}
+
+void test_errors(HipBackend &be) {
+    Buffer *b = be.allocate(4096, "scratch");
+    report("unknown kernel throws",
+           throws([&] { be.run("rms_norm_f32", {Arg::buf(b)}, Dim3{1}, Dim3{256}); },
+                  "cannot find kernel"));
+    report("threadgroup too large throws",
+           throws([&] {
+               uint32_t n = 1;
+               be.run("geglu_f32", {Arg::buf(b), Arg::buf(b), Arg::buf(b), Arg::val(n)}, Dim3{1},
+                      Dim3{2048});
+           },
+                  "threadgroup too large"));
+    report("wrong argument count throws",
+           throws([&] { be.run("geglu_f32", {Arg::buf(b)}, Dim3{1}, Dim3{256}); }, "expected 4"));
+    alignas(16384) static uint8_t page[32768];
+    report("wrapNoCopy rejects a misaligned pointer",
+           throws([&] { be.wrapNoCopy(page + 64, 16384); }, "wrapNoCopy"));
+    Buffer *w = be.wrapNoCopy(page, 16384);
+    report("wrapNoCopy accepts an aligned page", w != nullptr);
+    be.release(w);
+    const uint64_t before = MemoryTracker::get().category("scratch");
+    be.release(b);
+    report("release updates the memory tracker",
+           MemoryTracker::get().category("scratch") == before - 4096);
+}
+
+} // namespace
+
+int main(int argc, char **argv) {
+    const bool no_gpu = argc > 1 && std::strcmp(argv[1], "--no-gpu") == 0;
+    if (no_gpu) {
+        // Without a device, construction fails with the C ABI's message.
+        report("HipBackend without a device throws",
+               throws([] { HipBackend be(0); }, "HipBackend"));
+        return g_failures ? 1 : 0;
+    }
+    HipBackend be(0);
+    std::printf("device: %s\n", be.deviceName());
+    test_dense_mlp(be);
+    test_bf16_ops(be);
+    test_moe(be);
+    test_errors(be);
+    Profile::get().print(stdout);
+    std::printf("%s (%d failure%s)\n", g_failures ? "FAILED" : "OK", g_failures,
+                g_failures == 1 ? "" : "s");
+    return g_failures ? 1 : 0;
+}
