@@ -17,11 +17,15 @@ namespace apex_hip {
 namespace {
 
 using namespace gemm_core;
-constexpr int BM = 256;
+#ifndef APEX_GEMM_WC
+#define APEX_GEMM_WC 4
+#endif
+constexpr int WC = APEX_GEMM_WC;          // wave columns: 4 (1 x 4) or 2 (2 x 2)
+constexpr int MT = WC == 4 ? 8 : 4;       // 32-row MFMA tiles per wave
+constexpr int BM = Layout<MT, WC>::kBM;   // 256
 
 __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int MT = BM / 32;
 
     const uint32_t tiles_m = (a.M + BM - 1) / BM;
     const uint32_t tiles_n = (a.N + BN - 1) / BN;
@@ -42,16 +46,16 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a) {
     auto w_code = [=](int r) { return n0 + r < N ? (n0 + r) * (K / 2) : kOut; };
     auto w_scale = [=](int r) { return n0 + r < N ? (n0 + r) * (K / 16) : kOut; };
 
-    Acc<MT> acc;
-    gemm_tile<MT>(lds, ra, rc, rs, K, a_row, w_code, w_scale, acc);
+    Acc<MT, WC> acc;
+    gemm_tile<MT, WC>(lds, ra, rc, rs, K, a_row, w_code, w_scale, acc);
 
-    store_tile_bf16<MT>(acc, a.C, a.ldc, m0, n0, M, N, a.tensor_scale);
+    store_tile_bf16<MT, WC>(acc, a.C, a.ldc, m0, n0, M, N, a.tensor_scale);
 }
 
 hipError_t launch(const GemmArgs &a, hipStream_t stream) {
     const uint32_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     const uint32_t grid = 8 * ((tiles + 7) / 8);
-    constexpr size_t lds = Layout<BM / 32>::kLds;
+    constexpr size_t lds = Layout<MT, WC>::kLds;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void *)nvfp4_gemm_kernel,

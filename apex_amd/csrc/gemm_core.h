@@ -1,7 +1,7 @@
 // Tile core of the NVFP4 x bf16 MFMA GEMMs (dense prefill GEMM and the grouped MoE
 // expert GEMMs), gfx950.
 //
-// One workgroup of 4 waves computes a (32*MT) x 256 tile of C = A . W^T:
+// One workgroup of 4 waves computes a BM x 256 tile of C = A . W^T (BM = 32*MT*(4/WC)):
 //   A   bf16 rows (activations), K contiguous, 2*K bytes per row;
 //   W   NVFP4 rows (codes: K/2 bytes, E4M3 scales: K/16 bytes per row);
 //   C   fp32 accumulators, handed to the caller's epilogue.
@@ -17,8 +17,10 @@
 // v_mfma_f32_32x32x16_bf16 (measured: sustains ~90% of the bf16 peak with one wave per
 // SIMD; 16x16x32 only ~55%).
 //
-//  * 1 x 4 waves: wave w owns all 32*MT rows and W columns [64w, 64w+64) as MT x 2
-//    MFMA tiles, so every W element is dequantised exactly once per tile.
+//  * (4/WC) x WC waves: wave w owns rows [32 MT (w / WC), +32 MT) and columns
+//    [32 NT (w % WC), +32 NT) (NT = 8 / WC) as MT x NT MFMA tiles.  WC = 4 (1 x 4)
+//    dequantises every W element once per tile; WC = 2 (2 x 2) halves the A-fragment
+//    LDS reads per MFMA and dequantises each W element twice.
 //  * A streams HBM/L2 -> LDS with buffer_load ... lds (no VGPR round trip) through a
 //    ring of kStages stage buffers, kStages-1 stages ahead of the MFMAs.  A rows are
 //    128 bytes per stage with 16-byte pieces XOR-swizzled by (row / 2) % 8, so the 32
@@ -51,8 +53,11 @@ constexpr int kWCode = BN * (BK / 2);      // 8 KiB of W codes per stage
 constexpr int kWScale = BN * (BK / 16);    // 1 KiB of W scales per stage
 constexpr uint32_t kOut = 0x80000000u;     // an offset no descriptor covers
 
-template <int MT> struct Layout {
-    static constexpr int kAStage = MT * 32 * kARow;
+template <int MT, int WC = 4> struct Layout {
+    static constexpr int kWR = 4 / WC;
+    static constexpr int kNT = 8 / WC;
+    static constexpr int kBM = 32 * MT * kWR;
+    static constexpr int kAStage = kBM * kARow;
     static constexpr int kStage = kAStage + kWCode + kWScale;
     static constexpr size_t kLds = (size_t)kStages * kStage;
 };
@@ -68,34 +73,46 @@ __device__ __forceinline__ uint32_t pack_bf16_hi(float lo, float hi) {
 }
 
 // Accumulator element e of MFMA tile (i, j) of wave `wave`, lane `lane` sits at tile
-// row 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4 and tile column 64 wave + 32 j + lane % 32.
-template <int MT> using Acc = f32x16_t[MT][2];
+// row 32 MT (wave / WC) + 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4 and tile column
+// 32 NT (wave % WC) + 32 j + lane % 32.
+template <int MT, int WC = 4> using Acc = f32x16_t[MT][8 / WC];
 
-template <int MT, typename ARow, typename WCode, typename WScale>
+template <int MT, int WC> __device__ __forceinline__ int wave_row0() {
+    return 32 * MT * ((threadIdx.x >> 6) / WC);
+}
+template <int WC> __device__ __forceinline__ int wave_col0() {
+    return 32 * (8 / WC) * ((threadIdx.x >> 6) % WC);
+}
+
+template <int MT, int WC, typename ARow, typename WCode, typename WScale>
 __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t ra,
                                           __amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rs,
                                           uint32_t K, ARow a_row, WCode w_code, WScale w_scale,
-                                          Acc<MT> &acc) {
-    constexpr int NT = 2;
-    constexpr int kAStage = Layout<MT>::kAStage;
-    constexpr int kStage = Layout<MT>::kStage;
-    constexpr int kALoads = MT;               // DMA loads of 8 A rows per wave per stage
+                                          Acc<MT, WC> &acc) {
+    constexpr int NT = 8 / WC;
+    constexpr int WR = 4 / WC;
+    constexpr int kAStage = Layout<MT, WC>::kAStage;
+    constexpr int kStage = Layout<MT, WC>::kStage;
+    constexpr int kARows = 8 * MT * WR;       // A rows each wave copies per stage
+    constexpr int kALoads = MT * WR;          // DMA loads of 8 A rows per wave per stage
     constexpr int kLoadsPerStage = kALoads + 2 + 1;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wn = wave * 64;       // wave's column offset in the tile
+    // uniform: LDS destinations (M0) and their arithmetic stay in scalar registers
+    const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
+    const int wn = wave_col0<WC>();      // wave's column offset in the tile
+    const int wm = wave_row0<MT, WC>();  // wave's row offset in the tile
     const int frow = lane & 31;     // fragment row (A) / column (B) within a 32-wide tile
     const int h = lane >> 5;        // lane half: k pieces 4h .. 4h+3 of each stage
 
-    // A: wave w copies rows [8 MT w, 8 MT (w+1)) with MT DMA loads of 8 rows; lane l
+    // A: wave w copies rows [kARows w, kARows (w+1)) with DMA loads of 8 rows; lane l
     // lands at row 8i + l/8, physical piece l%8, so it fetches logical piece
     // (l%8) ^ ((row/2)%8) of that row.
     uint32_t a_off[kALoads];
 #pragma unroll
     for (int i = 0; i < kALoads; ++i) {
-        const int trow = wave * 8 * MT + 8 * i + (lane >> 3);
+        const int trow = wave * kARows + 8 * i + (lane >> 3);
         const uint32_t ro = a_row(trow);
         a_off[i] = ro == kOut ? kOut : ro + (((lane & 7) ^ ((trow >> 1) & 7)) * 16);
     }
@@ -114,21 +131,24 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     }
     const uint32_t ws_off = w_scale(wave * 64 + lane);
 
+    // The stage's K position rides in the scalar offset: the per-lane offsets are fixed
+    // for the whole tile (a valid row plus k0 stays inside its row; an out-of-range
+    // lane offset stays out of range).
     auto load_stage = [&](int buf, uint32_t k0) {
         uint8_t *base = lds + buf * kStage;
 #pragma unroll
         for (int i = 0; i < kALoads; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra, (lds_void_t *)(base + (wave * 8 * MT + 8 * i) * kARow), 16, a_off[i] + k0 * 2,
-                0, 0, 0);
+                ra, (lds_void_t *)(base + (wave * kARows + 8 * i) * kARow), 16, a_off[i],
+                (int)(k0 * 2), 0, 0);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rc, (lds_void_t *)(base + kAStage + (wave * 128 + i * 64) * 16), 16,
-                wc_off[i] + k0 / 2, 0, 0, APEX_WEIGHT_CPOL);
+                rc, (lds_void_t *)(base + kAStage + (wave * 128 + i * 64) * 16), 16, wc_off[i],
+                (int)(k0 / 2), 0, APEX_WEIGHT_CPOL);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (lds_void_t *)(base + kAStage + kWCode + wave * 64 * 4), 4, ws_off + k0 / 16, 0, 0,
-            APEX_WEIGHT_CPOL);
+            rs, (lds_void_t *)(base + kAStage + kWCode + wave * 64 * 4), 4, ws_off, (int)(k0 / 16),
+            0, APEX_WEIGHT_CPOL);
     };
 
 #pragma unroll
@@ -164,7 +184,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         const int piece = 4 * h + q;
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
-            const int r = i * 32 + frow;
+            const int r = wm + i * 32 + frow;
             dst[i] = *reinterpret_cast<const bf16x8_v *>(la + r * kARow + ((piece ^ ((r >> 1) & 7)) * 16));
         }
     };
@@ -251,19 +271,20 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
 // elements): tile row r, column c go to C[(m0 + r) * ldc + n0 + c] for m0 + r < M and
 // n0 + c < N.  Branch-free: the stores go through a buffer descriptor that ends at row
 // M (the hardware drops stores past it) and columns past N get an out-of-range offset.
-template <int MT>
-__device__ __forceinline__ void store_tile_bf16(const Acc<MT> &acc, uint16_t *C, uint32_t ldc,
+template <int MT, int WC>
+__device__ __forceinline__ void store_tile_bf16(const Acc<MT, WC> &acc, uint16_t *C, uint32_t ldc,
                                                 uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
                                                 float scale) {
+    constexpr int NT = 8 / WC;
     const int lane = threadIdx.x & 63;
-    const uint32_t cn = 64 * (threadIdx.x >> 6) + (lane & 31); // column within the tile
-    const uint32_t cm = 4 * (lane >> 5);                       // row within the tile
+    const uint32_t cn = wave_col0<WC>() + (lane & 31);          // column within the tile
+    const uint32_t cm = wave_row0<MT, WC>() + 4 * (lane >> 5);  // row within the tile
     const uint64_t rows = M - m0;
     const uint64_t bytes = rows * ldc * 2;
     const __amdgpu_buffer_rsrc_t rc =
         make_rsrc(C + (size_t)m0 * ldc + n0, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NT; ++j) {
         const bool col_ok = n0 + cn + 32 * j < N;
 #pragma unroll
         for (int i = 0; i < MT; ++i)

@@ -178,6 +178,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *logits, 
 // tiles first.  Counts, offsets and tile slots come from exclusive scans over the
 // experts, so every expert's entries are written in parallel.
 constexpr int kPlanScans = 5; // pair counts, active flags, class 0/1/2 tile counts
+constexpr int kPlanBatch = 8; // pairs per thread whose loads are issued together
 
 __device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
     __shared__ int cnt[kMoeMaxExperts], cur[kMoeMaxExperts];
@@ -188,8 +189,20 @@ __device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
     if (tid < (int)kMoeMaxExperts)
         cnt[tid] = 0;
     __syncthreads();
-    for (uint32_t p = tid; p < P; p += blockDim.x)
-        atomicAdd(&cnt[ids[p]], 1);
+    // Pairs in batches of kPlanBatch per thread: the batch's loads are all in flight
+    // before its atomics (a load -> atomic -> store chain per pair is latency-bound).
+    for (uint32_t p0 = 0; p0 < P; p0 += blockDim.x * kPlanBatch) {
+        int e[kPlanBatch];
+#pragma unroll
+        for (int b = 0; b < kPlanBatch; ++b) {
+            const uint32_t p = p0 + b * blockDim.x + tid;
+            e[b] = p < P ? ids[p] : -1;
+        }
+#pragma unroll
+        for (int b = 0; b < kPlanBatch; ++b)
+            if (e[b] >= 0)
+                atomicAdd(&cnt[e[b]], 1);
+    }
     __syncthreads();
     // inclusive Hillis-Steele scans over the 256 expert slots (experts >= E count 0)
     int val[kPlanScans] = {};
@@ -256,10 +269,24 @@ __device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
         v.hdr[2] = n0;
     }
     __syncthreads();
-    for (uint32_t p = tid; p < P; p += blockDim.x) {
-        const int pos = atomicAdd(&cur[ids[p]], 1);
-        v.pos_of_pair[p] = pos;
-        v.pair_of_pos[pos] = (int32_t)p;
+    for (uint32_t p0 = 0; p0 < P; p0 += blockDim.x * kPlanBatch) {
+        int e[kPlanBatch], pos[kPlanBatch];
+#pragma unroll
+        for (int b = 0; b < kPlanBatch; ++b) {
+            const uint32_t p = p0 + b * blockDim.x + tid;
+            e[b] = p < P ? ids[p] : -1;
+        }
+#pragma unroll
+        for (int b = 0; b < kPlanBatch; ++b)
+            pos[b] = e[b] >= 0 ? atomicAdd(&cur[e[b]], 1) : 0;
+#pragma unroll
+        for (int b = 0; b < kPlanBatch; ++b) {
+            const uint32_t p = p0 + b * blockDim.x + tid;
+            if (e[b] >= 0) {
+                v.pos_of_pair[p] = pos[b];
+                v.pair_of_pos[pos[b]] = (int32_t)p;
+            }
+        }
     }
 }
 
@@ -510,8 +537,8 @@ __device__ __forceinline__ void gateup_tile(const MoeArgs &a, uint8_t *lds, cons
         const uint32_t col = c0 + 32 * (r / 64) + r % 32;
         return col < I ? ((r & 32) ? us : gs) + col * (H / 16) : kOut;
     };
-    Acc<MT> acc;
-    gemm_tile<MT>(lds, ra, rw, rw, H, a_row, w_code, w_scale, acc);
+    Acc<MT, 4> acc;
+    gemm_tile<MT, 4>(lds, ra, rw, rw, H, a_row, w_code, w_scale, acc);
     // h[row0 + r][col] = gelu(gate) * up, branch-free: the store descriptor ends at
     // row nrows, columns past I get an out-of-range offset.
     const int lane = threadIdx.x & 63;
@@ -529,12 +556,25 @@ __device__ __forceinline__ void gateup_tile(const MoeArgs &a, uint8_t *lds, cons
         }
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b on XCD b % 8).
+// Workgroup b takes n-tile s % nn of m-tile 8 (s / nn) + b % 8, s = b / 8: each XCD
+// walks all n-tiles of one m-tile in turn, so the m-tile's A rows (gathered token rows
+// or h rows) are fetched into that XCD's L2 once, and consecutive m-tiles -- big ones
+// first -- are dealt to the XCDs in turn.  The grid is a multiple of 8 * nn and covers
+// the largest possible m-tile count; workgroups past the device's count exit at once.
+__device__ __forceinline__ void xcd_tile(uint32_t nn, uint32_t &mt, uint32_t &nt) {
+    const uint32_t s = blockIdx.x / 8;
+    mt = 8 * (s / nn) + blockIdx.x % 8;
+    nt = s % nn;
+}
+
 __global__ __launch_bounds__(kThreads) void moe_gateup_gemm_kernel(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t E = a.E, P = a.T * a.k;
     const PlanView v = plan_view(a.plan, E, P);
     const uint32_t nn = (a.I + kGateUpCols - 1) / kGateUpCols;
-    const uint32_t mt = blockIdx.x / nn, nt = blockIdx.x % nn;
+    uint32_t mt, nt;
+    xcd_tile(nn, mt, nt);
     if (mt >= uniform(v.hdr[1]))
         return;
     const int32_t *t = v.tiles + 4 * mt;
@@ -559,9 +599,9 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
     auto a_row = [=](int r) { return (uint32_t)r < nrows ? (row0 + r) * I * 2 : kOut; };
     auto w_code = [=](int r) { return n0 + r < H ? dw + (n0 + r) * (I / 2) : kOut; };
     auto w_scale = [=](int r) { return n0 + r < H ? ds + (n0 + r) * (I / 16) : kOut; };
-    Acc<MT> acc;
-    gemm_tile<MT>(lds, ra, rw, rw, I, a_row, w_code, w_scale, acc);
-    store_tile_bf16<MT>(acc, a.d + (size_t)row0 * H, H, 0, n0, nrows, H, 1.0f);
+    Acc<MT, 4> acc;
+    gemm_tile<MT, 4>(lds, ra, rw, rw, I, a_row, w_code, w_scale, acc);
+    store_tile_bf16<MT, 4>(acc, a.d + (size_t)row0 * H, H, 0, n0, nrows, H, 1.0f);
 }
 
 __global__ __launch_bounds__(kThreads) void moe_down_gemm_kernel(MoeArgs a) {
@@ -569,7 +609,8 @@ __global__ __launch_bounds__(kThreads) void moe_down_gemm_kernel(MoeArgs a) {
     const uint32_t E = a.E, P = a.T * a.k;
     const PlanView v = plan_view(a.plan, E, P);
     const uint32_t nn = (a.H + BN - 1) / BN;
-    const uint32_t mt = blockIdx.x / nn, nt = blockIdx.x % nn;
+    uint32_t mt, nt;
+    xcd_tile(nn, mt, nt);
     if (mt >= uniform(v.hdr[1]))
         return;
     const int32_t *t = v.tiles + 4 * mt;
@@ -753,12 +794,12 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     hipLaunchKernelGGL(moe_route_kernel, dim3((a.T + 3) / 4), dim3(256), 0, stream, a.logits, a.T,
                        a.E, a.k, a.ids, a.w);
     hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, stream, a);
+    const uint32_t mt8 = 8 * ((a.max_tiles + 7) / 8); // m-tiles rounded to whole XCD turns
     const uint32_t nn_gu = (a.I + kGateUpCols - 1) / kGateUpCols;
-    hipLaunchKernelGGL(moe_gateup_gemm_kernel, dim3(a.max_tiles * nn_gu), dim3(kThreads), kMaxLds,
-                       stream, a);
+    hipLaunchKernelGGL(moe_gateup_gemm_kernel, dim3(mt8 * nn_gu), dim3(kThreads), kMaxLds, stream,
+                       a);
     const uint32_t nn_d = (a.H + BN - 1) / BN;
-    hipLaunchKernelGGL(moe_down_gemm_kernel, dim3(a.max_tiles * nn_d), dim3(kThreads), kMaxLds,
-                       stream, a);
+    hipLaunchKernelGGL(moe_down_gemm_kernel, dim3(mt8 * nn_d), dim3(kThreads), kMaxLds, stream, a);
     hipLaunchKernelGGL(moe_combine_kernel, dim3(a.T, (a.H + kCombineCols - 1) / kCombineCols),
                        dim3(256), 0, stream, a);
     return hipGetLastError();

@@ -87,10 +87,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     return (uint16_t)(__builtin_isnan(f) ? quiet : rounded);
 }
 
-// GeLU, tanh approximation, fp32 constants of shaders/geglu.metal:15-16.
+// GeLU, tanh approximation, fp32 constants of shaders/geglu.metal:15-16:
+// 0.5 g (1 + tanh(u)), u = 0.7978845608028654 (g + 0.044715 g^3), evaluated through the
+// identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)) -- one exponential and one division
+// instead of a tanh.  exp overflowing to +inf gives g / inf = -0 (the limit).
 __device__ __forceinline__ float gelu_tanh(float g) {
-    const float t = tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g));
-    return 0.5f * g * (1.0f + t);
+    const float u = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    return g / (1.0f + __expf(-2.0f * u));
 }
 
 // Sum over aligned groups of G lanes (G in {8, 16, 32, 64}) of a wave64; every lane
