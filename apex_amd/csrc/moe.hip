@@ -377,7 +377,11 @@ __device__ __forceinline__ void rows_dot(float (&out)[NR], const RowRegs<SLOTS> 
 // a wave's 16-byte reads of one piece of consecutive chunks are conflict-free) and
 // read from there; otherwise each token's row is loaded from global memory (L2).
 constexpr int kGemvBlocksPerCU = 4; // 256-thread workgroups per CU (global x)
-constexpr int kXLdsThreads = 768;   // one workgroup per CU (x in LDS): 3 waves per SIMD
+// x in LDS: one workgroup of 16 waves per CU.  Measured on the 16-token decode step:
+// 16 waves without a prefetch register set beat 12 waves with one (the set costs ~30
+// VGPRs); kXLdsPrefetch keeps the double-buffered variant available.
+constexpr int kXLdsThreads = 1024;
+constexpr bool kXLdsPrefetch = false;
 constexpr uint32_t kXLdsBytes = 120 * 1024;
 
 template <bool GATE_UP, int G, int SLOTS, int NB, bool XLDS>
@@ -388,7 +392,7 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     // per-unit lookups are LDS reads that never wait behind the weight stream.
     __shared__ int s_act[kMoeMaxExperts], s_cnt[kMoeMaxExperts], s_off[kMoeMaxExperts];
     __shared__ uint32_t s_xrow[kMoeGemvMaxPairs]; // activation row of pos (token or pos)
-    extern __shared__ uint4 xl[];                 // XLDS: [T][4 pieces][nchunks]
+    extern __shared__ uint4 xl[];                 // XLDS: [T][4 pieces][nchunks + 1]
     const int lane = threadIdx.x & 63;
     const int sub = lane / G, gl = lane % G;
     const uint32_t E = a.E, P = a.T * a.k, H = a.H, I = a.I;
@@ -405,13 +409,16 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     for (uint32_t i = threadIdx.x; i < P; i += blockDim.x)
         s_xrow[i] = GATE_UP ? (uint32_t)v.pair_of_pos[i] / a.k : i;
     if constexpr (XLDS) {
-        // entry (t, piece q, chunk c) = bytes [64 c + 16 q, +16) of row t
-        const uint32_t n = a.T * 4 * nchunks;
+        // entry (t, piece q, chunk c) = bytes [64 c + 16 q, +16) of row t; chunk nchunks
+        // of every (t, q) plane is zero (its load lies past the descriptor), so lanes past
+        // the end of a row read zeros without a branch
+        const uint32_t nc = nchunks + 1;
+        const uint32_t n = a.T * 4 * nc;
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-            const uint32_t t = i / (4 * nchunks), rem = i % (4 * nchunks);
+            const uint32_t t = i / (4 * nc), rem = i % (4 * nc);
             const uint32_t c = rem / 4, q = rem % 4;
-            xl[(t * 4 + q) * nchunks + c] =
-                __builtin_bit_cast(uint4, load_b128(rx, t * K * 2 + c * 64 + q * 16));
+            const uint32_t off = (int)c < nchunks ? t * K * 2 + c * 64 + q * 16 : kOutOfRange;
+            xl[(t * 4 + q) * nc + c] = __builtin_bit_cast(uint4, load_b128(rx, off));
         }
     }
     const uint32_t U = uniform(v.hdr[0]);
@@ -457,12 +464,12 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
             float dots[NM * NB];
             if constexpr (XLDS) {
                 rows_dot<G, SLOTS, NM * NB, true>(dots, w, [&](int s) {
-                    const int c = gl + s * G;
+                    const int c = min(gl + s * G, nchunks); // chunk nchunks is zero
+                    const uint4 *plane = xl + xr * 4 * (nchunks + 1) + c;
                     XChunk<uint16_t> xc;
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
-                        xc.p[q] = c < nchunks ? __builtin_bit_cast(u32x4_t, xl[(xr * 4 + q) * nchunks + c])
-                                              : u32x4_t{0, 0, 0, 0};
+                        xc.p[q] = __builtin_bit_cast(u32x4_t, plane[q * (nchunks + 1)]);
                     return xc;
                 });
             } else {
@@ -486,7 +493,7 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     };
 
     const uint32_t u0 = blockIdx.x * waves_per_block + wave;
-    if constexpr (XLDS) {
+    if constexpr (XLDS && kXLdsPrefetch) {
         // Activations come from LDS, so the next unit's weight loads can be in flight
         // while this unit computes (two register sets, body unrolled twice so the
         // buffer indices are constants).
@@ -750,8 +757,8 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
         hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(1024), 0, stream, a);
         const dim3 grid((uint32_t)kNumCUs * kGemvBlocksPerCU), block(256);
         // gate/up: 32 lanes per row; x staged in LDS when it fits (one workgroup per
-        // CU, next unit's weights prefetched), else read per token from global memory
-        const uint32_t xbytes = a.T * (a.H / 32) * 64;
+        // CU), else read per token from global memory
+        const uint32_t xbytes = a.T * (a.H / 32 + 1) * 64;
         if (xbytes <= kXLdsBytes) {
             static bool attr[3] = {};
             const dim3 lgrid((uint32_t)kNumCUs), lblock(kXLdsThreads);

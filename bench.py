@@ -231,10 +231,40 @@ def time_gemm_prefill(steps, warmup, M=2048, N=21504, K=5376):
 
     sec = time_steps(step, steps, warmup, stream)
     stream.close()
+    for a in (dA, dc, ds, C):
+        a.close()
     tf = 2.0 * M * N * K / sec / 1e12
     return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
             "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(2 * M * N * K),
-            "workload": f"prefill GEMM: A bf16 [{M},{K}] x NVFP4 W [{N}x{K}]^T -> C bf16 [{M},{N}]"}
+            "workload": f"prefill GEMM: A bf16 [{M},{K}] x NVFP4 W [{N}x{K}]^T -> C bf16 [{M},{N}]",
+            "yardstick_vendor_bf16_gemm_tflops": vendor_bf16_gemm(M, N, K, steps, warmup)}
+
+
+def vendor_bf16_gemm(M, N, K, steps, warmup):
+    """Context for the GEMM line: the vendor library's plain bf16 GEMM of the same shape
+    (torch -> hipBLASLt, weights already bf16, no FP4 decode).  Not part of the path."""
+    try:
+        import torch
+        if not torch.cuda.is_available():
+            return None
+        a = torch.randn(M, K, device="cuda", dtype=torch.bfloat16)
+        w = torch.randn(N, K, device="cuda", dtype=torch.bfloat16)
+        for _ in range(warmup):
+            torch.nn.functional.linear(a, w)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            torch.nn.functional.linear(a, w)
+        e1.record()
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) / 1e3 / steps
+        del a, w
+        torch.cuda.empty_cache()
+        return round(2.0 * M * N * K / sec / 1e12, 2)
+    except Exception:  # torch absent or without a GPU: no yardstick
+        return None
 
 
 def calibrate():
