@@ -24,6 +24,11 @@ constexpr int WC = APEX_GEMM_WC;          // wave columns: 4 (1 x 4) or 2 (2 x 2
 constexpr int MT = WC == 4 ? 8 : 4;       // 32-row MFMA tiles per wave
 constexpr int BM = Layout<MT, WC>::kBM;   // 256
 
+// 16-byte epilogue stores need 8-column row pieces at 16-byte aligned addresses.
+__device__ __forceinline__ bool uniform_wide(const GemmArgs &a) {
+    return a.N % 8 == 0 && a.ldc % 8 == 0 && ((uintptr_t)a.C & 15) == 0;
+}
+
 __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -49,7 +54,7 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a) {
     Acc<MT, WC> acc;
     gemm_tile<MT, WC>(lds, ra, rc, rs, K, a_row, w_code, w_scale, acc);
 
-    store_tile_bf16<MT, WC>(acc, a.C, a.ldc, m0, n0, M, N, a.tensor_scale);
+    store_tile_bf16<MT, WC>(acc, a.C, a.ldc, m0, n0, M, N, a.tensor_scale, uniform_wide(a));
 }
 
 hipError_t launch(const GemmArgs &a, hipStream_t stream) {

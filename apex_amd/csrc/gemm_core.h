@@ -52,6 +52,12 @@ constexpr int kStages = 3;                 // ring depth
 constexpr int kWCode = BN * (BK / 2);      // 8 KiB of W codes per stage
 constexpr int kWScale = BN * (BK / 16);    // 1 KiB of W scales per stage
 constexpr uint32_t kOut = 0x80000000u;     // an offset no descriptor covers
+// W loads use the default cache policy: a stage takes 32 bytes of each 128-byte code
+// line and 4 bytes of each scale line, so a line serves 4 (codes) or 32 (scales)
+// consecutive stages and must stay in L2 between them.
+#ifndef APEX_GEMM_W_CPOL
+#define APEX_GEMM_W_CPOL 0
+#endif
 
 template <int MT, int WC = 4> struct Layout {
     static constexpr int kWR = 4 / WC;
@@ -72,10 +78,41 @@ __device__ __forceinline__ uint32_t pack_bf16_hi(float lo, float hi) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-// Accumulator element e of MFMA tile (i, j) of wave `wave`, lane `lane` sits at tile
-// row 32 MT (wave / WC) + 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4 and tile column
-// 32 NT (wave % WC) + 32 j + lane % 32.
+// The MFMAs take W as their first operand and A as their second, so each 32 x 32
+// accumulator holds a block of C^T: element e of MFMA tile (i, j) of wave `wave`, lane
+// `lane` sits at tile row 32 MT (wave / WC) + 32 i + lane % 32 and tile column
+// 32 NT (wave % WC) + 32 j + 8 (e / 4) + 4 (lane / 32) + e % 4 -- a lane holds runs of
+// 4 consecutive columns of one row, which the epilogues pack into 16-byte stores.
 template <int MT, int WC = 4> using Acc = f32x16_t[MT][8 / WC];
+
+// bf16 output of one accumulator block: `v` (the lane's 16 values, already through any
+// elementwise epilogue) -> two 16-byte pieces, piece p = columns 16 p + 8 (lane / 32)
+// + 0..7 of the lane's row (lane % 32).  The lane halves hold columns 8 g + 0..3 and
+// 8 g + 4..7 of group g; one v_permlane32_swap per register pair hands group 2p+1's
+// lower half to the upper lanes and group 2p's upper half to the lower lanes.
+// Rounding: v_cvt_pk_bf16_f32, round to nearest even.
+__device__ __forceinline__ void pack_bf16_cols(const f32x16_t &v, u32x4_t (&out)[2]) {
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    typedef float f32x2_v __attribute__((ext_vector_type(2)));
+    uint32_t pk[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+            pk[g][q] = __builtin_bit_cast(
+                uint32_t, __builtin_convertvector(f32x2_v{v[4 * g + 2 * q], v[4 * g + 2 * q + 1]},
+                                                  bf16x2_v));
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const auto r = __builtin_amdgcn_permlane32_swap(pk[2 * p][q], pk[2 * p + 1][q], false, false);
+            pk[2 * p][q] = r[0];
+            pk[2 * p + 1][q] = r[1];
+        }
+        out[p] = u32x4_t{pk[2 * p][0], pk[2 * p][1], pk[2 * p + 1][0], pk[2 * p + 1][1]};
+    }
+}
 
 template <int MT, int WC> __device__ __forceinline__ int wave_row0() {
     return 32 * MT * ((threadIdx.x >> 6) / WC);
@@ -97,7 +134,10 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     constexpr int kALoads = MT * WR;          // DMA loads of 8 A rows per wave per stage
     constexpr int kLoadsPerStage = kALoads + 2 + 1;
 
-    const int tid = threadIdx.x;
+    // Opaque per call: values derived from the thread index are recomputed for every
+    // tile instead of being hoisted out of a caller's tile loop into live registers.
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
     // uniform: LDS destinations (M0) and their arithmetic stay in scalar registers
     const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
@@ -145,10 +185,10 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         for (int i = 0; i < 2; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rc, (lds_void_t *)(base + kAStage + (wave * 128 + i * 64) * 16), 16, wc_off[i],
-                (int)(k0 / 2), 0, APEX_WEIGHT_CPOL);
+                (int)(k0 / 2), 0, APEX_GEMM_W_CPOL);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (lds_void_t *)(base + kAStage + kWCode + wave * 64 * 4), 4, ws_off, (int)(k0 / 16),
-            0, APEX_WEIGHT_CPOL);
+            0, APEX_GEMM_W_CPOL);
     };
 
 #pragma unroll
@@ -207,7 +247,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int i = 0; i < MT; ++i)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[i], B[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(B[j], A[i], acc[i][j], 0, 0, 0);
     };
     // One MFMA, then up to two VALU ops and one LDS read, for the MT*NT MFMAs of a step.
     auto interleave = [&]() {
@@ -271,31 +311,53 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
 // elements): tile row r, column c go to C[(m0 + r) * ldc + n0 + c] for m0 + r < M and
 // n0 + c < N.  Branch-free: the stores go through a buffer descriptor that ends at row
 // M (the hardware drops stores past it) and columns past N get an out-of-range offset.
+// `wide` (N and ldc multiples of 8, C 16-byte aligned): 16-byte stores of 8 columns;
+// otherwise one 2-byte store per element.
 template <int MT, int WC>
 __device__ __forceinline__ void store_tile_bf16(const Acc<MT, WC> &acc, uint16_t *C, uint32_t ldc,
                                                 uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
-                                                float scale) {
+                                                float scale, bool wide) {
     constexpr int NT = 8 / WC;
-    const int lane = threadIdx.x & 63;
-    const uint32_t cn = wave_col0<WC>() + (lane & 31);          // column within the tile
-    const uint32_t cm = wave_row0<MT, WC>() + 4 * (lane >> 5);  // row within the tile
+    // opaque per call (see gemm_tile): no store offsets hoisted out of a tile loop
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
+    const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
+    const uint32_t cm = 32 * MT * (wave / WC) + (lane & 31);             // row within the tile
+    const uint32_t cn = 32 * (8 / WC) * (wave % WC) + 8 * (lane >> 5);   // column within the tile
     const uint64_t rows = M - m0;
     const uint64_t bytes = rows * ldc * 2;
     const __amdgpu_buffer_rsrc_t rc =
         make_rsrc(C + (size_t)m0 * ldc + n0, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const bool col_ok = n0 + cn + 32 * j < N;
+    if (wide) {
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                u32x4_t o[2];
+                pack_bf16_cols(acc[i][j] * scale, o);
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const uint32_t c = cn + 32 * j + 16 * p;
+                    const uint32_t off = n0 + c < N ? ((cm + 32 * i) * ldc + c) * 2 : kOut;
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, o[p]), rc,
+                                                           (int)off, 0, 0);
+                }
+            }
+        return;
+    }
+    const uint32_t cq = 32 * (8 / WC) * (wave % WC) + 4 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const uint32_t r = cm + 32 * i + 8 * (e >> 2) + (e & 3);
-                const uint32_t off = col_ok ? (r * ldc + cn + 32 * j) * 2 : kOut;
+                const uint32_t c = cq + 32 * j + 8 * (e >> 2) + (e & 3);
+                const uint32_t off = n0 + c < N ? ((cm + 32 * i) * ldc + c) * 2 : kOut;
                 __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(acc[i][j][e] * scale), rc,
                                                       (int)off, 0, 0);
             }
-    }
 }
 
 } // namespace gemm_core
