@@ -32,7 +32,9 @@
 //   gate/up  each 256-wide W tile holds 128 gate rows and the same 128 up rows, placed
 //            so that a lane's two accumulator sets are gate and up of one h column:
 //            GeGLU epilogue in registers -> h[pos] (bf16).
-//   down     h rows are contiguous per expert -> d[pos] (bf16).
+//   down     h rows are contiguous per expert -> d[pos] (bf16); 128-row tiles, two
+//            workgroups per CU, so one's prologue and epilogue hide under the other's
+//            MFMAs (K = I is short).
 //   combine  y[t] = sum_j w[t,j] d[pos(t,j)] in slot order j, fp32 -> bf16: a fixed
 //            summation order, no float atomics, so results are deterministic.
 #include <type_traits>
@@ -560,7 +562,7 @@ __device__ __forceinline__ void gateup_tile(const MoeArgs &a, uint8_t *lds, cons
         f32x16_t v;
 #pragma unroll
         for (int q = 0; q < 16; ++q)
-            v[q] = gelu_tanh(acc[i][0][q]) * acc[i][1][q];
+            v[q] = gelu_tanh_fast(acc[i][0][q]) * acc[i][1][q];
         u32x4_t o[2];
         pack_bf16_cols(v, o);
 #pragma unroll
@@ -620,21 +622,38 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
     store_tile_bf16<MT, 4>(acc, a.d + (size_t)row0 * H, H, 0, n0, nrows, H, 1.0f, true);
 }
 
-__global__ __launch_bounds__(kThreads) void moe_down_gemm_kernel(MoeArgs a) {
+// The down GEMM's K (= I) is short, so a tile's prologue (plan lookups, first stages in
+// flight) and epilogue (output stores) are a large part of it.  It runs 128-row tiles
+// with two workgroups per CU (76.8 KB of LDS each): one workgroup's prologue and
+// epilogue overlap the other's MFMAs.  Class-0 tiles run as two 128-row halves, class-1
+// tiles as they are, class-2 tiles as 64-row tiles.  Virtual m-tiles: halves of class-0
+// tile k at 16 (k / 8) + k % 8 + 8 h (both on XCD k % 8, one after the other, so the
+// second finds the W tile in L2), then the class-1 and class-2 tiles.
+constexpr size_t kDownLds = Layout<4, 4>::kLds;
+
+__global__ __launch_bounds__(kThreads, 2) void moe_down_gemm_kernel(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t E = a.E, P = a.T * a.k;
     const PlanView v = plan_view(a.plan, E, P);
     const uint32_t nn = (a.H + BN - 1) / BN;
     uint32_t mt, nt;
     xcd_tile(nn, mt, nt);
-    if (mt >= uniform(v.hdr[1]))
+    const uint32_t n0t = uniform(v.hdr[2]), ntiles = uniform(v.hdr[1]);
+    const uint32_t nsplit = 16 * ((n0t + 7) / 8);
+    const bool split = mt < nsplit;
+    const uint32_t k0 = 8 * (mt / 16) + mt % 8;
+    if (split ? k0 >= n0t : mt - nsplit + n0t >= ntiles)
         return;
-    const int32_t *t = v.tiles + 4 * mt;
+    const int32_t *t = v.tiles + 4 * (split ? k0 : mt - nsplit + n0t);
     const int e = uniform(t[0]), cls = uniform(t[3]);
-    const uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]), n0 = nt * BN;
-    if (cls == 0)
-        down_tile<8>(a, lds, e, row0, nrows, n0);
-    else if (cls == 1)
+    uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]);
+    const uint32_t n0 = nt * BN;
+    if (split) {
+        const uint32_t h = (mt / 8) % 2;
+        row0 += 128 * h;
+        nrows = nrows - 128 * h < 128 ? nrows - 128 * h : 128;
+        down_tile<4>(a, lds, e, row0, nrows, n0);
+    } else if (cls == 1)
         down_tile<4>(a, lds, e, row0, nrows, n0);
     else
         down_tile<2>(a, lds, e, row0, nrows, n0);
@@ -804,7 +823,7 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     static bool lds_gateup = false, lds_down = false;
     hipError_t err = set_lds(moe_gateup_gemm_kernel, kMaxLds, lds_gateup);
     if (err == hipSuccess)
-        err = set_lds(moe_down_gemm_kernel, kMaxLds, lds_down);
+        err = set_lds(moe_down_gemm_kernel, kDownLds, lds_down);
     if (err != hipSuccess)
         return err;
     hipLaunchKernelGGL(moe_route_kernel, dim3((a.T + 3) / 4), dim3(256), 0, stream, a.logits, a.T,
@@ -814,8 +833,11 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     const uint32_t nn_gu = (a.I + kGateUpCols - 1) / kGateUpCols;
     hipLaunchKernelGGL(moe_gateup_gemm_kernel, dim3(mt8 * nn_gu), dim3(kThreads), kMaxLds, stream,
                        a);
+    // virtual m-tiles: at most 2 max_tiles + 16 (two halves per class-0 tile, padded
+    // to whole groups of 8)
     const uint32_t nn_d = (a.H + BN - 1) / BN;
-    hipLaunchKernelGGL(moe_down_gemm_kernel, dim3(mt8 * nn_d), dim3(kThreads), kMaxLds, stream, a);
+    const uint32_t vt8 = 8 * ((2 * a.max_tiles + 16 + 7) / 8);
+    hipLaunchKernelGGL(moe_down_gemm_kernel, dim3(vt8 * nn_d), dim3(kThreads), kDownLds, stream, a);
     hipLaunchKernelGGL(moe_combine_kernel, dim3(a.T, (a.H + kCombineCols - 1) / kCombineCols),
                        dim3(256), 0, stream, a);
     return hipGetLastError();

@@ -96,6 +96,17 @@ __device__ __forceinline__ float gelu_tanh(float g) {
     return g / (1.0f + __expf(-2.0f * u));
 }
 
+// The same function for GEMM epilogues, where it runs once per output element: the
+// constants folded into one base-2 exponent, -2 u log2(e) = g (k1 + k2 g^2), then
+// v_exp_f32 and v_rcp_f32 (each about 1 ulp) instead of a correctly rounded division;
+// a few fp32 ulps from gelu_tanh, with the same limits (+inf exponent -> g * 0 = -0).
+__device__ __forceinline__ float gelu_tanh_fast(float g) {
+    constexpr float k1 = -2.0f * 1.4426950408889634f * 0.7978845608028654f;
+    constexpr float k2 = k1 * 0.044715f;
+    const float t = g * __builtin_fmaf(k2, g * g, k1);
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
+}
+
 // Sum over aligned groups of G lanes (G in {8, 16, 32, 64}) of a wave64; every lane
 // of a group receives the group total.  DPP within rows of 16, then cross-row swaps.
 template <int G>
