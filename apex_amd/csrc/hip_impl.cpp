@@ -185,6 +185,8 @@ void moe_impl(const uint16_t *x, const uint16_t *logits, const apex_moe_slots *s
     a.plan = reinterpret_cast<int32_t *>(base + w.plan);
     a.h = reinterpret_cast<uint16_t *>(base + w.h);
     a.d = reinterpret_cast<uint16_t *>(base + w.d);
+    a.hist = gemm ? reinterpret_cast<int32_t *>(base + w.hist) : nullptr;
+    a.rank = gemm ? reinterpret_cast<int32_t *>(base + w.rank) : nullptr;
     a.max_tiles = w.max_tiles;
     hip_check(apex_hip::moe_ffn_launch(a, gemm, stream), "moe_ffn launch");
 }

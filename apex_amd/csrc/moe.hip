@@ -173,39 +173,22 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *logits, 
     }
 }
 
-// Grouping of the P = T*k pairs by expert (one workgroup of 1024 threads).  With
-// `tiles`, also the m-tile list of the grouped GEMMs: entries (expert, first pos,
-// rows, class) with class 0/1/2 = 256/128/64-row tiles -- per expert, full 256-row
-// tiles and a tail tile of the smallest class that holds the remainder -- all class-0
-// tiles first.  Counts, offsets and tile slots come from exclusive scans over the
-// experts, so every expert's entries are written in parallel.
+// Plan from per-expert pair counts `cnt` (LDS, kMoeMaxExperts entries, zero from E
+// on; one workgroup of >= kMoeMaxExperts threads): header, counts, offsets, the active
+// expert list and, with `tiles`, the m-tile list of the grouped GEMMs -- entries
+// (expert, first pos, rows, class) with class 0/1/2 = 256/128/64-row tiles: per
+// expert, full 256-row tiles and a tail tile of the smallest class that holds the
+// remainder, all class-0 tiles first.  Counts, offsets and tile slots come from
+// exclusive scans over the experts, so every expert's entries are written in
+// parallel.  `first` receives each expert's first position.
 constexpr int kPlanScans = 5; // pair counts, active flags, class 0/1/2 tile counts
 constexpr int kPlanBatch = 8; // pairs per thread whose loads are issued together
 
-__device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
-    __shared__ int cnt[kMoeMaxExperts], cur[kMoeMaxExperts];
+__device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first, bool tiles) {
     __shared__ int scan[kPlanScans][kMoeMaxExperts];
     const uint32_t E = a.E, P = a.T * a.k;
     const PlanView v = plan_view(a.plan, E, P);
     const int tid = threadIdx.x;
-    if (tid < (int)kMoeMaxExperts)
-        cnt[tid] = 0;
-    __syncthreads();
-    // Pairs in batches of kPlanBatch per thread: the batch's loads are all in flight
-    // before its atomics (a load -> atomic -> store chain per pair is latency-bound).
-    for (uint32_t p0 = 0; p0 < P; p0 += blockDim.x * kPlanBatch) {
-        int e[kPlanBatch];
-#pragma unroll
-        for (int b = 0; b < kPlanBatch; ++b) {
-            const uint32_t p = p0 + b * blockDim.x + tid;
-            e[b] = p < P ? ids[p] : -1;
-        }
-#pragma unroll
-        for (int b = 0; b < kPlanBatch; ++b)
-            if (e[b] >= 0)
-                atomicAdd(&cnt[e[b]], 1);
-    }
-    __syncthreads();
     // inclusive Hillis-Steele scans over the 256 expert slots (experts >= E count 0)
     int val[kPlanScans] = {};
     const int c = tid < (int)E ? cnt[tid] : 0;
@@ -239,7 +222,7 @@ __device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
     if (tid < (int)E) {
         const int e = tid;
         const int off = scan[0][e] - val[0]; // exclusive
-        cur[e] = off;
+        first[e] = off;
         v.off[e] = off;
         v.cnt[e] = c;
         if (c > 0)
@@ -271,6 +254,35 @@ __device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
         v.hdr[2] = n0;
     }
     __syncthreads();
+}
+
+// Grouping of the P = T*k pairs by expert in one workgroup of 1024 threads (decode:
+// P <= 256): counts by LDS atomics, plan_scan, then each pair's position in its
+// expert's group by a second round of atomics.
+__device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
+    __shared__ int cnt[kMoeMaxExperts], cur[kMoeMaxExperts];
+    const uint32_t E = a.E, P = a.T * a.k;
+    const PlanView v = plan_view(a.plan, E, P);
+    const int tid = threadIdx.x;
+    if (tid < (int)kMoeMaxExperts)
+        cnt[tid] = 0;
+    __syncthreads();
+    // Pairs in batches of kPlanBatch per thread: the batch's loads are all in flight
+    // before its atomics (a load -> atomic -> store chain per pair is latency-bound).
+    for (uint32_t p0 = 0; p0 < P; p0 += blockDim.x * kPlanBatch) {
+        int e[kPlanBatch];
+#pragma unroll
+        for (int b = 0; b < kPlanBatch; ++b) {
+            const uint32_t p = p0 + b * blockDim.x + tid;
+            e[b] = p < P ? ids[p] : -1;
+        }
+#pragma unroll
+        for (int b = 0; b < kPlanBatch; ++b)
+            if (e[b] >= 0)
+                atomicAdd(&cnt[e[b]], 1);
+    }
+    __syncthreads();
+    plan_scan(a, cnt, cur, tiles);
     for (uint32_t p0 = 0; p0 < P; p0 += blockDim.x * kPlanBatch) {
         int e[kPlanBatch], pos[kPlanBatch];
 #pragma unroll
@@ -292,7 +304,140 @@ __device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
     }
 }
 
-__global__ __launch_bounds__(1024) void moe_plan_kernel(MoeArgs a) { plan_block(a, a.ids, true); }
+// Prefill grouping, deterministic and free of contended atomics, in three launches.
+// 1. moe_route_hist_kernel: each workgroup routes kRouteBlockTokens tokens and marks,
+//    per expert, the bit of every one of its tokens that chose it (LDS atomicOr, whose
+//    result does not depend on order).  A pair's rank inside its workgroup's group is
+//    the popcount of its expert's mask below its token's bit; the mask's popcount is
+//    the workgroup's count for the expert -> hist[block][expert].
+// 2. moe_plan_scan_kernel (one workgroup): per expert, the exclusive scan of hist over
+//    the workgroups (written back in place) and the total count; plan_scan.
+// 3. moe_plan_scatter_kernel: pos = off[e] + hist[block][e] + rank, one pair per thread.
+constexpr uint32_t kRouteBlockTokens = 16; // one token per wave of a 1024-thread workgroup
+
+__global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
+    __shared__ unsigned long long mask[kMoeMaxExperts];
+    __shared__ int32_t s_id[kRouteBlockTokens * kMoeMaxTopK];
+    const uint32_t E = a.E, k = a.k;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t0 = blockIdx.x * kRouteBlockTokens;
+    const uint32_t nt = a.T - t0 < kRouteBlockTokens ? a.T - t0 : kRouteBlockTokens;
+    for (uint32_t e = threadIdx.x; e < kMoeMaxExperts; e += blockDim.x)
+        mask[e] = 0;
+    __syncthreads();
+    for (uint32_t tl = wave; tl < nt; tl += blockDim.x / 64) {
+        const uint32_t t = t0 + tl;
+        int32_t id;
+        float wt;
+        route_token(a.logits + (size_t)t * E, E, k, lane, id, wt);
+        if ((uint32_t)lane < k) {
+            a.ids[(size_t)t * k + lane] = id;
+            a.w[(size_t)t * k + lane] = wt;
+            s_id[tl * k + lane] = id;
+            atomicOr(&mask[id], 1ull << tl);
+        }
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < nt * k; q += blockDim.x) {
+        const uint32_t tl = q / k;
+        const unsigned long long below = (1ull << tl) - 1;
+        a.rank[(size_t)t0 * k + q] = __popcll(mask[s_id[q]] & below);
+    }
+    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x)
+        a.hist[(size_t)blockIdx.x * E + e] = __popcll(mask[e]);
+}
+
+__global__ __launch_bounds__(1024) void moe_plan_scan_kernel(MoeArgs a) {
+    __shared__ int cnt[kMoeMaxExperts], first[kMoeMaxExperts];
+    __shared__ int part[1024];
+    constexpr uint32_t kChunk = 16; // hist loads in flight per thread
+    const uint32_t E = a.E;
+    const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
+    // thread (e, q): expert e, part q of the workgroups
+    const uint32_t nq = blockDim.x / E;
+    const uint32_t e = threadIdx.x % E, q = threadIdx.x / E;
+    const bool active = q < nq;
+    const uint32_t per = (nb + nq - 1) / nq;
+    const uint32_t b0 = q * per < nb ? q * per : nb;
+    const uint32_t b1 = b0 + per < nb ? b0 + per : nb;
+    if (threadIdx.x < kMoeMaxExperts)
+        cnt[threadIdx.x] = 0;
+    if (per <= 2 * kChunk) {
+        // one load of the part's counts, kept in registers for the write-back
+        int c[2 * kChunk];
+        int sum = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < 2 * kChunk; ++i) {
+            c[i] = active && b0 + i < b1 ? a.hist[(size_t)(b0 + i) * E + e] : 0;
+            sum += c[i];
+        }
+        part[threadIdx.x] = sum;
+        __syncthreads();
+        if (active) {
+            int run = 0;
+            for (uint32_t qq = 0; qq < q; ++qq)
+                run += part[qq * E + e];
+#pragma unroll
+            for (uint32_t i = 0; i < 2 * kChunk; ++i)
+                if (b0 + i < b1) {
+                    a.hist[(size_t)(b0 + i) * E + e] = run;
+                    run += c[i];
+                }
+            if (q == nq - 1)
+                cnt[e] = run;
+        }
+        __syncthreads();
+        plan_scan(a, cnt, first, true);
+        return;
+    }
+    int sum = 0;
+    if (active)
+        for (uint32_t b = b0; b < b1; b += kChunk) {
+            int c[kChunk];
+#pragma unroll
+            for (uint32_t i = 0; i < kChunk; ++i)
+                c[i] = b + i < b1 ? a.hist[(size_t)(b + i) * E + e] : 0;
+#pragma unroll
+            for (uint32_t i = 0; i < kChunk; ++i)
+                sum += c[i];
+        }
+    part[threadIdx.x] = sum;
+    __syncthreads();
+    if (active) {
+        int run = 0; // this part's start: the earlier parts' totals
+        for (uint32_t qq = 0; qq < q; ++qq)
+            run += part[qq * E + e];
+        for (uint32_t b = b0; b < b1; b += kChunk) {
+            int c[kChunk];
+#pragma unroll
+            for (uint32_t i = 0; i < kChunk; ++i)
+                c[i] = b + i < b1 ? a.hist[(size_t)(b + i) * E + e] : 0;
+#pragma unroll
+            for (uint32_t i = 0; i < kChunk; ++i)
+                if (b + i < b1) {
+                    a.hist[(size_t)(b + i) * E + e] = run;
+                    run += c[i];
+                }
+        }
+        if (q == nq - 1)
+            cnt[e] = run;
+    }
+    __syncthreads();
+    plan_scan(a, cnt, first, true);
+}
+
+__global__ __launch_bounds__(256) void moe_plan_scatter_kernel(MoeArgs a) {
+    const uint32_t P = a.T * a.k;
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= P)
+        return;
+    const PlanView v = plan_view(a.plan, a.E, P);
+    const int e = a.ids[p];
+    const uint32_t b = p / a.k / kRouteBlockTokens;
+    const int pos = v.off[e] + a.hist[(size_t)b * a.E + e] + a.rank[p];
+    v.pos_of_pair[p] = pos;
+    v.pair_of_pos[pos] = (int32_t)p;
+}
 
 // Decode: route all T <= 32 tokens (two per wave) and plan, in one workgroup.
 __global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
@@ -730,6 +875,12 @@ MoeWorkspace moe_workspace(uint32_t T, uint32_t E, uint32_t k, uint32_t H, uint3
     off = align256(off + P * I * 2);
     w.d = off;
     off = align256(off + P * H * 2);
+    if (gemm) { // prefill grouping: per-workgroup expert counts and in-workgroup ranks
+        w.hist = off;
+        off = align256(off + 4 * (size_t)E * ((T + kRouteBlockTokens - 1) / kRouteBlockTokens));
+        w.rank = off;
+        off = align256(off + 4 * P);
+    }
     w.total = off;
     return w;
 }
@@ -826,9 +977,10 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
         err = set_lds(moe_down_gemm_kernel, kDownLds, lds_down);
     if (err != hipSuccess)
         return err;
-    hipLaunchKernelGGL(moe_route_kernel, dim3((a.T + 3) / 4), dim3(256), 0, stream, a.logits, a.T,
-                       a.E, a.k, a.ids, a.w);
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, stream, a);
+    const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
+    hipLaunchKernelGGL(moe_route_hist_kernel, dim3(nb), dim3(64 * kRouteBlockTokens), 0, stream, a);
+    hipLaunchKernelGGL(moe_plan_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL(moe_plan_scatter_kernel, dim3((a.T * a.k + 255) / 256), dim3(256), 0, stream, a);
     const uint32_t mt8 = 8 * ((a.max_tiles + 7) / 8); // m-tiles rounded to whole XCD turns
     const uint32_t nn_gu = (a.I + kGateUpCols - 1) / kGateUpCols;
     hipLaunchKernelGGL(moe_gateup_gemm_kernel, dim3(mt8 * nn_gu), dim3(kThreads), kMaxLds, stream,
