@@ -13,6 +13,7 @@
 #include "gemm.h"
 #include "gemv.h"
 #include "moe.h"
+#include "norm.h"
 
 namespace {
 
@@ -295,6 +296,64 @@ void launch_matmul_nvfp4(const LaunchCtx &c) {
               "matmul_nvfp4 launch");
 }
 
+void rms_norm_impl(const float *x, const uint16_t *w, float *y, uint32_t rows, uint32_t n,
+                   float eps, hipStream_t stream) {
+    if (rows == 0 || n == 0)
+        return;
+    require(x && w && y, "null pointer");
+    hip_check(apex_hip::rms_norm_launch({x, w, y, rows, n, eps}, stream), "rms_norm_f32 launch");
+}
+
+void head_norm_rope_impl(const apex_hip::HeadNormRopeArgs &a, hipStream_t stream) {
+    if (a.tokens == 0 || a.heads == 0)
+        return;
+    require(a.x && a.y && (a.w || !a.has_weight), "null pointer");
+    require(a.head_dim > 0 && a.head_dim % 2 == 0 && a.head_dim <= apex_hip::kHeadNormMaxDim,
+            "head_norm_rope: head_dim must be even and at most 512");
+    require(a.rope_pairs <= a.head_dim / 2, "head_norm_rope: rope_pairs exceeds head_dim / 2");
+    hip_check(apex_hip::head_norm_rope_launch(a, stream), "head_norm_rope_f32 launch");
+}
+
+// rms_norm_f32: src/ops.h:18-26 (rows = threadgroups.x), shaders/norm.metal:33-44.
+void launch_rms_norm(const LaunchCtx &c) {
+    const uint32_t rows = c.grid.x, n = c.u[3];
+    need(c, 0, (uint64_t)rows * n * 4, "rms_norm_f32 input");
+    need(c, 1, (uint64_t)n * 2, "rms_norm_f32 weights");
+    need(c, 2, (uint64_t)rows * n * 4, "rms_norm_f32 result");
+    rms_norm_impl((const float *)c.ptr[0], (const uint16_t *)c.ptr[1], (float *)c.ptr[2], rows, n,
+                  c.f[4], c.stream);
+}
+
+// head_norm_rope_f32: src/ops.h:88-118 (tokens = threadgroups.x, heads = threadgroups.y,
+// which the reference's launcher sets to the heads argument), shaders/head_norm_rope.metal.
+void launch_head_norm_rope(const LaunchCtx &c) {
+    apex_hip::HeadNormRopeArgs a{};
+    a.x = (const float *)c.ptr[0];
+    a.w = (const uint16_t *)c.ptr[1];
+    a.y = (float *)c.ptr[2];
+    a.tokens = c.grid.x;
+    a.heads = c.u[3];
+    a.head_dim = c.u[4];
+    a.has_weight = c.u[5] != 0;
+    a.rope_pairs = c.u[6];
+    a.rope_base = c.f[7];
+    a.abs_pos = c.u[8];
+    a.out_token_stride = c.u[9];
+    a.out_head_stride = c.u[10];
+    a.eps = c.f[11];
+    if (c.grid.y != a.heads)
+        fail(APEX_HIP_E_INVALID, "head_norm_rope_f32: threadgroups.y must equal heads");
+    if (a.heads == 0)
+        return;
+    need(c, 0, (uint64_t)a.tokens * a.heads * a.head_dim * 4, "head_norm_rope_f32 input");
+    if (a.has_weight)
+        need(c, 1, (uint64_t)a.head_dim * 2, "head_norm_rope_f32 weights");
+    need(c, 2, ((uint64_t)(a.tokens - 1) * a.out_token_stride +
+                (uint64_t)(a.heads - 1) * a.out_head_stride + a.head_dim) * 4,
+         "head_norm_rope_f32 output");
+    head_norm_rope_impl(a, c.stream);
+}
+
 // geglu_f32: src/ops.h:53-54.
 void launch_geglu_f32(const LaunchCtx &c) {
     const uint64_t threads = (uint64_t)c.grid.x * c.grid.y * c.grid.z *
@@ -389,6 +448,8 @@ const KernelSpec kKernels[] = {
     {"dequant_nvfp4_bf16", "BBBUUF", 1u << 2, launch_dequant<true>},
     {"moe_ffn_nvfp4_bf16", "BBBBBUUUUUUUUUUUU", (1u << 3) | (1u << 4), launch_moe_ffn},
     {"moe_route_bf16", "BBBUUU", (1u << 1) | (1u << 2), launch_moe_route},
+    {"rms_norm_f32", "BBBUF", 1u << 2, launch_rms_norm},
+    {"head_norm_rope_f32", "BBBUUUUFUUUF", 1u << 2, launch_head_norm_rope},
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -679,6 +740,23 @@ int apex_geglu_f32(const float *gate, const float *up, float *out, uint32_t coun
         require(gate && up && out, "null pointer");
         hip_check(apex_hip::geglu_f32_launch(gate, up, out, count, as_stream(stream)),
                   "geglu_f32 launch");
+    });
+}
+
+int apex_rms_norm_f32(const float *x, const uint16_t *weights, float *y, uint32_t rows,
+                      uint32_t hidden_dim, float eps, void *stream) {
+    return guard([&] { rms_norm_impl(x, weights, y, rows, hidden_dim, eps, as_stream(stream)); });
+}
+
+int apex_head_norm_rope_f32(const float *x, const uint16_t *weights, int has_weights, float *y,
+                            uint32_t tokens, uint32_t heads, uint32_t head_dim, uint32_t rope_pairs,
+                            float rope_base, uint32_t abs_pos, uint32_t out_token_stride,
+                            uint32_t out_head_stride, float eps, void *stream) {
+    return guard([&] {
+        apex_hip::HeadNormRopeArgs a{x, weights, y, tokens, heads, head_dim,
+                                     has_weights ? 1u : 0u, rope_pairs, rope_base, abs_pos,
+                                     out_token_stride, out_head_stride, eps};
+        head_norm_rope_impl(a, as_stream(stream));
     });
 }
 

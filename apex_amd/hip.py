@@ -99,6 +99,9 @@ _PROTOS = {
     "apex_moe_workspace_bytes": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
     "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
     "apex_hip_set_moe_path": (_I, [_I]),
+    "apex_rms_norm_f32": (_I, [_P, _P, _P, _U32, _U32, _F, _P]),
+    "apex_head_norm_rope_f32": (_I, [_P, _P, _I, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32,
+                                     _F, _P]),
 }
 
 
@@ -268,6 +271,18 @@ def geglu_f32(gate, up, out, count, stream=None):
 def nvfp4_dequant(codes, scales, out, rows, K, tensor_scale=1.0, stream=None):
     f = lib().apex_nvfp4_dequant_bf16 if out.dtype == np.uint16 else lib().apex_nvfp4_dequant_f32
     check(f(codes.ptr, scales.ptr, tensor_scale, out.ptr, rows, K, _s(stream)))
+
+
+def rms_norm_f32(x, w, y, rows, hidden_dim, eps, stream=None):
+    check(lib().apex_rms_norm_f32(x.ptr, w.ptr, y.ptr, rows, hidden_dim, eps, _s(stream)))
+
+
+def head_norm_rope_f32(x, w, y, tokens, heads, head_dim, rope_pairs, rope_base, abs_pos,
+                       out_token_stride, out_head_stride, eps, has_weights=True, stream=None):
+    check(lib().apex_head_norm_rope_f32(x.ptr, w.ptr if w is not None else None,
+                                        1 if has_weights else 0, y.ptr, tokens, heads, head_dim,
+                                        rope_pairs, rope_base, abs_pos, out_token_stride,
+                                        out_head_stride, eps, _s(stream)))
 
 
 def read_probe(buf, sink, stream=None) -> None:

@@ -1,6 +1,6 @@
 // Kernel-launch helpers over the Backend interface, as src/ops.h provides them for the
-// engine: the reference's NVFP4 ops under their reference names and argument order
-// (matmulNvfp4, geglu, denseMlp: src/ops.h:7-16, 28-69), plus the HIP backend's
+// engine: the reference's ops under their reference names and argument order
+// (rmsNorm, matmulNvfp4, geglu, denseMlp, headNormRope: src/ops.h:7-118), plus the HIP backend's
 // additional ops -- bf16 activations, the fused GeGLU projection, the MFMA prefill
 // GEMM and the MoE expert FFN.  Every helper only queues work (Backend::run); results
 // are visible after Backend::sync().
@@ -22,6 +22,35 @@ struct Nvfp4Matrix {
     uint32_t w_rows;
     uint32_t hidden_dim;
 };
+
+// RMSNorm of fp32 rows with bf16 weights (src/ops.h:18-26): one threadgroup per row.
+inline void rmsNorm(Backend &backend, Buffer *input, Buffer *weights, size_t weight_offset,
+                    Buffer *result, uint32_t rows, uint32_t hidden_dim, float eps) {
+    constexpr uint32_t kThreads = 256;
+    backend.run("rms_norm_f32",
+                {Arg::buf(input), Arg::buf(weights, weight_offset), Arg::buf(result),
+                 Arg::val(hidden_dim), Arg::val(eps)},
+                Dim3{rows}, Dim3{kThreads});
+}
+
+// Per-head RMSNorm, optional learned scaling and RoPE on the first rope_pairs pairs
+// (src/ops.h:71-118): input [tokens, heads, head_dim] fp32; head (t, h) is written at
+// output + output_offset + (t * out_token_stride + h * out_head_stride) floats.
+inline void headNormRope(Backend &backend, Buffer *input, Buffer *weights, size_t weights_offset,
+                         bool has_weights, Buffer *output, size_t output_offset, uint32_t tokens,
+                         uint32_t heads, uint32_t head_dim, uint32_t rope_pairs, float rope_base,
+                         uint32_t abs_pos, uint32_t out_token_stride, uint32_t out_head_stride,
+                         float eps) {
+    constexpr uint32_t kThreads = 256;
+    const uint32_t weight_flag = has_weights ? 1u : 0u;
+    backend.run("head_norm_rope_f32",
+                {Arg::buf(input), Arg::buf(weights, weights_offset),
+                 Arg::buf(output, output_offset), Arg::val(heads), Arg::val(head_dim),
+                 Arg::val(weight_flag), Arg::val(rope_pairs), Arg::val(rope_base),
+                 Arg::val(abs_pos), Arg::val(out_token_stride), Arg::val(out_head_stride),
+                 Arg::val(eps)},
+                Dim3{tokens, heads}, Dim3{kThreads});
+}
 
 // fp32 [tokens, hidden_dim] -> fp32 [tokens, w_rows] (src/ops.h:34-46): the reference
 // launch shape, rows in groups of 8 and tokens on the grid's y axis.

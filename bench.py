@@ -240,6 +240,46 @@ def time_gemm_prefill(steps, warmup, M=2048, N=21504, K=5376):
             "yardstick_vendor_bf16_gemm_tflops": vendor_bf16_gemm(M, N, K, steps, warmup)}
 
 
+def time_norms(steps, warmup, T=4096, H=2816, heads=16, D=256):
+    """The two normalisation kernels at prefill size: RMSNorm of x fp32 [4096, 2816]
+    and per-head RMSNorm + RoPE of q fp32 [4096, 16, 256] (128 rotated pairs).  Both
+    read and write their activations once: algorithmic bytes = 2 x activations +
+    weights."""
+    rng = np.random.default_rng(0)
+    out = {}
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    w = synth.bf16_from_f32((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    dx, dw, dy = (hip.DeviceArray.from_numpy(x), hip.DeviceArray.from_numpy(w),
+                  hip.DeviceArray((T, H), np.float32))
+    stream = hip.Stream()
+    sec = time_steps(lambda i: hip.rms_norm_f32(dx, dw, dy, T, H, 1e-6, stream=stream), steps,
+                     warmup, stream)
+    algo = 2 * x.nbytes + w.nbytes
+    out["rms_norm"] = {"value": round(algo / sec / 1e9, 2), "unit": "GB/s",
+                       "ms_per_step": round(sec * 1e3, 6),
+                       "roofline_frac": round(algo / sec / 1e9 / HBM_PEAK_GBS, 4),
+                       "algorithmic_bytes": int(algo),
+                       "workload": f"rms_norm_f32: x fp32 [{T},{H}], bf16 weights [{H}]"}
+    q = rng.standard_normal((T, heads, D)).astype(np.float32)
+    hw = synth.bf16_from_f32((1 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+    dq, dhw, do = (hip.DeviceArray.from_numpy(q), hip.DeviceArray.from_numpy(hw),
+                   hip.DeviceArray(q.shape, np.float32))
+    sec = time_steps(lambda i: hip.head_norm_rope_f32(dq, dhw, do, T, heads, D, D // 2, 10000.0,
+                                                      0, heads * D, D, 1e-6, stream=stream),
+                     steps, warmup, stream)
+    algo = 2 * q.nbytes + hw.nbytes
+    out["head_norm_rope"] = {"value": round(algo / sec / 1e9, 2), "unit": "GB/s",
+                             "ms_per_step": round(sec * 1e3, 6),
+                             "roofline_frac": round(algo / sec / 1e9 / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes": int(algo),
+                             "workload": f"head_norm_rope_f32: q fp32 [{T},{heads},{D}], "
+                                         f"{D // 2} rotated pairs"}
+    stream.close()
+    for a in (dx, dw, dy, dq, dhw, do):
+        a.close()
+    return out
+
+
 def vendor_bf16_gemm(M, N, K, steps, warmup):
     """Context for the GEMM line: the vendor library's plain bf16 GEMM of the same shape
     (torch -> hipBLASLt, weights already bf16, no FP4 decode).  Not part of the path."""
@@ -301,7 +341,7 @@ def main(argv=None):
                     help="time only the headline fused-GeGLU workload")
     ap.add_argument("--calibrate", action="store_true",
                     help="run the known-size read and copy kernels first (counter scaling)")
-    ap.add_argument("--only", choices=["moe_prefill", "gemm_prefill", "moe_decode"],
+    ap.add_argument("--only", choices=["moe_prefill", "gemm_prefill", "moe_decode", "norms"],
                     help="profiling aid: time one secondary workload and print its record only")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -313,7 +353,7 @@ def main(argv=None):
         calibrate()
     if args.only:
         fn = {"moe_prefill": time_moe_prefill, "gemm_prefill": time_gemm_prefill,
-              "moe_decode": time_moe_decode}[args.only]
+              "moe_decode": time_moe_decode, "norms": time_norms}[args.only]
         print(json.dumps({args.only: fn(args.steps, args.warmup)}), flush=True)
         return 0
     r = time_geglu(args.steps, args.warmup)
@@ -356,6 +396,7 @@ def main(argv=None):
             "gemm_prefill": time_gemm_prefill(sec_steps, sec_warm),
             "moe_decode": time_moe_decode(max(1, args.steps // 10), max(1, args.warmup // 10)),
         }
+        line["secondary"].update(time_norms(max(1, args.steps // 10), max(1, args.warmup // 10)))
     if not args.no_cpu:
         cb = cpu_baseline_geglu(args.cpu_budget)
         cb.pop("_h")

@@ -127,8 +127,17 @@ int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
  *                     U down_w, U down_s (apex_moe_ffn_bf16).
  *   moe_route_bf16    B logits bf16 [T,E], B ids i32 [T,k], B weights f32 [T,k], U T,
  *                     U E, U top_k (apex_moe_route_bf16).
+ *   rms_norm_f32      B input f32 [rows,n], B weights bf16 [n], B result f32 [rows,n],
+ *                     U hidden_dim n, F eps; rows = threadgroups.x (src/ops.h:18-26,
+ *                     shaders/norm.metal:33-81).
+ *   head_norm_rope_f32 B input f32 [T,heads,head_dim], B weights bf16 [head_dim], B
+ *                     output, U heads, U head_dim, U has_weight, U rope_pairs, F
+ *                     rope_base, U abs_pos, U out_token_stride, U out_head_stride, F eps;
+ *                     T = threadgroups.x, threadgroups.y = heads (src/ops.h:88-118,
+ *                     shaders/head_norm_rope.metal:5-72).  head_dim even, <= 512.
  * For the kernels after geglu_f32 the launch shape is chosen by the backend; the
- * caller's threadgroups/threads must only be nonzero. */
+ * caller's threadgroups/threads must only be nonzero (the norms read T / rows from
+ * threadgroups as the reference launches do). */
 int apex_hip_run(apex_hip_backend *backend, const char *kernel, const apex_hip_arg *args,
                  size_t nargs, apex_hip_dim3 threadgroups, apex_hip_dim3 threads_per_group);
 
@@ -191,6 +200,22 @@ int apex_nvfp4_geglu_bf16(const uint16_t *x, const uint32_t *gate_codes,
 /* shaders/geglu.metal:6-24: out[i] = gelu_tanh(gate[i]) * up[i]; out may alias gate. */
 int apex_geglu_f32(const float *gate, const float *up, float *out, uint32_t count,
                    void *stream);
+
+/* shaders/norm.metal:33-81 (src/ops.h:18-26 rmsNorm): per row of x [rows, hidden_dim]
+ * fp32, y = x * (1 / sqrt(mean(x^2) + eps)) * w with w bf16 [hidden_dim]; fp32 sums.
+ * y may alias x. */
+int apex_rms_norm_f32(const float *x, const uint16_t *weights, float *y, uint32_t rows,
+                      uint32_t hidden_dim, float eps, void *stream);
+
+/* shaders/head_norm_rope.metal:5-72 (src/ops.h:88-118 headNormRope): per token t and
+ * head h of x [tokens, heads, head_dim] fp32, RMS-normalise the head (times w bf16
+ * [head_dim] if has_weights), then rotate pairs (i, head_dim/2 + i) for i < rope_pairs
+ * by (abs_pos + t) * rope_base^(-2 i / head_dim); write head (t, h) at
+ * y + t * out_token_stride + h * out_head_stride.  head_dim even and <= 512. */
+int apex_head_norm_rope_f32(const float *x, const uint16_t *weights, int has_weights, float *y,
+                            uint32_t tokens, uint32_t heads, uint32_t head_dim, uint32_t rope_pairs,
+                            float rope_base, uint32_t abs_pos, uint32_t out_token_stride,
+                            uint32_t out_head_stride, float eps, void *stream);
 
 /* src/nvfp4.h:27-43 on the device: out[r, k] = e2m1 * e4m3 * tensor_scale. */
 int apex_nvfp4_dequant_f32(const uint32_t *codes, const uint8_t *scales, float tensor_scale,

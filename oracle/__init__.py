@@ -55,6 +55,9 @@ def lib():
         L.orc_bf16_to_float.argtypes = [C.c_uint16]
         L.orc_float_to_bf16.restype = C.c_uint16
         L.orc_float_to_bf16.argtypes = [_F]
+        L.orc_rms_norm.argtypes = [_P, _P, _P, _SZ, _SZ, _F]
+        L.orc_head_norm_rope.argtypes = [_P, _P, C.c_int, _P, _SZ, _SZ, _SZ, _SZ, _F, C.c_uint32,
+                                         _SZ, _SZ, _F]
         _lib = L
     return _lib
 
@@ -183,6 +186,32 @@ def float_to_bf16(f: float) -> int:
     return lib().orc_float_to_bf16(f)
 
 
+def rms_norm(x, w_bf16, eps: float) -> np.ndarray:
+    """RMSNorm of every row of x [rows, n] fp32 with bf16 weights [n]."""
+    x, px = _c(np.atleast_2d(x), np.float32)
+    w, pw = _c(w_bf16, np.uint16)
+    y = np.empty_like(x)
+    lib().orc_rms_norm(px, pw, y.ctypes.data, x.shape[0], x.shape[1], eps)
+    return y
+
+
+def head_norm_rope(x, w_bf16, rope_pairs: int, rope_base: float, abs_pos: int, eps: float,
+                   has_weight: bool = True, out_token_stride=None, out_head_stride=None,
+                   out_size=None) -> np.ndarray:
+    """x [tokens, heads, head_dim] fp32 -> flat fp32 output laid out by the strides
+    (default: dense [tokens, heads, head_dim])."""
+    x, px = _c(x, np.float32)
+    T, Hh, D = x.shape
+    ots = Hh * D if out_token_stride is None else out_token_stride
+    ohs = D if out_head_stride is None else out_head_stride
+    n = out_size if out_size is not None else (T - 1) * ots + (Hh - 1) * ohs + D
+    y = np.zeros(n, np.float32)
+    w, pw = _c(w_bf16 if w_bf16 is not None else np.zeros(D, np.uint16), np.uint16)
+    lib().orc_head_norm_rope(px, pw, 1 if has_weight else 0, y.ctypes.data, T, Hh, D, rope_pairs,
+                             rope_base, abs_pos, ots, ohs, eps)
+    return y
+
+
 # ---- the reference's own CPU code, compiled from its sources (where available) ----
 
 def ref_available() -> bool:
@@ -205,6 +234,7 @@ def ref():
         R.ref_gelu_tanh.restype = _F
         R.ref_gelu_tanh.argtypes = [_F]
         R.ref_diff.argtypes = [_P, _P, _SZ, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        R.ref_rms_norm.argtypes = [_P, _P, _P, _SZ, _F]
         _ref = R
     return _ref
 
@@ -227,3 +257,14 @@ def ref_decode(codes, scales) -> np.ndarray:
     for r in range(rows):
         ref().ref_decode_row(pc + r * K // 2, ps + r * K // 16, out[r].ctypes.data, K)
     return out
+
+
+def ref_rms_norm(x, w_bf16, eps: float) -> np.ndarray:
+    """The reference's rmsNormCpu (src/tests/cpu_ref.h:10-22), row by row."""
+    x, px = _c(np.atleast_2d(x), np.float32)
+    w, pw = _c(w_bf16, np.uint16)
+    y = np.empty_like(x)
+    n = x.shape[1]
+    for r in range(x.shape[0]):
+        ref().ref_rms_norm(px + r * n * 4, pw, y[r].ctypes.data, n, eps)
+    return y

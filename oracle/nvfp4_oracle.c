@@ -217,3 +217,54 @@ uint16_t orc_float_to_bf16(float f) {
     u += 0x7FFFu + ((u >> 16) & 1u);
     return (uint16_t)(u >> 16);
 }
+
+/* src/tests/cpu_ref.h:10-22 (rmsNormCpu): fp64 sum of squares in index order,
+ * inv = 1 / sqrt(float(ss / n) + eps) in float, y = x * inv * w in float. */
+void orc_rms_norm(const float *x, const uint16_t *w_bf16, float *y, size_t rows, size_t n,
+                  float eps) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * n;
+        float *yr = y + r * n;
+        double ss = 0.0;
+        for (size_t i = 0; i < n; ++i)
+            ss += (double)xr[i] * xr[i];
+        const float inv = 1.0f / sqrtf((float)(ss / (double)n) + eps);
+        for (size_t i = 0; i < n; ++i)
+            yr[i] = xr[i] * inv * orc_bf16_to_float(w_bf16[i]);
+    }
+}
+
+/* shaders/head_norm_rope.metal:5-72 (no CPU reference exists): per (token, head) the
+ * rmsNormCpu arithmetic above over head_dim values (times w when has_weight), then
+ * pairs (i, half + i), i < rope_pairs, rotated by the angle the shader forms in fp32:
+ * pos = float(abs_pos + token), angle = pos * powf(rope_base, -2.0f * i / head_dim)
+ * (head_norm_rope.metal:53-55); cos, sin and the rotation in fp64, cast once. */
+void orc_head_norm_rope(const float *x, const uint16_t *w_bf16, int has_weight, float *y,
+                        size_t tokens, size_t heads, size_t head_dim, size_t rope_pairs,
+                        float rope_base, uint32_t abs_pos, size_t out_token_stride,
+                        size_t out_head_stride, float eps) {
+    const size_t half = head_dim / 2;
+    float *row = (float *)malloc(head_dim * sizeof(float));
+    for (size_t t = 0; t < tokens; ++t)
+        for (size_t h = 0; h < heads; ++h) {
+            const float *xr = x + (t * heads + h) * head_dim;
+            float *yr = y + t * out_token_stride + h * out_head_stride;
+            double ss = 0.0;
+            for (size_t i = 0; i < head_dim; ++i)
+                ss += (double)xr[i] * xr[i];
+            const float inv = 1.0f / sqrtf((float)(ss / (double)head_dim) + eps);
+            for (size_t i = 0; i < head_dim; ++i)
+                row[i] = xr[i] * inv * (has_weight ? orc_bf16_to_float(w_bf16[i]) : 1.0f);
+            const float pos = (float)(abs_pos + (uint32_t)t);
+            for (size_t i = 0; i < rope_pairs; ++i) {
+                const float angle = pos * powf(rope_base, -2.0f * (float)i / (float)head_dim);
+                const double c = cos((double)angle), sn = sin((double)angle);
+                const double a = row[i], b = row[half + i];
+                row[i] = (float)(a * c - b * sn);
+                row[half + i] = (float)(a * sn + b * c);
+            }
+            for (size_t i = 0; i < head_dim; ++i)
+                yr[i] = row[i];
+        }
+    free(row);
+}

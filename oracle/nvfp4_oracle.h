@@ -25,6 +25,10 @@
  *                       the routing weights.  Parity vs mlx-lm: UNPINNED (mlx-lm
  *                       is not importable; see the MoE section of the design notes)
  *   orc_e4m3_from_float round-to-nearest-even, checked against torch.float8_e4m3fn
+ *   orc_rms_norm        compiled reference rmsNormCpu (bit-exact), scale invariance
+ *   orc_head_norm_rope  rope_pairs = 0 / position 0 reduce to orc_rms_norm per head;
+ *                       recovered rotation angles equal pos * base^(-2i/d) (numpy);
+ *                       pair norms preserved; relative-position invariance of q.k
  */
 #ifndef APEX_NVFP4_ORACLE_H
 #define APEX_NVFP4_ORACLE_H
@@ -99,6 +103,20 @@ typedef struct {
 void orc_moe_ffn(const uint8_t *slots, const orc_expert_layout *layout, const float *x,
                  const int32_t *ids, const float *weights, float *y, size_t T, size_t k,
                  size_t H, size_t I);
+
+/* src/tests/cpu_ref.h:10-22 (rmsNormCpu) over `rows` rows of n values: fp64 sum of
+ * squares, inv = 1 / sqrt(float(ss / n) + eps), y = x * inv * bf16 weight. */
+void orc_rms_norm(const float *x, const uint16_t *w_bf16, float *y, size_t rows, size_t n,
+                  float eps);
+
+/* shaders/head_norm_rope.metal:5-72: per (token, head) the RMSNorm above (weights
+ * optional), then RoPE on pairs (i, head_dim/2 + i), i < rope_pairs, with the fp32
+ * angle float(abs_pos + token) * powf(rope_base, -2i/head_dim) of the shader and the
+ * rotation in fp64.  Output head (t, h) at y + t*out_token_stride + h*out_head_stride. */
+void orc_head_norm_rope(const float *x, const uint16_t *w_bf16, int has_weight, float *y,
+                        size_t tokens, size_t heads, size_t head_dim, size_t rope_pairs,
+                        float rope_base, uint32_t abs_pos, size_t out_token_stride,
+                        size_t out_head_stride, float eps);
 
 /* Round-to-nearest-even float -> FP8 E4M3 byte, saturating to +-448 (never emits
  * 0x7F/0xFF).  The synthetic generator's scale rounding, restated for checking. */

@@ -25,6 +25,10 @@ void ref_matvec_nvfp4(const uint32_t *codes, const uint8_t *scales, const float 
 
 float ref_gelu_tanh(float g) { return geluTanh(g); }
 
+void ref_rms_norm(const float *x, const uint16_t *w_bf16, float *y, size_t n, float eps) {
+    rmsNormCpu(x, w_bf16, y, n, eps);
+}
+
 void ref_diff(const float *a, const float *b, size_t n, double *max_abs, double *rel_l2) {
     const Diff d = diff(a, b, n);
     *max_abs = d.max_abs;

@@ -16,6 +16,8 @@ Fixtures:
                      for rows 1-64, K 16-256, tokens 1-3, covering all 16 codes
   matvec_2048.npz    the reference's output for the 2048x2048 single GEMV (x = bf16
                      N(0,1), seed 0), 2048 fp32
+  rms_norm.npz       per case: x (fp32 [rows, n]), w (bf16 bits [n]), eps and the
+                     reference's rmsNormCpu output (src/tests/cpu_ref.h:10-22)
   digests.json       SHA-256 of the synthetic inputs the fixtures were made from
 """
 from __future__ import annotations
@@ -36,6 +38,9 @@ from apex_amd import synth  # noqa: E402
 
 TINY = [(1, 16, 1), (3, 32, 2), (8, 48, 1), (16, 64, 3), (5, 128, 1), (64, 256, 2),
         (2, 16, 3), (33, 96, 1)]
+
+
+RMS_CASES = [(1, 16, 1e-6), (3, 100, 1e-5), (2, 2816, 1e-6), (1, 5376, 0.0)]
 
 
 def sha(*arrays) -> str:
@@ -88,6 +93,15 @@ def main() -> None:
     digests["moe_decode_case_seed0_tiny"] = sha(xm, lm, slots.data)
     xp, lp, slotsp = synth.moe_prefill_case(seed=0, tokens=8, H=64, I=32, E=16)
     digests["moe_prefill_case_seed0_tiny"] = sha(xp, lp, slotsp.data)
+    norm = {}
+    for i, (rows, n, eps) in enumerate(RMS_CASES):
+        rng = np.random.default_rng(2000 + i)
+        xn = rng.standard_normal((rows, n)).astype(np.float32) * np.float32(1 + i)
+        wn = synth.bf16_from_f32((1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32))
+        norm[f"c{i}_x"], norm[f"c{i}_w"] = xn, wn
+        norm[f"c{i}_eps"] = np.float32(eps)
+        norm[f"c{i}_y"] = oracle.ref_rms_norm(xn, wn, eps)
+    np.savez(HERE / "rms_norm.npz", **norm)
     (HERE / "digests.json").write_text(json.dumps(digests, indent=1, sort_keys=True) + "\n")
     print("wrote", sorted(p.name for p in HERE.glob("*.npz")), "and digests.json")
 

@@ -228,6 +228,62 @@ void test_moe(HipBackend &be) {
         be.release(b);
 }
 
+// src/tests/test_norm.cpp:70-101 pattern: weights at an offset inside a shared
+// "core" buffer, rmsNorm over every token row, compared by rel L2 (tolerance 1e-5).
+void test_norms(HipBackend &be) {
+    Rng rng{7};
+    const uint32_t T = 5, H = 2816;
+    std::vector<float> x((size_t)T * H);
+    for (auto &v : x)
+        v = rng.normal();
+    const size_t woff = 4096; // bytes before the weights inside the core buffer
+    std::vector<uint8_t> core(woff + H * 2);
+    for (uint32_t i = 0; i < H; ++i) {
+        const uint16_t w = to_bf16(1.0f + 0.1f * rng.normal());
+        std::memcpy(core.data() + woff + 2 * i, &w, 2);
+    }
+    Buffer *cb = upload(be, core.data(), core.size(), "core_weights");
+    Buffer *in = upload(be, x.data(), x.size() * 4, "activations");
+    Buffer *out = be.allocate(x.size() * 4, "activations");
+    const float eps = 1e-6f;
+    rmsNorm(be, in, cb, woff, out, T, H, eps);
+    be.sync();
+    std::vector<float> want(x.size());
+    orc_rms_norm(x.data(), reinterpret_cast<const uint16_t *>(core.data() + woff), want.data(), T,
+                 H, eps);
+    double r = rel_l2(static_cast<const float *>(be.contents(out)), want.data(), want.size());
+    report("rmsNorm vs oracle", r < 1e-5, "rel_l2 " + std::to_string(r));
+
+    // per-head norm + RoPE: 3 tokens x 8 heads x 256, 128 rotated pairs, output placed
+    // into a wider buffer (token stride 2 * heads * head_dim, at an offset)
+    const uint32_t nt = 3, heads = 8, D = 256, pairs = 128, pos0 = 7;
+    const uint32_t ts = 2 * heads * D, hs = D;
+    const float base = 10000.0f;
+    std::vector<float> q((size_t)nt * heads * D);
+    for (auto &v : q)
+        v = rng.normal();
+    std::vector<uint16_t> hw(D);
+    for (auto &w : hw)
+        w = to_bf16(1.0f + 0.1f * rng.normal());
+    Buffer *qb = upload(be, q.data(), q.size() * 4, "activations");
+    Buffer *wb = upload(be, hw.data(), hw.size() * 2, "core_weights");
+    const size_t out_off = 256; // bytes
+    const size_t n_out = (size_t)(nt - 1) * ts + (heads - 1) * hs + D;
+    Buffer *ob = be.allocate(out_off + n_out * 4, "activations");
+    std::memset(be.contents(ob), 0, out_off + n_out * 4);
+    headNormRope(be, qb, wb, 0, true, ob, out_off, nt, heads, D, pairs, base, pos0, ts, hs, eps);
+    be.sync();
+    std::vector<float> want_q(n_out, 0.0f);
+    orc_head_norm_rope(q.data(), hw.data(), 1, want_q.data(), nt, heads, D, pairs, base, pos0, ts,
+                       hs, eps);
+    const float *got_q =
+        reinterpret_cast<const float *>(static_cast<const uint8_t *>(be.contents(ob)) + out_off);
+    r = rel_l2(got_q, want_q.data(), n_out);
+    report("headNormRope vs oracle", r < 1e-5, "rel_l2 " + std::to_string(r));
+    for (Buffer *b : {cb, in, out, qb, wb, ob})
+        be.release(b);
+}
+
 bool throws(const std::function<void()> &f, const char *needle) {
     try {
         f();
@@ -240,7 +296,7 @@ bool throws(const std::function<void()> &f, const char *needle) {
 void test_errors(HipBackend &be) {
     Buffer *b = be.allocate(4096, "scratch");
     report("unknown kernel throws",
-           throws([&] { be.run("rms_norm_f32", {Arg::buf(b)}, Dim3{1}, Dim3{256}); },
+           throws([&] { be.run("attention_f32", {Arg::buf(b)}, Dim3{1}, Dim3{256}); },
                   "cannot find kernel"));
     report("threadgroup too large throws",
            throws([&] {
@@ -278,6 +334,7 @@ int main(int argc, char **argv) {
     test_dense_mlp(be);
     test_bf16_ops(be);
     test_moe(be);
+    test_norms(be);
     test_errors(be);
     Profile::get().print(stdout);
     std::printf("%s (%d failure%s)\n", g_failures ? "FAILED" : "OK", g_failures,

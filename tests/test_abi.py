@@ -58,6 +58,8 @@ EXPECTED = {
     "gemm_nvfp4_bf16": "BBBBUUUF",
     "dequant_nvfp4_f32": "BBBUUF",
     "dequant_nvfp4_bf16": "BBBUUF",
+    "rms_norm_f32": "BBBUF",
+    "head_norm_rope_f32": "BBBUUUUFUUUF",
 }
 
 
@@ -71,6 +73,11 @@ def test_registry_names_and_signatures():
     text = HEADER.read_text()
     for k in names:
         assert f"`{k}`" in text or f" {k} " in text or f"{k}:" in text or k in text
+
+
+class FakeArray:
+    """A non-null device address for host-side validation paths that fail first."""
+    ptr = 0x1000
 
 
 class FakeBuffer:
@@ -110,9 +117,27 @@ def test_validate_accepts_the_reference_launch():
 
 
 def test_validate_unknown_kernel():
-    rc = rc_of(lambda: hip.validate_run("rms_norm_f32", matmul_args()))
+    rc = rc_of(lambda: hip.validate_run("attention_f32", matmul_args()))
     assert rc == E_UNKNOWN_KERNEL
-    assert "rms_norm_f32" in hip.lib().apex_hip_last_error().decode()
+    assert "attention_f32" in hip.lib().apex_hip_last_error().decode()
+
+
+def test_validate_accepts_the_reference_norm_launches():
+    # src/ops.h:18-26: Dim3{rows}, 256 threads; src/ops.h:88-118: Dim3{tokens, heads}
+    assert rc_of(lambda: hip.validate_run("rms_norm_f32", [buf(), buf(), buf(), u32(2816),
+                                                           f32(1e-6)], (4,), (256,))) == 0
+    args = [buf(), buf(), buf(), u32(8), u32(256), u32(1), u32(128), f32(1e4), u32(0),
+            u32(2048), u32(256), f32(1e-6)]
+    assert rc_of(lambda: hip.validate_run("head_norm_rope_f32", args, (3, 8), (256,))) == 0
+
+
+def test_head_norm_rope_shape_errors_are_host_checks():
+    """Invalid head shapes are rejected before any device work (no GPU needed)."""
+    fake = FakeArray()
+    for head_dim, pairs in ((255, 0), (1024, 0), (256, 129)):
+        rc = rc_of(lambda: hip.head_norm_rope_f32(fake, fake, fake, 1, 1, head_dim, pairs, 1e4,
+                                                  0, head_dim, head_dim, 1e-6))
+        assert rc == E_INVALID, (head_dim, pairs)
 
 
 def test_validate_wrong_arg_count():

@@ -41,5 +41,6 @@ def test_host_layer_on_gpu():
     assert r.returncode == 0, r.stdout
     assert "FAIL" not in r.stdout
     for name in ("denseMlp fp32 (4 launches) vs oracle", "denseMlpFused fp32 (2 launches) vs oracle",
-                 "matmulNvfp4Bf16 T=96", "moeFfn vs oracle", "unknown kernel throws"):
+                 "matmulNvfp4Bf16 T=96", "moeFfn vs oracle", "rmsNorm vs oracle",
+                 "headNormRope vs oracle", "unknown kernel throws"):
         assert f"PASS {name}" in r.stdout

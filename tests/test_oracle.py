@@ -380,3 +380,98 @@ def test_bf16_rounding():
     torch = pytest.importorskip("torch")
     t = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got, t)
+
+
+# ---- RMSNorm and per-head RMSNorm + RoPE -------------------------------------------
+
+def test_rms_norm_golden_from_reference():
+    """orc_rms_norm against the reference's rmsNormCpu outputs, bit for bit."""
+    g = load("rms_norm.npz")
+    n = len([k for k in g.files if k.endswith("_y")])
+    assert n >= 4
+    for i in range(n):
+        got = oracle.rms_norm(g[f"c{i}_x"], g[f"c{i}_w"], float(g[f"c{i}_eps"]))
+        assert np.array_equal(got.view(np.uint32), g[f"c{i}_y"].view(np.uint32)), f"case {i}"
+
+
+def test_rms_norm_matches_compiled_reference_live():
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref not built (reference not mounted)")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 2112)).astype(np.float32)
+    w = synth.bf16_from_f32(rng.standard_normal(2112).astype(np.float32))
+    a, b = oracle.rms_norm(x, w, 1e-6), oracle.ref_rms_norm(x, w, 1e-6)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_rms_norm_power_of_two_scale_invariance():
+    """With eps = 0, scaling a row by 2 scales ss by 4 exactly and inv by 1/2 exactly:
+    the output is bit-identical (a dropped square, a wrong mean or a missing weight
+    would break it or the golden test)."""
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((3, 333)).astype(np.float32)
+    w = synth.bf16_from_f32(rng.standard_normal(333).astype(np.float32))
+    a, b = oracle.rms_norm(x, w, 0.0), oracle.rms_norm(2 * x, w, 0.0)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # unit weights: every row has mean square 1
+    ones = synth.bf16_from_f32(np.ones(333, np.float32))
+    y = oracle.rms_norm(x, ones, 0.0).astype(np.float64)
+    assert np.allclose(np.mean(y * y, axis=1), 1.0, rtol=1e-6)
+
+
+def _rope_case(seed, T=3, heads=2, D=16):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, heads, D)).astype(np.float32)
+    w = synth.bf16_from_f32((1.0 + 0.2 * rng.standard_normal(D)).astype(np.float32))
+    return x, w
+
+
+def test_head_norm_rope_without_rotation_is_rms_norm_per_head():
+    """rope_pairs = 0, or the rotation at position 0 (angle 0), reduce to rmsNormCpu on
+    every head: bit-identical to orc_rms_norm (itself pinned to the reference)."""
+    x, w = _rope_case(1)
+    T, Hh, D = x.shape
+    want = oracle.rms_norm(x.reshape(T * Hh, D), w, 1e-6).ravel()
+    got = oracle.head_norm_rope(x, w, 0, 10000.0, 5, 1e-6)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    got0 = oracle.head_norm_rope(x[:1], w, D // 2, 10000.0, 0, 1e-6)
+    assert np.array_equal(got0.view(np.uint32), want[: Hh * D].view(np.uint32))
+    # no learned weights: unit scaling
+    ones = synth.bf16_from_f32(np.ones(D, np.float32))
+    want1 = oracle.rms_norm(x.reshape(T * Hh, D), ones, 1e-6).ravel()
+    got1 = oracle.head_norm_rope(x, None, 0, 10000.0, 5, 1e-6, has_weight=False)
+    assert np.array_equal(got1.view(np.uint32), want1.view(np.uint32))
+
+
+def test_head_norm_rope_rotation_angles_and_pairing():
+    """The rotation of pair i (elements i and D/2 + i, shaders/head_norm_rope.metal:
+    50-66) recovered from the output by atan2 equals (abs_pos + t) * base^(-2 i / D)
+    computed here in fp64, for the rotated pairs; the other pairs are untouched and
+    every pair keeps its norm.  Interleaved pairing, a sign flip, i / D instead of
+    2 i / D or a missing token offset all fail this."""
+    x, w = _rope_case(2, T=3, heads=2, D=16)
+    T, Hh, D = x.shape
+    half, pairs, base, pos0 = D // 2, 6, 500.0, 9
+    n = oracle.head_norm_rope(x, w, 0, base, pos0, 1e-6).reshape(T, Hh, D).astype(np.float64)
+    r = oracle.head_norm_rope(x, w, pairs, base, pos0, 1e-6).reshape(T, Hh, D).astype(np.float64)
+    for t in range(T):
+        for i in range(half):
+            a, b = n[:, :, i][t], n[:, :, half + i][t]
+            c, d = r[:, :, i][t], r[:, :, half + i][t]
+            assert np.allclose(np.hypot(a, b), np.hypot(c, d), rtol=1e-6)
+            theta = np.arctan2(a * d - b * c, a * c + b * d)
+            want = (pos0 + t) * base ** (-2.0 * i / D) if i < pairs else 0.0
+            want = math.remainder(want, 2 * math.pi)
+            assert np.allclose(theta, want, atol=2e-5), (t, i, theta, want)
+
+
+def test_head_norm_rope_output_strides():
+    """Head (t, h) lands at t * out_token_stride + h * out_head_stride."""
+    x, w = _rope_case(3, T=2, heads=3, D=8)
+    T, Hh, D = x.shape
+    dense = oracle.head_norm_rope(x, w, 4, 100.0, 1, 1e-6).reshape(T, Hh, D)
+    ts, hs = 40, 12
+    out = oracle.head_norm_rope(x, w, 4, 100.0, 1, 1e-6, out_token_stride=ts, out_head_stride=hs)
+    for t in range(T):
+        for h in range(Hh):
+            assert np.array_equal(out[t * ts + h * hs: t * ts + h * hs + D], dense[t, h])
