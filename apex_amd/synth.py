@@ -119,6 +119,19 @@ def gemv_case(seed: int = 0, tokens: int = 1, rows: int = 2048, K: int = 2048):
     return x, w
 
 
+def dense_mlp_case(seed: int = 0, tokens: int = 1, H: int = 2816, I: int = 2112):
+    """Gemma dense MLP block (tools/out.txt:121-186 shapes): residual input h fp32 [T,H]
+    ~N(0,1), pre-FFN RMSNorm weights bf16 [H] ~1+0.1N(0,1), gate/up NVFP4 [I,H], down
+    NVFP4 [H,I].  Draws: h, norm weights, gate, up, down."""
+    rng = np.random.default_rng(seed)
+    h = rng.standard_normal((tokens, H), dtype=np.float32)
+    norm_w = bf16_from_f32((1.0 + 0.1 * rng.standard_normal(H, dtype=np.float32)).astype(np.float32))
+    gate = nvfp4_weights(rng, I, H)
+    up = nvfp4_weights(rng, I, H)
+    down = nvfp4_weights(rng, H, I)
+    return h, norm_w, gate, up, down
+
+
 def geglu_case(seed: int = 0, tokens: int = 1, rows: int = 21504, K: int = 5376):
     """Decode fused GeGLU.  Draws: x [T,K], gate W, up W."""
     rng = np.random.default_rng(seed)

@@ -280,6 +280,50 @@ def time_norms(steps, warmup, T=4096, H=2816, heads=16, D=256):
     return out
 
 
+def time_dense_mlp_decode(steps, warmup, H=2816, I=2112):
+    """The Gemma dense MLP block at batch 1 (fp32 activations, the reference contract):
+    rms_norm_f32 -> fused gate/up GeGLU GEMV -> down GEMV, 3 launches per token, weights
+    rotated over enough copies to exceed the MALL.  Algorithmic bytes per token: the
+    three NVFP4 matrices plus the activations each kernel reads and writes."""
+    h, nw, g, u, d = synth.dense_mlp_case(seed=0, tokens=1, H=H, I=I)
+    mats = (g.codes, g.scales, u.codes, u.scales, d.codes, d.scales)
+    w_bytes = sum(a.nbytes for a in mats)
+    act = (2 * H * 4 + H * 2) + (H * 4 + I * 4) + (I * 4 + H * 4)
+    algo = w_bytes + act
+    copies = max(4, int(np.ceil(2.5 * MALL_BYTES / w_bytes)))
+    base = [hip.DeviceArray.from_numpy(a) for a in mats]
+    sets = [base]
+    for _ in range(copies - 1):
+        s = [hip.DeviceArray(a.shape, a.dtype) for a in base]
+        for dd, b in zip(s, base):
+            dd.copy_from(b)
+        sets.append(s)
+    dh, dnw = hip.DeviceArray.from_numpy(h), hip.DeviceArray.from_numpy(nw)
+    xn, hh, y = (hip.DeviceArray((1, H), np.float32), hip.DeviceArray((1, I), np.float32),
+                 hip.DeviceArray((1, H), np.float32))
+    stream = hip.Stream()
+
+    def step(i):
+        gc, gs, uc, us, dc, ds = sets[i % copies]
+        hip.rms_norm_f32(dh, dnw, xn, 1, H, 1e-6, stream=stream)
+        hip.nvfp4_geglu_f32(xn, gc, gs, uc, us, hh, 1, I, H, stream=stream)
+        hip.nvfp4_matmul_f32(hh, dc, ds, y, 1, H, I, stream=stream)
+
+    sec = time_steps(step, steps, warmup, stream)
+    stream.close()
+    for arrs in sets:
+        for a in arrs:
+            a.close()
+    for a in (dh, dnw, xn, hh, y):
+        a.close()
+    gbs = algo / sec / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(sec * 1e3, 6),
+            "roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(algo),
+            "weight_copies_rotated": copies,
+            "workload": f"dense MLP decode, batch 1, fp32: rms_norm [1,{H}] -> fused GeGLU "
+                        f"NVFP4 [{I}x{H}] x2 -> down NVFP4 [{H}x{I}] (3 launches)"}
+
+
 def vendor_bf16_gemm(M, N, K, steps, warmup):
     """Context for the GEMM line: the vendor library's plain bf16 GEMM of the same shape
     (torch -> hipBLASLt, weights already bf16, no FP4 decode).  Not part of the path."""
@@ -341,7 +385,8 @@ def main(argv=None):
                     help="time only the headline fused-GeGLU workload")
     ap.add_argument("--calibrate", action="store_true",
                     help="run the known-size read and copy kernels first (counter scaling)")
-    ap.add_argument("--only", choices=["moe_prefill", "gemm_prefill", "moe_decode", "norms"],
+    ap.add_argument("--only", choices=["moe_prefill", "gemm_prefill", "moe_decode", "norms",
+                                       "dense_mlp_decode"],
                     help="profiling aid: time one secondary workload and print its record only")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -353,7 +398,8 @@ def main(argv=None):
         calibrate()
     if args.only:
         fn = {"moe_prefill": time_moe_prefill, "gemm_prefill": time_gemm_prefill,
-              "moe_decode": time_moe_decode, "norms": time_norms}[args.only]
+              "moe_decode": time_moe_decode, "norms": time_norms,
+              "dense_mlp_decode": time_dense_mlp_decode}[args.only]
         print(json.dumps({args.only: fn(args.steps, args.warmup)}), flush=True)
         return 0
     r = time_geglu(args.steps, args.warmup)
@@ -397,6 +443,8 @@ def main(argv=None):
             "moe_decode": time_moe_decode(max(1, args.steps // 10), max(1, args.warmup // 10)),
         }
         line["secondary"].update(time_norms(max(1, args.steps // 10), max(1, args.warmup // 10)))
+        line["secondary"]["dense_mlp_decode"] = time_dense_mlp_decode(
+            max(1, args.steps // 10), max(1, args.warmup // 10))
     if not args.no_cpu:
         cb = cpu_baseline_geglu(args.cpu_budget)
         cb.pop("_h")
