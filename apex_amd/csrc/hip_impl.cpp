@@ -156,18 +156,23 @@ bool moe_use_gemm(uint32_t T, uint32_t k, uint32_t H, uint32_t I) {
              H <= 3072 && I <= 1024);
 }
 
-void moe_impl(const uint16_t *x, const uint16_t *logits, const apex_moe_slots *slots, uint16_t *y,
-              uint32_t T, uint32_t E, uint32_t k, uint32_t H, uint32_t I, void *ws,
-              size_t ws_bytes, hipStream_t stream) {
+// Router logits arrive as bf16 (`logits`) or fp32 (`logits_f32`, with an optional
+// bf16 per-expert scale on the routing weights); exactly one is given.
+void moe_impl(const uint16_t *x, const uint16_t *logits, const float *logits_f32,
+              const uint16_t *pes, const apex_moe_slots *slots, uint16_t *y, uint32_t T,
+              uint32_t E, uint32_t k, uint32_t H, uint32_t I, void *ws, size_t ws_bytes,
+              hipStream_t stream) {
     require(slots != nullptr, "moe_ffn: slots is null");
     if (T == 0)
         return;
-    require(x && logits && slots->base && y && ws, "moe_ffn: null pointer");
+    require(x && (logits || logits_f32) && slots->base && y && ws, "moe_ffn: null pointer");
     init_device_tuning();
     const bool gemm = moe_use_gemm(T, k, H, I);
     apex_hip::MoeArgs a{};
     a.x = x;
     a.logits = logits;
+    a.logits_f32 = logits_f32;
+    a.pes = pes;
     a.slots = {static_cast<const uint8_t *>(slots->base), slots->stride, slots->gate_w,
                slots->gate_s, slots->up_w, slots->up_s, slots->down_w, slots->down_s};
     a.y = y;
@@ -201,6 +206,28 @@ void moe_route_impl(const uint16_t *logits, uint32_t T, uint32_t E, uint32_t k, 
     require(k >= 1 && k <= apex_hip::kMoeMaxTopK && k <= E,
             "moe_route: top_k must be in [1, min(16, experts)]");
     hip_check(apex_hip::moe_route_launch(logits, T, E, k, ids, w, stream), "moe_route launch");
+}
+
+void route_f32_impl(const float *logits, const uint16_t *pes, uint32_t T, uint32_t E, uint32_t k,
+                    int32_t *ids, float *w, hipStream_t stream) {
+    if (T == 0)
+        return;
+    require(logits && ids && w, "moe_route: null pointer");
+    require(E >= 1 && E <= apex_hip::kMoeMaxExperts, "moe_route: experts must be in [1, 256]");
+    require(k >= 1 && k <= apex_hip::kMoeMaxTopK && k <= E,
+            "moe_route: top_k must be in [1, min(16, experts)]");
+    hip_check(apex_hip::moe_route_f32_launch(logits, pes, T, E, k, ids, w, stream),
+              "moe_route launch");
+}
+
+void router_impl(const apex_hip::MoeRouterArgs &a, hipStream_t stream) {
+    if (a.T == 0)
+        return;
+    require(a.h && a.norm_w && a.qw && a.qs && a.qb && a.logits, "moe_router: null pointer");
+    const char *why = nullptr;
+    if (!apex_hip::moe_router_supported(a, &why))
+        fail(APEX_HIP_E_INVALID, std::string("moe_router: ") + why);
+    hip_check(apex_hip::moe_router_logits_launch(a, stream), "moe_router launch");
 }
 
 } // namespace
@@ -424,8 +451,54 @@ void launch_moe_ffn(const LaunchCtx &c) {
     need(c, 1, (uint64_t)T * E * 2, "moe_ffn logits");
     need(c, 2, (uint64_t)E * s.stride, "moe_ffn expert slots");
     need(c, 3, (uint64_t)T * H * 2, "moe_ffn output");
-    moe_impl((const uint16_t *)c.ptr[0], (const uint16_t *)c.ptr[1], &s, (uint16_t *)c.ptr[3], T, E,
-             k, H, I, c.ptr[4], c.avail[4], c.stream);
+    moe_impl((const uint16_t *)c.ptr[0], (const uint16_t *)c.ptr[1], nullptr, nullptr, &s,
+             (uint16_t *)c.ptr[3], T, E, k, H, I, c.ptr[4], c.avail[4], c.stream);
+}
+
+// moe_ffn_f32logits_nvfp4_bf16: x, fp32 logits, per-expert scale, expert slots, y,
+// workspace; T, E, k, H, I; slot stride and the six piece offsets; has_scale.
+void launch_moe_ffn_f32logits(const LaunchCtx &c) {
+    const uint32_t T = c.u[6], E = c.u[7], k = c.u[8], H = c.u[9], I = c.u[10];
+    const bool has_pes = c.u[18] != 0;
+    apex_moe_slots s{c.ptr[3], c.u[11], c.u[12], c.u[13], c.u[14], c.u[15], c.u[16], c.u[17]};
+    need(c, 0, (uint64_t)T * H * 2, "moe_ffn x");
+    need(c, 1, (uint64_t)T * E * 4, "moe_ffn logits");
+    if (has_pes)
+        need(c, 2, (uint64_t)E * 2, "moe_ffn per-expert scale");
+    need(c, 3, (uint64_t)E * s.stride, "moe_ffn expert slots");
+    need(c, 4, (uint64_t)T * H * 2, "moe_ffn output");
+    moe_impl((const uint16_t *)c.ptr[0], nullptr, (const float *)c.ptr[1],
+             has_pes ? (const uint16_t *)c.ptr[2] : nullptr, &s, (uint16_t *)c.ptr[4], T, E, k, H, I,
+             c.ptr[5], c.avail[5], c.stream);
+}
+
+// moe_router_logits_q8_f32: h, router.scale, proj weights, scales, biases, logits; T, E,
+// H, eps (docs/B6_3_attention.md:721-725).
+void launch_moe_router(const LaunchCtx &c) {
+    const uint32_t T = c.u[6], E = c.u[7], H = c.u[8];
+    need(c, 0, (uint64_t)T * H * 4, "moe_router hidden");
+    need(c, 1, (uint64_t)H * 2, "moe_router norm weights");
+    need(c, 2, (uint64_t)E * H, "moe_router weights");
+    need(c, 3, (uint64_t)E * (H / 64) * 2, "moe_router scales");
+    need(c, 4, (uint64_t)E * (H / 64) * 2, "moe_router biases");
+    need(c, 5, (uint64_t)T * E * 4, "moe_router logits");
+    router_impl({(const float *)c.ptr[0], (const uint16_t *)c.ptr[1], c.f[9],
+                 (const uint32_t *)c.ptr[2], (const uint16_t *)c.ptr[3],
+                 (const uint16_t *)c.ptr[4], T, E, H, (float *)c.ptr[5]},
+                c.stream);
+}
+
+// moe_route_f32: fp32 logits, per-expert scale, ids, weights; T, E, k, has_scale.
+void launch_moe_route_f32(const LaunchCtx &c) {
+    const uint32_t T = c.u[4], E = c.u[5], k = c.u[6];
+    const bool has_pes = c.u[7] != 0;
+    need(c, 0, (uint64_t)T * E * 4, "moe_route logits");
+    if (has_pes)
+        need(c, 1, (uint64_t)E * 2, "moe_route per-expert scale");
+    need(c, 2, (uint64_t)T * k * 4, "moe_route ids");
+    need(c, 3, (uint64_t)T * k * 4, "moe_route weights");
+    route_f32_impl((const float *)c.ptr[0], has_pes ? (const uint16_t *)c.ptr[1] : nullptr, T, E, k,
+                   (int32_t *)c.ptr[2], (float *)c.ptr[3], c.stream);
 }
 
 void launch_moe_route(const LaunchCtx &c) {
@@ -450,6 +523,10 @@ const KernelSpec kKernels[] = {
     {"moe_route_bf16", "BBBUUU", (1u << 1) | (1u << 2), launch_moe_route},
     {"rms_norm_f32", "BBBUF", 1u << 2, launch_rms_norm},
     {"head_norm_rope_f32", "BBBUUUUFUUUF", 1u << 2, launch_head_norm_rope},
+    {"moe_router_logits_q8_f32", "BBBBBBUUUF", 1u << 5, launch_moe_router},
+    {"moe_route_f32", "BBBBUUUU", (1u << 2) | (1u << 3), launch_moe_route_f32},
+    {"moe_ffn_f32logits_nvfp4_bf16", "BBBBBBUUUUUUUUUUUUU", (1u << 4) | (1u << 5),
+     launch_moe_ffn_f32logits},
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -918,8 +995,40 @@ int apex_moe_ffn_bf16(const uint16_t *x, const uint16_t *logits, const apex_moe_
                       uint32_t hidden, uint32_t inter, void *workspace, size_t workspace_bytes,
                       void *stream) {
     return guard([&] {
-        moe_impl(x, logits, slots, y, tokens, experts, top_k, hidden, inter, workspace,
-                 workspace_bytes, as_stream(stream));
+        moe_impl(x, logits, nullptr, nullptr, slots, y, tokens, experts, top_k, hidden, inter,
+                 workspace, workspace_bytes, as_stream(stream));
+    });
+}
+
+int apex_moe_ffn_f32logits_bf16(const uint16_t *x, const float *logits,
+                                const uint16_t *per_expert_scale, const apex_moe_slots *slots,
+                                uint16_t *y, uint32_t tokens, uint32_t experts, uint32_t top_k,
+                                uint32_t hidden, uint32_t inter, void *workspace,
+                                size_t workspace_bytes, void *stream) {
+    return guard([&] {
+        require(logits != nullptr || tokens == 0, "moe_ffn: null pointer");
+        moe_impl(x, nullptr, logits, per_expert_scale, slots, y, tokens, experts, top_k, hidden,
+                 inter, workspace, workspace_bytes, as_stream(stream));
+    });
+}
+
+int apex_moe_route_f32(const float *logits, const uint16_t *per_expert_scale, uint32_t tokens,
+                       uint32_t experts, uint32_t top_k, int32_t *ids, float *weights,
+                       void *stream) {
+    return guard([&] {
+        route_f32_impl(logits, per_expert_scale, tokens, experts, top_k, ids, weights,
+                       as_stream(stream));
+    });
+}
+
+int apex_moe_router_logits_q8(const float *h, const uint16_t *norm_weights, float eps,
+                              const uint32_t *proj_weights, const uint16_t *proj_scales,
+                              const uint16_t *proj_biases, uint32_t tokens, uint32_t experts,
+                              uint32_t hidden, float *logits, void *stream) {
+    return guard([&] {
+        router_impl({h, norm_weights, eps, proj_weights, proj_scales, proj_biases, tokens, experts,
+                     hidden, logits},
+                    as_stream(stream));
     });
 }
 

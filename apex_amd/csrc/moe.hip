@@ -113,17 +113,19 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
-// Top-k of one token's E logits (E <= 256) by wave 0..63 lanes, then softmax over the
-// k; lane j < k returns slot j's expert id and weight.  Keys order by logit, then by
-// lower expert id (the reference tie-break), and are unique per expert.
-__device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, uint32_t k,
-                                            int lane, int32_t &my_id, float &my_w) {
+// Top-k of one token's E logits (E <= 256; logit(e) returns expert e's as fp32) by wave
+// lanes 0..63, then softmax over the k; lane j < k returns slot j's expert id and
+// weight.  Keys order by logit, then by lower expert id (the reference tie-break), and
+// are unique per expert.
+template <typename Logit>
+__device__ __forceinline__ void route_token_by(Logit logit, uint32_t E, uint32_t k, int lane,
+                                               int32_t &my_id, float &my_w) {
     uint64_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t e = lane + 64 * q;
         if (e < E) {
-            const uint32_t u = (uint32_t)logits[e] << 16;
+            const uint32_t u = __float_as_uint(logit(e));
             const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
             key[q] = ((uint64_t)ord << 32) | (0xFFFFFFFFu - e);
         } else {
@@ -155,6 +157,210 @@ __device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, 
     for (int o = 32; o >= 1; o >>= 1)
         z += __shfl_xor(z, o, 64);
     my_w = p / z;
+}
+
+// route_token_by over one token's bf16 logits.
+__device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, uint32_t k,
+                                            int lane, int32_t &my_id, float &my_w) {
+    route_token_by([&](uint32_t e) { return __uint_as_float((uint32_t)logits[e] << 16); }, E, k,
+                   lane, my_id, my_w);
+}
+
+// Token t of the FFN's logits (fp32 when given, else bf16); lane j < k's weight times
+// the per-expert scale of its expert when one is given.
+__device__ __forceinline__ void route_token_args(const MoeArgs &a, uint32_t t, int lane,
+                                                 int32_t &id, float &wt) {
+    if (a.logits_f32) {
+        const float *l = a.logits_f32 + (size_t)t * a.E;
+        route_token_by([&](uint32_t e) { return l[e]; }, a.E, a.k, lane, id, wt);
+    } else {
+        route_token(a.logits + (size_t)t * a.E, a.E, a.k, lane, id, wt);
+    }
+    if (a.pes && (uint32_t)lane < a.k)
+        wt *= bf16_bits_to_f32(a.pes[id]);
+}
+
+__global__ __launch_bounds__(256) void moe_route_f32_kernel(const float *logits,
+                                                            const uint16_t *pes, uint32_t T,
+                                                            uint32_t E, uint32_t k, int32_t *ids,
+                                                            float *w) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T)
+        return;
+    int32_t id;
+    float wt;
+    const float *l = logits + (size_t)t * E;
+    route_token_by([&](uint32_t e) { return l[e]; }, E, k, lane, id, wt);
+    if ((uint32_t)lane < k) {
+        ids[(size_t)t * k + lane] = id;
+        w[(size_t)t * k + lane] = pes ? wt * bf16_bits_to_f32(pes[id]) : wt;
+    }
+}
+
+// Router logits (MoeRouterArgs): one workgroup of WAVES waves per tile of TT tokens.
+// The tile's normalised rows xn = h * inv * w (the rmsNormCpu order) and their
+// per-group sums go to LDS once.  Lane l owns experts l, l + 64, ... (EPL of them) and
+// the waves split the 64-element groups of K, so each activation read is an LDS
+// broadcast feeding 4 * EPL FMAs per token; the next group's codes are loaded while
+// the current one is used.  Per group g:
+//   logit[t][e] += scale[e][g] * sum_k xn[t][k] q[e][k] + bias[e][g] * sum_k xn[t][k]
+// in fp32 (w = scale * q + bias expanded, the bias term from the shared group sum);
+// the waves' partial logits are summed in wave order.
+constexpr uint32_t kQGroup = 64;
+constexpr size_t kMaxDynLds = 160 * 1024 - 256; // a CU's LDS, less the static arrays
+
+template <int TT, int EPL, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void moe_router_kernel(MoeRouterArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float rsm[];
+    __shared__ float inv_s[TT];
+    const uint32_t H = a.H, E = a.E, NG = H / kQGroup;
+    float *xn = rsm;                     // [TT][H]
+    float *gsum = xn + TT * H;           // [TT][NG]
+    float *part = gsum + TT * NG;        // [WAVES][TT][E]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t0 = blockIdx.x * TT;
+    const uint32_t nt = a.T - t0 < (uint32_t)TT ? a.T - t0 : (uint32_t)TT;
+    // the first group's codes and scales do not depend on h: in flight from the start
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
+    uint32_t row[EPL]; // byte offset of each owned expert's codes (out of range if none)
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const uint32_t e = lane + 64 * j;
+        row[j] = e < E ? e * H : kOutOfRange;
+    }
+    const uint32_t g0 = wave * NG / WAVES, g1 = (wave + 1) * NG / WAVES;
+    float acc[EPL][TT];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+            acc[j][t] = 0.0f;
+    u32x4_t q4[EPL][4], nq[EPL][4];
+    uint32_t sb[EPL], nsb[EPL]; // bf16 scale (low half) and bias (high half) of the group
+    auto load_group = [&](u32x4_t (&dst)[EPL][4], uint32_t (&dsb)[EPL], uint32_t g) {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                dst[j][i] = load_b128(rq, row[j] == kOutOfRange ? kOutOfRange : row[j] + g * kQGroup + 16 * i);
+            const uint32_t e = lane + 64 * j;
+            const uint32_t er = e < E ? e : E - 1;
+            dsb[j] = (uint32_t)a.qs[(size_t)er * NG + g] | ((uint32_t)a.qb[(size_t)er * NG + g] << 16);
+        }
+    };
+    if (g0 < g1)
+        load_group(nq, nsb, g0);
+    // the tile's rows into LDS (16-byte loads, a batch in flight per thread), then the
+    // sums of squares and the scaling from there
+    {
+        const __amdgpu_buffer_rsrc_t rh = make_rsrc(a.h + (size_t)t0 * H, nt * H * 4);
+        constexpr int kBatch = 4;
+        const uint32_t n4 = TT * H / 4;
+        for (uint32_t i0 = threadIdx.x; i0 < n4; i0 += kBatch * blockDim.x) {
+            u32x4_t v[kBatch];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const uint32_t i = i0 + b * blockDim.x;
+                v[b] = load_b128(rh, i < n4 ? i * 16 : kOutOfRange); // rows past nt read 0
+            }
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const uint32_t i = i0 + b * blockDim.x;
+                if (i < n4)
+                    *reinterpret_cast<u32x4_t *>(xn + 4 * i) = v[b];
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t t = wave; t < (uint32_t)TT; t += WAVES) {
+        float ss = 0.0f;
+        for (uint32_t i = lane; i < H; i += 64)
+            ss += xn[t * H + i] * xn[t * H + i];
+        ss = group_sum<64>(ss);
+        if (lane == 0)
+            inv_s[t] = t < nt ? 1.0f / sqrtf(ss / (float)H + a.eps) : 0.0f;
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < TT * H; i += blockDim.x)
+        xn[i] = xn[i] * inv_s[i / H] * bf16_bits_to_f32(a.norm_w[i % H]);
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < TT * NG; i += blockDim.x) {
+        const float *r = xn + (i / NG) * H + (i % NG) * kQGroup;
+        float sum = 0.0f;
+        for (uint32_t j = 0; j < kQGroup; ++j)
+            sum += r[j];
+        gsum[i] = sum;
+    }
+    __syncthreads();
+    for (uint32_t g = g0; g < g1; ++g) {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                q4[j][i] = nq[j][i];
+            sb[j] = nsb[j];
+        }
+        if (g + 1 < g1)
+            load_group(nq, nsb, g + 1);
+        float aq[EPL][TT];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j)
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+                aq[j][t] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            float q[EPL][4];
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                const uint32_t wv = q4[j][w / 4][w % 4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    q[j][b] = (float)((wv >> (8 * b)) & 0xFFu);
+            }
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const float4 xv = *reinterpret_cast<const float4 *>(xn + t * H + g * kQGroup + 4 * w);
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) {
+                    aq[j][t] = __builtin_fmaf(xv.x, q[j][0], aq[j][t]);
+                    aq[j][t] = __builtin_fmaf(xv.y, q[j][1], aq[j][t]);
+                    aq[j][t] = __builtin_fmaf(xv.z, q[j][2], aq[j][t]);
+                    aq[j][t] = __builtin_fmaf(xv.w, q[j][3], aq[j][t]);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const float sc = __uint_as_float(sb[j] << 16);
+            const float bi = __uint_as_float(sb[j] & 0xFFFF0000u);
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+                acc[j][t] += sc * aq[j][t] + bi * gsum[t * NG + g];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const uint32_t e = lane + 64 * j;
+        if (e < E)
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+                part[(wave * TT + t) * E + e] = acc[j][t];
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nt * E; i += blockDim.x) {
+        const uint32_t t = i / E, e = i % E;
+        float v = 0.0f;
+        for (int w = 0; w < WAVES; ++w)
+            v += part[(w * TT + t) * E + e];
+        a.logits[(size_t)(t0 + t) * E + e] = v;
+    }
+}
+
+template <int TT, int WAVES> size_t router_lds(const MoeRouterArgs &a) {
+    const uint32_t NG = a.H / kQGroup;
+    return 4 * ((size_t)TT * a.H + (size_t)TT * NG + (size_t)WAVES * TT * a.E);
 }
 
 __global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *logits, uint32_t T,
@@ -329,7 +535,7 @@ __global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
         const uint32_t t = t0 + tl;
         int32_t id;
         float wt;
-        route_token(a.logits + (size_t)t * E, E, k, lane, id, wt);
+        route_token_args(a, t, lane, id, wt);
         if ((uint32_t)lane < k) {
             a.ids[(size_t)t * k + lane] = id;
             a.w[(size_t)t * k + lane] = wt;
@@ -446,7 +652,7 @@ __global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
     for (uint32_t t = wave; t < a.T; t += blockDim.x / 64) {
         int32_t id;
         float wt;
-        route_token(a.logits + (size_t)t * a.E, a.E, a.k, lane, id, wt);
+        route_token_args(a, t, lane, id, wt);
         if ((uint32_t)lane < a.k) {
             a.ids[t * a.k + lane] = id;
             a.w[t * a.k + lane] = wt;
@@ -927,6 +1133,66 @@ hipError_t moe_route_launch(const uint16_t *logits, uint32_t T, uint32_t E, uint
     hipLaunchKernelGGL(moe_route_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, logits, T, E, k,
                        ids, w);
     return hipGetLastError();
+}
+
+hipError_t moe_route_f32_launch(const float *logits, const uint16_t *pes, uint32_t T, uint32_t E,
+                                uint32_t k, int32_t *ids, float *w, hipStream_t stream) {
+    if (T == 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(moe_route_f32_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, logits, pes,
+                       T, E, k, ids, w);
+    return hipGetLastError();
+}
+
+bool moe_router_supported(const MoeRouterArgs &a, const char **why) {
+    auto no = [&](const char *m) {
+        *why = m;
+        return false;
+    };
+    if (a.E == 0 || a.E > kMoeMaxExperts)
+        return no("experts must be in [1, 256]");
+    if (a.H == 0 || a.H % kQGroup || a.H > kRouterMaxHidden)
+        return no("hidden must be a positive multiple of 64, at most 4096");
+    if ((uint64_t)a.E * a.H >= (1ull << 31))
+        return no("router weights must be below 2 GiB");
+    if ((uintptr_t)a.qw % 16)
+        return no("router weights must be 16-byte aligned");
+    return true;
+}
+
+template <int TT, int EPL, int WAVES>
+hipError_t router_launch(const MoeRouterArgs &a, hipStream_t stream) {
+    static bool set = false;
+    const size_t lds = router_lds<TT, WAVES>(a);
+    hipError_t e = set_lds(moe_router_kernel<TT, EPL, WAVES>, lds, set);
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL((moe_router_kernel<TT, EPL, WAVES>), dim3((a.T + TT - 1) / TT),
+                       dim3(64 * WAVES), lds, stream, a);
+    return hipGetLastError();
+}
+
+template <int TT, int WAVES>
+hipError_t router_launch_epl(const MoeRouterArgs &a, hipStream_t stream) {
+    switch ((a.E + 63) / 64) {
+    case 1: return router_launch<TT, 1, WAVES>(a, stream);
+    case 2: return router_launch<TT, 2, WAVES>(a, stream);
+    case 3: return router_launch<TT, 3, WAVES>(a, stream);
+    default: // 4 experts per lane: at most 8 waves, or the registers spill
+        return router_launch<TT, 4, (WAVES > 8 ? 8 : WAVES)>(a, stream);
+    }
+}
+
+hipError_t moe_router_logits_launch(const MoeRouterArgs &a, hipStream_t stream) {
+    if (a.T == 0)
+        return hipSuccess;
+    // few tokens: one token per workgroup of 16 waves (parallelism over tokens and K);
+    // many: tiles of 8 (or, for the widest shapes, 4) tokens share the weight reads
+    if (a.T <= 256)
+        return router_launch_epl<1, 16>(a, stream);
+    if (router_lds<8, 8>(a) <= kMaxDynLds)
+        return router_launch_epl<8, 8>(a, stream);
+    return router_launch_epl<4, 8>(a, stream);
 }
 
 hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {

@@ -100,6 +100,10 @@ _PROTOS = {
     "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
     "apex_hip_set_moe_path": (_I, [_I]),
     "apex_rms_norm_f32": (_I, [_P, _P, _P, _U32, _U32, _F, _P]),
+    "apex_moe_router_logits_q8": (_I, [_P, _P, _F, _P, _P, _P, _U32, _U32, _U32, _P, _P]),
+    "apex_moe_route_f32": (_I, [_P, _P, _U32, _U32, _U32, _P, _P, _P]),
+    "apex_moe_ffn_f32logits_bf16": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P,
+                                         _SZ, _P]),
     "apex_head_norm_rope_f32": (_I, [_P, _P, _I, _P, _U32, _U32, _U32, _U32, _F, _U32, _U32, _U32,
                                      _F, _P]),
 }
@@ -315,6 +319,27 @@ def moe_slots(base: DeviceArray, stride: int, offsets: dict) -> MoeSlots:
 def moe_route_bf16(logits, ids, weights, tokens, experts, top_k, stream=None):
     check(lib().apex_moe_route_bf16(logits.ptr, tokens, experts, top_k, ids.ptr, weights.ptr,
                                     _s(stream)))
+
+
+def moe_router_logits_q8(h, norm_w, proj_w, proj_s, proj_b, logits, tokens, experts, hidden,
+                         eps=1e-6, stream=None):
+    check(lib().apex_moe_router_logits_q8(h.ptr, norm_w.ptr, eps, proj_w.ptr, proj_s.ptr,
+                                          proj_b.ptr, tokens, experts, hidden, logits.ptr,
+                                          _s(stream)))
+
+
+def moe_route_f32(logits, per_expert_scale, ids, weights, tokens, experts, top_k, stream=None):
+    check(lib().apex_moe_route_f32(logits.ptr, per_expert_scale.ptr if per_expert_scale is not None
+                                   else None, tokens, experts, top_k, ids.ptr, weights.ptr,
+                                   _s(stream)))
+
+
+def moe_ffn_f32logits_bf16(x, logits, per_expert_scale, slots: "MoeSlots", y, tokens, experts,
+                           top_k, hidden, inter, workspace, stream=None):
+    check(lib().apex_moe_ffn_f32logits_bf16(
+        x.ptr, logits.ptr, per_expert_scale.ptr if per_expert_scale is not None else None,
+        C.byref(slots), y.ptr, tokens, experts, top_k, hidden, inter, workspace.ptr,
+        workspace.nbytes, _s(stream)))
 
 
 def moe_workspace_bytes(tokens, experts, top_k, hidden, inter) -> int:

@@ -155,4 +155,52 @@ inline void moeFfn(Backend &backend, Buffer *x, Buffer *logits, const ExpertSlot
                 Dim3{1}, Dim3{256});
 }
 
+// Gemma-4 router (docs/B6_3_attention.md:721-725), the tensors of tools/out.txt:247-290:
+// router.scale (RMSNorm weights, bf16 [hidden]), router.proj (affine 8-bit: u32 codes
+// [experts, hidden/4], bf16 scales and biases [experts, hidden/64]) and
+// router.per_expert_scale (bf16 [experts]), each at an offset in a weights buffer.
+struct RouterWeights {
+    Buffer *buffer;
+    size_t norm_offset, codes_offset, scales_offset, biases_offset, per_expert_scale_offset;
+    uint32_t experts, hidden;
+};
+
+// Router logits fp32 [tokens, experts] from the raw hidden h fp32 [tokens, hidden].
+inline void moeRouterLogits(Backend &backend, Buffer *h, const RouterWeights &R, Buffer *logits,
+                            uint32_t tokens, float eps) {
+    backend.run("moe_router_logits_q8_f32",
+                {Arg::buf(h), Arg::buf(R.buffer, R.norm_offset), Arg::buf(R.buffer, R.codes_offset),
+                 Arg::buf(R.buffer, R.scales_offset), Arg::buf(R.buffer, R.biases_offset),
+                 Arg::buf(logits), Arg::val(tokens), Arg::val(R.experts), Arg::val(R.hidden),
+                 Arg::val(eps)},
+                Dim3{1}, Dim3{256});
+}
+
+// Top-k of fp32 logits, softmax over the k, times router.per_expert_scale:
+// ids i32 / weights f32 [tokens, top_k].
+inline void moeRoute(Backend &backend, Buffer *logits, const RouterWeights &R, Buffer *ids,
+                     Buffer *weights, uint32_t tokens, uint32_t top_k) {
+    const uint32_t has_scale = 1;
+    backend.run("moe_route_f32",
+                {Arg::buf(logits), Arg::buf(R.buffer, R.per_expert_scale_offset), Arg::buf(ids),
+                 Arg::buf(weights), Arg::val(tokens), Arg::val(R.experts), Arg::val(top_k),
+                 Arg::val(has_scale)},
+                Dim3{1}, Dim3{256});
+}
+
+// The MoE block after the router projection: routing from the fp32 logits (times
+// router.per_expert_scale) and the expert FFN, bf16 x, y [tokens, hidden].
+inline void moeFfnFromLogits(Backend &backend, Buffer *x, Buffer *logits, const RouterWeights &R,
+                             const ExpertSlots &E, Buffer *y, Buffer *workspace, uint32_t tokens,
+                             uint32_t top_k, uint32_t hidden, uint32_t inter) {
+    const uint32_t has_scale = 1;
+    backend.run("moe_ffn_f32logits_nvfp4_bf16",
+                {Arg::buf(x), Arg::buf(logits), Arg::buf(R.buffer, R.per_expert_scale_offset),
+                 Arg::buf(E.slots), Arg::buf(y), Arg::buf(workspace), Arg::val(tokens),
+                 Arg::val(R.experts), Arg::val(top_k), Arg::val(hidden), Arg::val(inter),
+                 Arg::val(E.stride), Arg::val(E.gate_w), Arg::val(E.gate_s), Arg::val(E.up_w),
+                 Arg::val(E.up_s), Arg::val(E.down_w), Arg::val(E.down_s), Arg::val(has_scale)},
+                Dim3{1}, Dim3{256});
+}
+
 } // namespace apex

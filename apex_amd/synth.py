@@ -132,6 +132,47 @@ def dense_mlp_case(seed: int = 0, tokens: int = 1, H: int = 2816, I: int = 2112)
     return h, norm_w, gate, up, down
 
 
+@dataclasses.dataclass
+class RouterWeights:
+    """Gemma-4 router tensors (tools/out.txt:247-290): router.scale bf16 [H],
+    router.proj affine 8-bit (weight u32 [E, H/4], scales and biases bf16 [E, H/64])
+    and router.per_expert_scale bf16 [E]."""
+    norm_w: np.ndarray
+    qw: np.ndarray
+    qs: np.ndarray
+    qb: np.ndarray
+    pes: np.ndarray
+
+    def dequant(self) -> np.ndarray:
+        """fp64 [E, H]: scale * q + bias per 64-element group."""
+        q = self.qw.view(np.uint8).astype(np.float64)
+        E, H = q.shape
+        s = np.repeat(bf16_to_f32(self.qs).astype(np.float64), 64, axis=1)
+        b = np.repeat(bf16_to_f32(self.qb).astype(np.float64), 64, axis=1)
+        return s * q + b
+
+
+def router_weights(rng: np.random.Generator, E: int = 128, H: int = 2816) -> RouterWeights:
+    """Draw order: norm weights ~1+0.1N, codes (uniform bytes), group scales
+    |N|*0.004+0.001, group biases -127.5*scale+0.01N (centred groups), per-expert
+    scales ~1+0.1N."""
+    norm_w = bf16_from_f32((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    q = rng.integers(0, 256, size=(E, H), dtype=np.uint8)
+    sc = (np.abs(rng.standard_normal((E, H // 64))) * 0.004 + 0.001).astype(np.float32)
+    qs = bf16_from_f32(sc)
+    bi = (-127.5 * bf16_to_f32(qs) + 0.01 * rng.standard_normal((E, H // 64))).astype(np.float32)
+    qb = bf16_from_f32(bi)
+    pes = bf16_from_f32((1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32))
+    return RouterWeights(norm_w, q.view(np.uint32).reshape(E, H // 4), qs, qb, pes)
+
+
+def router_case(seed: int = 0, tokens: int = 16, E: int = 128, H: int = 2816):
+    """Router front-end input: raw hidden h fp32 [T, H] ~ N(0,1), then the router weights."""
+    rng = np.random.default_rng(seed)
+    h = rng.standard_normal((tokens, H), dtype=np.float32)
+    return h, router_weights(rng, E, H)
+
+
 def geglu_case(seed: int = 0, tokens: int = 1, rows: int = 21504, K: int = 5376):
     """Decode fused GeGLU.  Draws: x [T,K], gate W, up W."""
     rng = np.random.default_rng(seed)

@@ -324,6 +324,27 @@ def time_dense_mlp_decode(steps, warmup, H=2816, I=2112):
                         f"NVFP4 [{I}x{H}] x2 -> down NVFP4 [{H}x{I}] (3 launches)"}
 
 
+def time_router(steps, warmup, E=128, H=2816):
+    """Gemma-4 router logits (RMSNorm with router.scale + affine 8-bit projection, fp32)
+    at the decode (16 tokens) and prefill (4096 tokens) sizes; FLOPs = 2 T E H."""
+    out = {}
+    for T, name in ((16, "router_decode"), (4096, "router_prefill")):
+        h, rw = synth.router_case(seed=0, tokens=T, E=E, H=H)
+        arrs = [hip.DeviceArray.from_numpy(a) for a in (h, rw.norm_w, rw.qw, rw.qs, rw.qb)]
+        lg = hip.DeviceArray((T, E), np.float32)
+        stream = hip.Stream()
+        sec = time_steps(lambda i: hip.moe_router_logits_q8(*arrs, lg, T, E, H, 1e-6,
+                                                            stream=stream), steps, warmup, stream)
+        stream.close()
+        for a in arrs + [lg]:
+            a.close()
+        out[name] = {"value": round(2.0 * T * E * H / sec / 1e12, 3), "unit": "TFLOP/s",
+                     "ms_per_step": round(sec * 1e3, 6),
+                     "workload": f"router logits: h fp32 [{T},{H}], affine q8 [{E}x{H}] "
+                                 f"(group 64), fp32 out [{T},{E}]"}
+    return out
+
+
 def vendor_bf16_gemm(M, N, K, steps, warmup):
     """Context for the GEMM line: the vendor library's plain bf16 GEMM of the same shape
     (torch -> hipBLASLt, weights already bf16, no FP4 decode).  Not part of the path."""
@@ -386,7 +407,7 @@ def main(argv=None):
     ap.add_argument("--calibrate", action="store_true",
                     help="run the known-size read and copy kernels first (counter scaling)")
     ap.add_argument("--only", choices=["moe_prefill", "gemm_prefill", "moe_decode", "norms",
-                                       "dense_mlp_decode"],
+                                       "dense_mlp_decode", "router"],
                     help="profiling aid: time one secondary workload and print its record only")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -399,7 +420,7 @@ def main(argv=None):
     if args.only:
         fn = {"moe_prefill": time_moe_prefill, "gemm_prefill": time_gemm_prefill,
               "moe_decode": time_moe_decode, "norms": time_norms,
-              "dense_mlp_decode": time_dense_mlp_decode}[args.only]
+              "dense_mlp_decode": time_dense_mlp_decode, "router": time_router}[args.only]
         print(json.dumps({args.only: fn(args.steps, args.warmup)}), flush=True)
         return 0
     r = time_geglu(args.steps, args.warmup)
@@ -445,6 +466,7 @@ def main(argv=None):
         line["secondary"].update(time_norms(max(1, args.steps // 10), max(1, args.warmup // 10)))
         line["secondary"]["dense_mlp_decode"] = time_dense_mlp_decode(
             max(1, args.steps // 10), max(1, args.warmup // 10))
+        line["secondary"].update(time_router(max(1, args.steps // 100), max(1, args.warmup // 100)))
     if not args.no_cpu:
         cb = cpu_baseline_geglu(args.cpu_budget)
         cb.pop("_h")

@@ -127,6 +127,15 @@ int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
  *                     U down_w, U down_s (apex_moe_ffn_bf16).
  *   moe_route_bf16    B logits bf16 [T,E], B ids i32 [T,k], B weights f32 [T,k], U T,
  *                     U E, U top_k (apex_moe_route_bf16).
+ *   moe_router_logits_q8_f32 B h f32 [T,H], B router.scale bf16 [H], B proj weights
+ *                     u32 [E,H/4], B proj scales bf16 [E,H/64], B proj biases, B logits f32
+ *                     [T,E], U T, U E, U H, F eps (apex_moe_router_logits_q8).
+ *   moe_route_f32     B logits f32 [T,E], B per-expert scale bf16 [E], B ids, B weights,
+ *                     U T, U E, U top_k, U has_scale (apex_moe_route_f32).
+ *   moe_ffn_f32logits_nvfp4_bf16 B x bf16, B logits f32, B per-expert scale, B expert
+ *                     slots, B y bf16, B workspace, U T, U E, U top_k, U H, U I, U slot
+ *                     stride, the six U piece offsets, U has_scale
+ *                     (apex_moe_ffn_f32logits_bf16).
  *   rms_norm_f32      B input f32 [rows,n], B weights bf16 [n], B result f32 [rows,n],
  *                     U hidden_dim n, F eps; rows = threadgroups.x (src/ops.h:18-26,
  *                     shaders/norm.metal:33-81).
@@ -273,6 +282,24 @@ typedef struct {
 int apex_moe_route_bf16(const uint16_t *logits, uint32_t tokens, uint32_t experts, uint32_t top_k,
                         int32_t *ids, float *weights, void *stream);
 
+/* Gemma-4 router logits (docs/B6_3_attention.md:721-725; tensors router.scale,
+ * router.proj.{weight,scales,biases} of tools/out.txt:247-290): per token, RMSNorm of
+ * the raw hidden h fp32 [tokens, hidden] with norm_weights bf16 [hidden] (rmsNormCpu
+ * arithmetic), then logits[t, e] = sum_k xn[t, k] * (scale[e, g] * q[e, k] + bias[e, g])
+ * with q the unsigned byte (k % 4) of proj_weights[e, k / 4] (u32 [experts, hidden/4]),
+ * g = k / 64 and scales/biases bf16 [experts, hidden/64]; fp32 out [tokens, experts].
+ * experts <= 256, hidden a multiple of 64 and at most 4096. */
+int apex_moe_router_logits_q8(const float *h, const uint16_t *norm_weights, float eps,
+                              const uint32_t *proj_weights, const uint16_t *proj_scales,
+                              const uint16_t *proj_biases, uint32_t tokens, uint32_t experts,
+                              uint32_t hidden, float *logits, void *stream);
+
+/* apex_moe_route_bf16 on fp32 logits, each routing weight then multiplied by the bf16
+ * per_expert_scale[expert] (router.per_expert_scale; null: no scale). */
+int apex_moe_route_f32(const float *logits, const uint16_t *per_expert_scale, uint32_t tokens,
+                       uint32_t experts, uint32_t top_k, int32_t *ids, float *weights,
+                       void *stream);
+
 /* Device workspace (bytes) apex_moe_ffn_bf16 needs for these sizes (either path). */
 size_t apex_moe_workspace_bytes(uint32_t tokens, uint32_t experts, uint32_t top_k, uint32_t hidden,
                                 uint32_t inter);
@@ -292,6 +319,16 @@ int apex_moe_ffn_bf16(const uint16_t *x, const uint16_t *logits, const apex_moe_
 
 /* Path selection of apex_moe_ffn_bf16: 0 by size (default), 1 grouped GEMV, 2 grouped GEMM. */
 int apex_hip_set_moe_path(int path);
+
+/* apex_moe_ffn_bf16 routed from fp32 router logits [tokens, experts] (as
+ * apex_moe_router_logits_q8 writes them), each routing weight times the bf16
+ * per_expert_scale[expert] when one is given: the whole Gemma-4 MoE block after the
+ * router projection.  Same workspace and limits as apex_moe_ffn_bf16. */
+int apex_moe_ffn_f32logits_bf16(const uint16_t *x, const float *logits,
+                                const uint16_t *per_expert_scale, const apex_moe_slots *slots,
+                                uint16_t *y, uint32_t tokens, uint32_t experts, uint32_t top_k,
+                                uint32_t hidden, uint32_t inter, void *workspace,
+                                size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -56,6 +56,7 @@ def lib():
         L.orc_float_to_bf16.restype = C.c_uint16
         L.orc_float_to_bf16.argtypes = [_F]
         L.orc_rms_norm.argtypes = [_P, _P, _P, _SZ, _SZ, _F]
+        L.orc_moe_router_logits_q8.argtypes = [_P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _P]
         L.orc_head_norm_rope.argtypes = [_P, _P, C.c_int, _P, _SZ, _SZ, _SZ, _SZ, _F, C.c_uint32,
                                          _SZ, _SZ, _F]
         _lib = L
@@ -193,6 +194,20 @@ def rms_norm(x, w_bf16, eps: float) -> np.ndarray:
     y = np.empty_like(x)
     lib().orc_rms_norm(px, pw, y.ctypes.data, x.shape[0], x.shape[1], eps)
     return y
+
+
+def moe_router_logits(h, norm_w, qw, qs, qb, eps: float) -> np.ndarray:
+    """Router logits fp32 [T, E] (orc_moe_router_logits_q8)."""
+    h, ph = _c(np.atleast_2d(h), np.float32)
+    nw, pnw = _c(norm_w, np.uint16)
+    qw, pqw = _c(qw, np.uint32)
+    qs, pqs = _c(qs, np.uint16)
+    qb, pqb = _c(qb, np.uint16)
+    T, H = h.shape
+    E = qw.shape[0]
+    out = np.empty((T, E), np.float32)
+    lib().orc_moe_router_logits_q8(ph, pnw, eps, pqw, pqs, pqb, T, E, H, out.ctypes.data)
+    return out
 
 
 def head_norm_rope(x, w_bf16, rope_pairs: int, rope_base: float, abs_pos: int, eps: float,

@@ -268,3 +268,33 @@ void orc_head_norm_rope(const float *x, const uint16_t *w_bf16, int has_weight, 
         }
     free(row);
 }
+
+/* docs/B6_3_attention.md:721-725: rmsNormCpu arithmetic (above) with the router.scale
+ * weights, then the affine 8-bit projection w[e][k] = scale[e][g] * q[e][k] + bias[e][g],
+ * q = byte k % 4 (least significant first) of word k / 4, g = k / 64; the sum runs in
+ * fp64 per group (scale * sum xn q + bias * sum xn) and over groups in index order. */
+void orc_moe_router_logits_q8(const float *h, const uint16_t *norm_w, float eps,
+                              const uint32_t *qw, const uint16_t *qs, const uint16_t *qb,
+                              size_t T, size_t E, size_t H, float *logits) {
+    float *xn = (float *)malloc(H * sizeof(float));
+    const size_t NG = H / 64;
+    for (size_t t = 0; t < T; ++t) {
+        orc_rms_norm(h + t * H, norm_w, xn, 1, H, eps);
+        for (size_t e = 0; e < E; ++e) {
+            const uint8_t *q = (const uint8_t *)(qw + e * (H / 4));
+            double acc = 0.0;
+            for (size_t g = 0; g < NG; ++g) {
+                double sq = 0.0, sx = 0.0;
+                for (size_t j = 0; j < 64; ++j) {
+                    const size_t k = 64 * g + j;
+                    sq += (double)xn[k] * (double)q[k];
+                    sx += (double)xn[k];
+                }
+                acc += (double)orc_bf16_to_float(qs[e * NG + g]) * sq +
+                       (double)orc_bf16_to_float(qb[e * NG + g]) * sx;
+            }
+            logits[t * E + e] = (float)acc;
+        }
+    }
+    free(xn);
+}

@@ -26,6 +26,9 @@
  *                       is not importable; see the MoE section of the design notes)
  *   orc_e4m3_from_float round-to-nearest-even, checked against torch.float8_e4m3fn
  *   orc_rms_norm        compiled reference rmsNormCpu (bit-exact), scale invariance
+ *   orc_moe_router_logits_q8  fp64 matvec with the explicitly dequantised weights
+ *                       (numpy); byte order on one-hot codes; the norm is orc_rms_norm.
+ *                       Parity vs mlx-lm's router: UNPINNED (not importable)
  *   orc_head_norm_rope  rope_pairs = 0 / position 0 reduce to orc_rms_norm per head;
  *                       recovered rotation angles equal pos * base^(-2i/d) (numpy);
  *                       pair norms preserved; relative-position invariance of q.k
@@ -117,6 +120,13 @@ void orc_head_norm_rope(const float *x, const uint16_t *w_bf16, int has_weight, 
                         size_t tokens, size_t heads, size_t head_dim, size_t rope_pairs,
                         float rope_base, uint32_t abs_pos, size_t out_token_stride,
                         size_t out_head_stride, float eps);
+
+/* Gemma-4 router logits (docs/B6_3_attention.md:721-725): xn = rmsNormCpu(h, norm_w),
+ * logits[t][e] = sum_k xn[k] * (scale[e][k/64] * q[e][k] + bias[e][k/64]) with q byte
+ * k % 4 (LSB first) of qw[e][k/4]; per group scale * sum(xn q) + bias * sum(xn) in fp64. */
+void orc_moe_router_logits_q8(const float *h, const uint16_t *norm_w, float eps,
+                              const uint32_t *qw, const uint16_t *qs, const uint16_t *qb,
+                              size_t T, size_t E, size_t H, float *logits);
 
 /* Round-to-nearest-even float -> FP8 E4M3 byte, saturating to +-448 (never emits
  * 0x7F/0xFF).  The synthetic generator's scale rounding, restated for checking. */

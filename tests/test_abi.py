@@ -60,6 +60,9 @@ EXPECTED = {
     "dequant_nvfp4_bf16": "BBBUUF",
     "rms_norm_f32": "BBBUF",
     "head_norm_rope_f32": "BBBUUUUFUUUF",
+    "moe_router_logits_q8_f32": "BBBBBBUUUF",
+    "moe_route_f32": "BBBBUUUU",
+    "moe_ffn_f32logits_nvfp4_bf16": "BBBBBBUUUUUUUUUUUUU",
 }
 
 

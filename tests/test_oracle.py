@@ -475,3 +475,37 @@ def test_head_norm_rope_output_strides():
     for t in range(T):
         for h in range(Hh):
             assert np.array_equal(out[t * ts + h * hs: t * ts + h * hs + D], dense[t, h])
+
+
+# ---- Gemma-4 router front-end ------------------------------------------------------
+
+def test_router_logits_equal_the_dequantised_matvec():
+    """orc_moe_router_logits_q8 (per-group scale * sum(xn q) + bias * sum(xn)) against
+    the fp64 product of the normed rows with explicitly dequantised weights
+    scale * q + bias (numpy): a dropped bias term, a wrong group index or a byte-order
+    slip fails."""
+    h, rw = synth.router_case(seed=3, tokens=4, E=24, H=448)
+    got = oracle.moe_router_logits(h, rw.norm_w, rw.qw, rw.qs, rw.qb, 1e-6)
+    xn = oracle.rms_norm(h, rw.norm_w, 1e-6).astype(np.float64)
+    want = xn @ rw.dequant().T
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(want).max())
+
+
+def test_router_logits_byte_order_and_bias():
+    """One-hot codes: element k of expert e is byte k % 4 of word k / 4, least
+    significant byte first; zero scales leave bias * sum of the group."""
+    H, E = 128, 4
+    h = np.zeros((1, H), np.float32)
+    h[0, 5] = 1.0
+    ones = synth.bf16_from_f32(np.ones(H, np.float32))
+    q = np.zeros((E, H), np.uint8)
+    q[2, 5] = 200          # expert 2 sees xn[5] * 200 * scale
+    qs = synth.bf16_from_f32(np.full((E, H // 64), 0.5, np.float32))
+    qb = np.zeros((E, H // 64), np.uint16)
+    lg = oracle.moe_router_logits(h, ones, q.view(np.uint32), qs, qb, 0.0)
+    xn5 = np.float32(np.sqrt(H))  # a one-hot row normalises to sqrt(H)
+    assert np.allclose(lg[0], [0, 0, xn5 * 200 * 0.5, 0], rtol=1e-6)
+    qs0 = np.zeros_like(qs)
+    qb1 = synth.bf16_from_f32(np.full((E, H // 64), 0.25, np.float32))
+    lg = oracle.moe_router_logits(h, ones, q.view(np.uint32), qs0, qb1, 0.0)
+    assert np.allclose(lg[0], np.full(E, xn5 * 0.25), rtol=1e-6)
