@@ -39,7 +39,7 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++20", "-fPIC", "-Wall",
 CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", "-I", str(INCLUDE), "-I", str(HOST)]
 
 HIP_UNITS = ["hip_impl.cpp", "gemv.hip", "gemv_f32.hip", "gemv_bf16_plain.hip", "moe.hip",
-             "gemv_bf16_geglu.hip", "gemm.hip", "norm.hip"]
+             "gemv_bf16_geglu.hip", "gemm.hip", "norm.hip", "file_io.cpp"]
 HOST_UNITS = ["hip_backend.cpp"]
 
 

@@ -14,6 +14,7 @@
 #include "gemv.h"
 #include "moe.h"
 #include "norm.h"
+#include "file_io.h"
 
 namespace {
 
@@ -77,6 +78,11 @@ void check_nvfp4_shape(uint32_t rows, uint32_t K) {
 // Tokens from which a bf16 product runs as an MFMA GEMM instead of a GEMV: below it
 // the weights dominate the traffic and the GEMV streams them at the HBM rate.
 constexpr uint32_t kGemmMinTokens = 64;
+
+// Pinned staging for file -> device streaming: 4 buffers of 16 MiB (a read and a copy
+// in flight with room to spare; 64 MiB pinned per call).
+constexpr uint64_t kFileChunk = 16ull << 20;
+constexpr uint32_t kFileBuffers = 4;
 
 void gemm_impl(const uint16_t *A, const uint32_t *codes, const uint8_t *scales, float ts,
                uint16_t *C, uint32_t M, uint32_t N, uint32_t K, hipStream_t stream) {
@@ -685,6 +691,25 @@ int apex_hip_contents(apex_hip_backend *b, apex_hip_buffer *buf, void **out) {
     });
 }
 
+int apex_hip_load_file(apex_hip_backend *b, apex_hip_buffer *buf, uint64_t buffer_offset,
+                       const char *path, uint64_t file_offset, uint64_t bytes) {
+    return guard([&] {
+        require(b && buf && path, "null argument");
+        require(buffer_offset <= buf->length && bytes <= buf->length - buffer_offset,
+                "load_file: range past the end of the buffer");
+        if (bytes == 0)
+            return;
+        ensure_device_current(b, buf); // the rest of the buffer keeps what the host wrote
+        const apex_hip::FileRange r{file_offset, bytes, static_cast<char *>(buf->dev) + buffer_offset};
+        const apex_hip::FileCopyStatus st =
+            apex_hip::copy_file_ranges(path, &r, 1, kFileChunk, kFileBuffers, b->stream);
+        if (!st.error.empty())
+            fail(APEX_HIP_E_INVALID, "load_file: " + st.error);
+        buf->host_valid = false;
+        buf->dev_valid = true;
+    });
+}
+
 int apex_hip_release(apex_hip_backend *b, apex_hip_buffer *buf) {
     return guard([&] {
         if (!buf)
@@ -1029,6 +1054,43 @@ int apex_moe_router_logits_q8(const float *h, const uint16_t *norm_weights, floa
         router_impl({h, norm_weights, eps, proj_weights, proj_scales, proj_biases, tokens, experts,
                      hidden, logits},
                     as_stream(stream));
+    });
+}
+
+int apex_file_to_device(const char *path, uint64_t file_offset, uint64_t bytes, void *dst,
+                        uint64_t chunk_bytes, uint32_t n_buffers, void *stream) {
+    return guard([&] {
+        require(path && (dst || bytes == 0), "null pointer");
+        if (bytes == 0)
+            return;
+        const apex_hip::FileRange r{file_offset, bytes, dst};
+        const apex_hip::FileCopyStatus st = apex_hip::copy_file_ranges(
+            path, &r, 1, chunk_bytes ? chunk_bytes : kFileChunk, n_buffers ? n_buffers : kFileBuffers,
+            as_stream(stream));
+        if (!st.error.empty())
+            fail(APEX_HIP_E_INVALID, "file_to_device: " + st.error);
+    });
+}
+
+int apex_experts_to_device(const char *path, uint64_t stride, uint64_t slot_bytes,
+                           const int32_t *experts, uint32_t n_experts, void *dst,
+                           uint64_t dst_stride, uint64_t chunk_bytes, uint32_t n_buffers,
+                           void *stream) {
+    return guard([&] {
+        require(path && (n_experts == 0 || (experts && dst)), "null pointer");
+        require(slot_bytes <= stride && slot_bytes <= dst_stride,
+                "experts_to_device: slot_bytes exceeds a stride");
+        std::vector<apex_hip::FileRange> r(n_experts);
+        for (uint32_t i = 0; i < n_experts; ++i) {
+            require(experts[i] >= 0, "experts_to_device: negative expert index");
+            r[i] = {(uint64_t)experts[i] * stride, slot_bytes,
+                    static_cast<char *>(dst) + (uint64_t)i * dst_stride};
+        }
+        const apex_hip::FileCopyStatus st = apex_hip::copy_file_ranges(
+            path, r.data(), r.size(), chunk_bytes ? chunk_bytes : kFileChunk,
+            n_buffers ? n_buffers : kFileBuffers, as_stream(stream));
+        if (!st.error.empty())
+            fail(APEX_HIP_E_INVALID, "experts_to_device: " + st.error);
     });
 }
 

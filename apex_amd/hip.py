@@ -44,6 +44,7 @@ def dim3(x, y=1, z=1) -> Dim3:
 
 _P = C.c_void_p
 _U32 = C.c_uint32
+_U64 = C.c_uint64
 _F = C.c_float
 _SZ = C.c_size_t
 _I = C.c_int
@@ -100,6 +101,9 @@ _PROTOS = {
     "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
     "apex_hip_set_moe_path": (_I, [_I]),
     "apex_rms_norm_f32": (_I, [_P, _P, _P, _U32, _U32, _F, _P]),
+    "apex_file_to_device": (_I, [C.c_char_p, _U64, _U64, _P, _U64, _U32, _P]),
+    "apex_experts_to_device": (_I, [C.c_char_p, _U64, _U64, _P, _U32, _P, _U64, _U64, _U32, _P]),
+    "apex_hip_load_file": (_I, [_P, _P, _U64, C.c_char_p, _U64, _U64]),
     "apex_moe_router_logits_q8": (_I, [_P, _P, _F, _P, _P, _P, _U32, _U32, _U32, _P, _P]),
     "apex_moe_route_f32": (_I, [_P, _P, _U32, _U32, _U32, _P, _P, _P]),
     "apex_moe_ffn_f32logits_bf16": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P,
@@ -289,6 +293,20 @@ def head_norm_rope_f32(x, w, y, tokens, heads, head_dim, rope_pairs, rope_base, 
                                         out_head_stride, eps, _s(stream)))
 
 
+def file_to_device(path, file_offset, nbytes, dst, dst_offset=0, chunk_bytes=0, n_buffers=0,
+                   stream=None):
+    check(lib().apex_file_to_device(str(path).encode(), file_offset, nbytes, dst.ptr + dst_offset,
+                                    chunk_bytes, n_buffers, _s(stream)))
+
+
+def experts_to_device(path, stride, slot_bytes, experts, dst, dst_stride, chunk_bytes=0,
+                      n_buffers=0, stream=None):
+    ids = np.ascontiguousarray(experts, np.int32)
+    check(lib().apex_experts_to_device(str(path).encode(), stride, slot_bytes, ids.ctypes.data,
+                                       len(ids), dst.ptr, dst_stride, chunk_bytes, n_buffers,
+                                       _s(stream)))
+
+
 def read_probe(buf, sink, stream=None) -> None:
     check(lib().apex_hip_read_probe(buf.ptr, buf.nbytes, sink.ptr, _s(stream)))
 
@@ -452,6 +470,10 @@ class Backend:
             return np.empty(0, dt)
         raw = (C.c_char * (n * dt.itemsize)).from_address(p.value)
         return np.frombuffer(raw, dtype=dt, count=n)
+
+    def load_file(self, b: Buffer, offset: int, path, file_offset: int, nbytes: int) -> None:
+        check(lib().apex_hip_load_file(self.handle, b.handle, offset, str(path).encode(),
+                                       file_offset, nbytes))
 
     def release(self, b: Buffer) -> None:
         check(lib().apex_hip_release(self.handle, b.handle))

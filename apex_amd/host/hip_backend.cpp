@@ -76,6 +76,13 @@ void HipBackend::sync() {
     check(apex_hip_sync(b_), "sync");
 }
 
+void HipBackend::loadFile(Buffer *buffer, size_t offset, const std::string &path,
+                          uint64_t file_offset, uint64_t bytes) {
+    check(apex_hip_load_file(b_, buffer ? buffer->handle : nullptr, offset, path.c_str(),
+                             file_offset, bytes),
+          "loadFile");
+}
+
 void *HipBackend::devicePtr(Buffer *buffer) const {
     void *p = nullptr;
     check(apex_hip_buffer_device_ptr(buffer->handle, &p), "devicePtr");

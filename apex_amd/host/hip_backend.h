@@ -16,6 +16,7 @@
 // one host thread drives one backend, which owns one in-order stream.
 #pragma once
 #include <cstddef>
+#include <cstdint>
 #include <string>
 
 #include "apex_hip.h"
@@ -49,6 +50,12 @@ class HipBackend : public Backend {
     void *devicePtr(Buffer *buffer) const;
     // The backend's stream (hipStream_t), for interop with other HIP code.
     void *stream() const;
+    // Stream bytes [file_offset, file_offset + bytes) of a file into the buffer at
+    // `offset` (pread into pinned staging overlapped with host-to-device copies); returns
+    // when they are on the device.  Where the reference maps a packed file and wraps the
+    // mapping (src/tests/dense_mlp.cpp:24-30), a discrete GPU loads it once.
+    void loadFile(Buffer *buffer, size_t offset, const std::string &path, uint64_t file_offset,
+                  uint64_t bytes);
 
     HipBackend(const HipBackend &) = delete;
     HipBackend &operator=(const HipBackend &) = delete;

@@ -271,3 +271,89 @@ def moe_prefill_case(seed: int = 0, tokens: int = 4096, H: int = 2816, I: int = 
     logits = zipf_logits(rng, tokens, E)
     slots = expert_slots(rng, E, H, I)
     return x, logits, slots
+
+
+# ---- packed model directories (tools/repack.py:180-257 format) ---------------------
+
+PIECE_NAMES = {"gate_w": "gate_proj.weight", "gate_s": "gate_proj.scales",
+               "up_w": "up_proj.weight", "up_s": "up_proj.scales",
+               "down_w": "down_proj.weight", "down_s": "down_proj.scales"}
+
+
+def write_packed_model(out_dir, seed: int = 0, layers: int = 2, E: int = 128, H: int = 2816,
+                       I: int = 704):
+    """A synthetic packed model directory in the repack format: layer_NN.bin (E expert
+    slots at a fixed page-aligned stride, the six pieces in the fixed order),
+    core.bin (per layer: pre_feedforward_layernorm_2.weight and the router tensors,
+    page-aligned) and manifest.json.  Returns (manifest dict, per-layer ExpertSlots,
+    per-layer RouterWeights)."""
+    import hashlib
+    import json
+    from pathlib import Path
+
+    out = Path(out_dir)
+    out.mkdir(parents=True, exist_ok=True)
+    rng = np.random.default_rng(seed)
+    page = SLOT_ALIGN
+    tensors, core = [], bytearray()
+
+    def add_core(name, dtype, shape, arr):
+        off = (len(core) + page - 1) // page * page
+        core.extend(b"\0" * (off - len(core)))
+        data = np.ascontiguousarray(arr).tobytes()
+        core.extend(data)
+        tensors.append({"name": name, "dtype": dtype, "shape": list(shape), "offset": off,
+                        "nbytes": len(data), "sha256": hashlib.sha256(data).hexdigest()})
+
+    layer_entries, all_slots, all_routers = [], [], []
+    for layer in range(layers):
+        slots = expert_slots(rng, E, H, I)
+        rw = router_weights(rng, E, H)
+        norm2 = bf16_from_f32((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+        p = f"layers.{layer}."
+        add_core(p + "pre_feedforward_layernorm_2.weight", "BF16", [H], norm2)
+        add_core(p + "router.scale", "BF16", [H], rw.norm_w)
+        add_core(p + "router.proj.weight", "U32", [E, H // 4], rw.qw)
+        add_core(p + "router.proj.scales", "BF16", [E, H // 64], rw.qs)
+        add_core(p + "router.proj.biases", "BF16", [E, H // 64], rw.qb)
+        add_core(p + "router.per_expert_scale", "BF16", [E], rw.pes)
+        name = f"layer_{layer:02d}.bin"
+        (out / name).write_bytes(slots.data.tobytes())
+        shapes = {"gate_w": ("U32", [I, H // 8]), "gate_s": ("U8", [I, H // 16]),
+                  "up_w": ("U32", [I, H // 8]), "up_s": ("U8", [I, H // 16]),
+                  "down_w": ("U32", [H, I // 8]), "down_s": ("U8", [H, I // 16])}
+        used = sum(int(np.prod(shapes[k][1])) * (4 if shapes[k][0] == "U32" else 1) for k in PIECES)
+        layer_entries.append({
+            "layer": layer, "file": name, "size": E * slots.stride, "num_experts": E,
+            "stride": slots.stride,
+            "pieces": [{"name": PIECE_NAMES[k], "dtype": shapes[k][0], "shape": shapes[k][1],
+                        "offset": slots.offsets[k],
+                        "nbytes": int(np.prod(shapes[k][1])) * (4 if shapes[k][0] == "U32" else 1)}
+                       for k in PIECES],
+            "expert_sha256": [hashlib.sha256(slots.data[e * slots.stride:e * slots.stride + used]
+                                             .tobytes()).hexdigest() for e in range(E)],
+        })
+        all_slots.append(slots)
+        all_routers.append(rw)
+    core.extend(b"\0" * ((len(core) + page - 1) // page * page - len(core)))
+    (out / "core.bin").write_bytes(bytes(core))
+    manifest = {
+        "version": 1, "alignment": page,
+        "text_config": {
+            "hidden_size": H, "intermediate_size": 2112, "moe_intermediate_size": I,
+            "num_attention_heads": 16, "num_key_value_heads": 8, "head_dim": 256,
+            "num_hidden_layers": layers, "num_experts": E, "top_k_experts": 8,
+            "vocab_size": 262144, "sliding_window": 1024, "rms_norm_eps": 1e-6,
+            "final_logit_softcapping": 30.0,
+            "layer_types": ["sliding_attention"] * layers,
+            "global_head_dim": 512, "num_global_key_value_heads": 2, "attention_k_eq_v": True,
+            "rope_parameters": {"sliding_attention": {"rope_theta": 10000.0},
+                                "full_attention": {"rope_theta": 1000000.0,
+                                                   "partial_rotary_factor": 0.25}},
+        },
+        "quantization": {"group_size": 64, "bits": 8, "mode": "affine"},
+        "core": {"file": "core.bin", "tensors": tensors, "size": len(core)},
+        "layers": layer_entries,
+    }
+    (out / "manifest.json").write_text(json.dumps(manifest, indent=1) + "\n")
+    return manifest, all_slots, all_routers

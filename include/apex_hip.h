@@ -154,6 +154,15 @@ int apex_hip_run(apex_hip_backend *backend, const char *kernel, const apex_hip_a
  * kernels. */
 int apex_hip_sync(apex_hip_backend *backend);
 
+/* No reference counterpart (the reference maps files into unified memory, src/file.h:
+ * 27-73, and wraps the mapping with Backend::wrapNoCopy): bytes [file_offset,
+ * file_offset + bytes) of the file at `path` are streamed into `buffer` at
+ * buffer_offset through pinned staging buffers (pread overlapped with host-to-device
+ * copies on the backend's stream); returns when they are on the device.  The rest of
+ * the buffer keeps its contents. */
+int apex_hip_load_file(apex_hip_backend *backend, apex_hip_buffer *buffer, uint64_t buffer_offset,
+                       const char *path, uint64_t file_offset, uint64_t bytes);
+
 /* No reference counterpart (the reference's buffers are host-visible): the device
  * address of a buffer (valid until release), its length, and the backend's stream
  * (a hipStream_t) for hosts mixing backend kernels with direct entry points. */
@@ -299,6 +308,20 @@ int apex_moe_router_logits_q8(const float *h, const uint16_t *norm_weights, floa
 int apex_moe_route_f32(const float *logits, const uint16_t *per_expert_scale, uint32_t tokens,
                        uint32_t experts, uint32_t top_k, int32_t *ids, float *weights,
                        void *stream);
+
+/* Packed weight files (tools/repack.py:180-257: core.bin, layer_NN.bin with 128 expert
+ * slots at a fixed stride) into device memory.  apex_file_to_device copies bytes
+ * [file_offset, file_offset + bytes) to dst; apex_experts_to_device copies slot
+ * experts[i] (file bytes [experts[i] * stride, + slot_bytes)) to dst + i * dst_stride
+ * for i < n_experts (experts is a host array).  Both read chunk_bytes at a time into a
+ * ring of n_buffers pinned host buffers while earlier chunks' host-to-device copies
+ * run on `stream` (0: 16 MiB, 4 buffers), and return once every copy has completed. */
+int apex_file_to_device(const char *path, uint64_t file_offset, uint64_t bytes, void *dst,
+                        uint64_t chunk_bytes, uint32_t n_buffers, void *stream);
+int apex_experts_to_device(const char *path, uint64_t stride, uint64_t slot_bytes,
+                           const int32_t *experts, uint32_t n_experts, void *dst,
+                           uint64_t dst_stride, uint64_t chunk_bytes, uint32_t n_buffers,
+                           void *stream);
 
 /* Device workspace (bytes) apex_moe_ffn_bf16 needs for these sizes (either path). */
 size_t apex_moe_workspace_bytes(uint32_t tokens, uint32_t experts, uint32_t top_k, uint32_t hidden,

@@ -17,6 +17,8 @@
 #include <vector>
 
 #include "hip_backend.h"
+#include "model_info.h"
+#include "model_loader.h"
 #include "nvfp4_oracle.h"
 #include "ops.h"
 #include "profiling.h"
@@ -284,6 +286,111 @@ void test_norms(HipBackend &be) {
         be.release(b);
 }
 
+bool throws(const std::function<void()> &f, const char *needle);
+
+// manifest.json of a packed directory (written by the Python side in the repack
+// format): the ModelInfo fields the engine reads.
+void test_manifest(const std::string &dir) {
+    const ModelInfo m = ModelInfo::load(dir);
+    const bool cfg = m.config.hidden_size > 0 && m.config.num_experts > 0 &&
+                     m.config.top_k_experts == 8 && m.config.rms_norm_eps > 0 &&
+                     m.config.rope_theta_full == 1000000.0 && m.quant_group_size == 64 &&
+                     m.quant_bits == 8 && m.quant_mode == "affine" &&
+                     (int)m.config.layer_types.size() == m.config.num_hidden_layers;
+    report("manifest: config and quantization", cfg);
+    bool pieces = m.expert_pieces.size() == 6 && m.expert_slot_size % 16384 == 0;
+    uint64_t end = 0;
+    for (const char *n : {"gate_proj.weight", "gate_proj.scales", "up_proj.weight",
+                          "up_proj.scales", "down_proj.weight", "down_proj.scales"}) {
+        const ExpertPiece &p = m.piece(n);
+        pieces = pieces && p.offset == end; // contiguous, in the fixed order
+        end = p.offset + p.nbytes;
+    }
+    pieces = pieces && end <= m.expert_slot_size;
+    report("manifest: expert slot pieces", pieces);
+    bool layers = (int)m.layers.size() == m.config.num_hidden_layers;
+    for (const LayerFile &f : m.layers)
+        layers = layers && f.stride == m.expert_slot_size &&
+                 f.size == (uint64_t)f.num_experts * f.stride &&
+                 (int)f.expert_sha256.size() == f.num_experts &&
+                 m.layer_file(f.layer) == m.dir + "/" + f.file;
+    report("manifest: layer files", layers);
+    const TensorInfo &t = m.getTensor("layers.0.router.proj.weight");
+    report("manifest: core tensors", t.dtype == "U32" && t.offset % 16384 == 0 &&
+                                         t.nbytes == (uint64_t)t.shape[0] * t.shape[1] * 4);
+    report("manifest: unknown tensor throws",
+           throws([&] { (void)m.getTensor("no.such.tensor"); }, "tensor not found"));
+}
+
+// The MoE block of layer 1 from a packed directory loaded to the device: router logits
+// and the routed expert FFN over buffers streamed from core.bin and layer_01.bin,
+// against the oracle composition on the same files' bytes.
+void test_packed_moe(HipBackend &be, const std::string &dir) {
+    const ModelInfo m = ModelInfo::load(dir);
+    const int layer = 1;
+    Buffer *core = loadCore(be, m);
+    Buffer *slots = loadExpertLayer(be, m, layer);
+    const RouterWeights R = routerWeights(m, core, layer);
+    const ExpertSlots S = expertSlots(m, slots);
+    const uint32_t T = 5, H = m.config.hidden_size, E = m.config.num_experts,
+                   I = m.config.moe_intermediate_size, k = m.config.top_k_experts;
+    Rng rng{9};
+    std::vector<float> h((size_t)T * H);
+    for (auto &v : h)
+        v = rng.normal();
+    std::vector<uint16_t> x((size_t)T * H);
+    for (auto &v : x)
+        v = to_bf16(rng.normal());
+    Buffer *bh = upload(be, h.data(), h.size() * 4, "activations");
+    Buffer *bx = upload(be, x.data(), x.size() * 2, "activations");
+    Buffer *lg = be.allocate((size_t)T * E * 4, "activations");
+    Buffer *y = be.allocate((size_t)T * H * 2, "activations");
+    Buffer *ws = be.allocate(moeWorkspaceBytes(T, E, k, H, I), "scratch");
+    moeRouterLogits(be, bh, R, lg, T, (float)m.config.rms_norm_eps);
+    moeFfnFromLogits(be, bx, lg, R, S, y, ws, T, k, H, I);
+    be.sync();
+
+    // oracle on the files' own bytes
+    std::vector<uint8_t> cb(m.core_size), lb(m.layers[layer].size);
+    FILE *f = std::fopen((m.dir + "/core.bin").c_str(), "rb");
+    bool ok = f && std::fread(cb.data(), 1, cb.size(), f) == cb.size();
+    if (f)
+        std::fclose(f);
+    f = std::fopen(m.layer_file(layer).c_str(), "rb");
+    ok = ok && f && std::fread(lb.data(), 1, lb.size(), f) == lb.size();
+    if (f)
+        std::fclose(f);
+    report("packed files read back", ok);
+    auto at = [&](const char *name) {
+        return cb.data() + m.getTensor("layers.1.router." + std::string(name)).offset;
+    };
+    std::vector<float> want_lg((size_t)T * E);
+    orc_moe_router_logits_q8(h.data(), (const uint16_t *)at("scale"), (float)m.config.rms_norm_eps,
+                             (const uint32_t *)at("proj.weight"), (const uint16_t *)at("proj.scales"),
+                             (const uint16_t *)at("proj.biases"), T, E, H, want_lg.data());
+    const float *got_lg = static_cast<const float *>(be.contents(lg));
+    const double r_lg = rel_l2(got_lg, want_lg.data(), want_lg.size());
+    report("packed router logits vs oracle", r_lg < 1e-5, "rel_l2 " + std::to_string(r_lg));
+    // route on the device's logits (the oracle's top-k on them), scale, dense FFNs
+    std::vector<int32_t> ids((size_t)T * k);
+    std::vector<float> w((size_t)T * k), xf((size_t)T * H), yf((size_t)T * H), got((size_t)T * H);
+    orc_moe_route(got_lg, T, E, k, ids.data(), w.data());
+    const uint16_t *pes = (const uint16_t *)at("per_expert_scale");
+    for (size_t i = 0; i < ids.size(); ++i)
+        w[i] *= from_bf16(pes[ids[i]]);
+    for (size_t i = 0; i < xf.size(); ++i)
+        xf[i] = from_bf16(x[i]);
+    orc_expert_layout L{m.expert_slot_size, S.gate_w, S.gate_s, S.up_w, S.up_s, S.down_w, S.down_s};
+    orc_moe_ffn(lb.data(), &L, xf.data(), ids.data(), w.data(), yf.data(), T, k, H, I);
+    const uint16_t *gy = static_cast<const uint16_t *>(be.contents(y));
+    for (size_t i = 0; i < got.size(); ++i)
+        got[i] = from_bf16(gy[i]);
+    const double r = rel_l2(got.data(), yf.data(), yf.size());
+    report("packed MoE block vs oracle", r < 1e-2, "rel_l2 " + std::to_string(r));
+    for (Buffer *b : {core, slots, bh, bx, lg, y, ws})
+        be.release(b);
+}
+
 bool throws(const std::function<void()> &f, const char *needle) {
     try {
         f();
@@ -322,7 +429,16 @@ void test_errors(HipBackend &be) {
 } // namespace
 
 int main(int argc, char **argv) {
-    const bool no_gpu = argc > 1 && std::strcmp(argv[1], "--no-gpu") == 0;
+    bool no_gpu = false;
+    std::string packed;
+    for (int i = 1; i < argc; ++i) {
+        if (std::strcmp(argv[i], "--no-gpu") == 0)
+            no_gpu = true;
+        else if (std::strcmp(argv[i], "--packed") == 0 && i + 1 < argc)
+            packed = argv[++i];
+    }
+    if (!packed.empty())
+        test_manifest(packed);
     if (no_gpu) {
         // Without a device, construction fails with the C ABI's message.
         report("HipBackend without a device throws",
@@ -335,6 +451,8 @@ int main(int argc, char **argv) {
     test_bf16_ops(be);
     test_moe(be);
     test_norms(be);
+    if (!packed.empty())
+        test_packed_moe(be, packed);
     test_errors(be);
     Profile::get().print(stdout);
     std::printf("%s (%d failure%s)\n", g_failures ? "FAILED" : "OK", g_failures,

@@ -25,22 +25,36 @@ def run(*args, timeout=300):
     return r
 
 
-def test_host_layer_without_device():
-    """On a machine without a GPU the backend constructor throws std::runtime_error."""
+@pytest.fixture(scope="module")
+def packed_dir(tmp_path_factory):
+    """A small packed model directory in the repack format (2 layers, 16 experts)."""
+    from apex_amd import synth
+    d = tmp_path_factory.mktemp("packed")
+    synth.write_packed_model(d, seed=4, layers=2, E=16, H=512, I=256)
+    return str(d)
+
+
+def test_host_layer_without_device(packed_dir):
+    """On a machine without a GPU the backend constructor throws std::runtime_error;
+    the manifest reader (ModelInfo::load) needs no device."""
     import torch  # noqa: F401  (only to mirror the environment; the check is C++)
     if torch.cuda.is_available():
         pytest.skip("a GPU is present")
-    r = run("--no-gpu")
+    r = run("--no-gpu", "--packed", packed_dir)
     assert r.returncode == 0, r.stdout
     assert "PASS HipBackend without a device throws" in r.stdout
+    for name in ("config and quantization", "expert slot pieces", "layer files", "core tensors",
+                 "unknown tensor throws"):
+        assert f"PASS manifest: {name}" in r.stdout
 
 
 @pytest.mark.gpu
-def test_host_layer_on_gpu():
-    r = run()
+def test_host_layer_on_gpu(packed_dir):
+    r = run("--packed", packed_dir)
     assert r.returncode == 0, r.stdout
     assert "FAIL" not in r.stdout
     for name in ("denseMlp fp32 (4 launches) vs oracle", "denseMlpFused fp32 (2 launches) vs oracle",
                  "matmulNvfp4Bf16 T=96", "moeFfn vs oracle", "rmsNorm vs oracle",
-                 "headNormRope vs oracle", "unknown kernel throws"):
+                 "headNormRope vs oracle", "unknown kernel throws", "manifest: layer files",
+                 "packed router logits vs oracle", "packed MoE block vs oracle"):
         assert f"PASS {name}" in r.stdout
