@@ -17,11 +17,8 @@ namespace apex_hip {
 namespace {
 
 using namespace gemm_core;
-#ifndef APEX_GEMM_WC
-#define APEX_GEMM_WC 4
-#endif
-constexpr int WC = APEX_GEMM_WC;          // wave columns: 4 (1 x 4) or 2 (2 x 2)
-constexpr int MT = WC == 4 ? 8 : 4;       // 32-row MFMA tiles per wave
+constexpr int WC = 4;                     // 1 x 4 waves (the 2 x 2 layout measured slower)
+constexpr int MT = 8;                     // 32-row MFMA tiles per wave
 constexpr int BM = Layout<MT, WC>::kBM;   // 256
 
 // 16-byte epilogue stores need 8-column row pieces at 16-byte aligned addresses.

@@ -54,10 +54,9 @@ constexpr int kWScale = BN * (BK / 16);    // 1 KiB of W scales per stage
 constexpr uint32_t kOut = 0x80000000u;     // an offset no descriptor covers
 // W loads use the default cache policy: a stage takes 32 bytes of each 128-byte code
 // line and 4 bytes of each scale line, so a line serves 4 (codes) or 32 (scales)
-// consecutive stages and must stay in L2 between them.
-#ifndef APEX_GEMM_W_CPOL
-#define APEX_GEMM_W_CPOL 0
-#endif
+// consecutive stages and must stay in L2 between them (the streaming policy of the
+// GEMV re-fetched the lines: 3.8x the L2 misses on the MoE gate/up GEMM).
+constexpr int kWCpol = 0;
 
 template <int MT, int WC = 4> struct Layout {
     static constexpr int kWR = 4 / WC;
@@ -134,10 +133,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     constexpr int kALoads = MT * WR;          // DMA loads of 8 A rows per wave per stage
     constexpr int kLoadsPerStage = kALoads + 2 + 1;
 
-    // Opaque per call: values derived from the thread index are recomputed for every
-    // tile instead of being hoisted out of a caller's tile loop into live registers.
-    int tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
+    const int tid = threadIdx.x;
     const int lane = tid & 63;
     // uniform: LDS destinations (M0) and their arithmetic stay in scalar registers
     const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
@@ -185,10 +181,10 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         for (int i = 0; i < 2; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rc, (lds_void_t *)(base + kAStage + (wave * 128 + i * 64) * 16), 16, wc_off[i],
-                (int)(k0 / 2), 0, APEX_GEMM_W_CPOL);
+                (int)(k0 / 2), 0, kWCpol);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (lds_void_t *)(base + kAStage + kWCode + wave * 64 * 4), 4, ws_off, (int)(k0 / 16),
-            0, APEX_GEMM_W_CPOL);
+            0, kWCpol);
     };
 
 #pragma unroll
@@ -318,11 +314,8 @@ __device__ __forceinline__ void store_tile_bf16(const Acc<MT, WC> &acc, uint16_t
                                                 uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
                                                 float scale, bool wide) {
     constexpr int NT = 8 / WC;
-    // opaque per call (see gemm_tile): no store offsets hoisted out of a tile loop
-    int tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    const int lane = tid & 63;
-    const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
+    const int lane = threadIdx.x & 63;
+    const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)threadIdx.x >> 6);
     const uint32_t cm = 32 * MT * (wave / WC) + (lane & 31);             // row within the tile
     const uint32_t cn = 32 * (8 / WC) * (wave % WC) + 8 * (lane >> 5);   // column within the tile
     const uint64_t rows = M - m0;

@@ -647,6 +647,7 @@ __global__ __launch_bounds__(256) void moe_plan_scatter_kernel(MoeArgs a) {
 
 // Decode: route all T <= 32 tokens (two per wave) and plan, in one workgroup.
 __global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
+    __shared__ int32_t s_ids[kMoeGemvMaxPairs]; // the grouping reads the ids from here
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     for (uint32_t t = wave; t < a.T; t += blockDim.x / 64) {
@@ -656,11 +657,11 @@ __global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
         if ((uint32_t)lane < a.k) {
             a.ids[t * a.k + lane] = id;
             a.w[t * a.k + lane] = wt;
+            s_ids[t * a.k + lane] = id;
         }
     }
-    __threadfence_block();
     __syncthreads();
-    plan_block(a, a.ids, false);
+    plan_block(a, s_ids, false);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1172,14 +1173,25 @@ hipError_t router_launch(const MoeRouterArgs &a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// The most waves a workgroup of the router can have without spilling: per owned expert
+// a lane holds two groups of codes (32 registers), 2 * TT partial logits, 4 decoded
+// codes and 3 offsets / scales, plus about 40 of its own; a SIMD's 512 registers are
+// shared by WAVES / 4 waves.
+constexpr int router_waves(int TT, int EPL, int want) {
+    const int need = EPL * (32 + 2 * TT + 7) + 40;
+    int w = want;
+    while (w > 4 && need > 512 / (w / 4))
+        w /= 2;
+    return w;
+}
+
 template <int TT, int WAVES>
 hipError_t router_launch_epl(const MoeRouterArgs &a, hipStream_t stream) {
     switch ((a.E + 63) / 64) {
-    case 1: return router_launch<TT, 1, WAVES>(a, stream);
-    case 2: return router_launch<TT, 2, WAVES>(a, stream);
-    case 3: return router_launch<TT, 3, WAVES>(a, stream);
-    default: // 4 experts per lane: at most 8 waves, or the registers spill
-        return router_launch<TT, 4, (WAVES > 8 ? 8 : WAVES)>(a, stream);
+    case 1: return router_launch<TT, 1, router_waves(TT, 1, WAVES)>(a, stream);
+    case 2: return router_launch<TT, 2, router_waves(TT, 2, WAVES)>(a, stream);
+    case 3: return router_launch<TT, 3, router_waves(TT, 3, WAVES)>(a, stream);
+    default: return router_launch<TT, 4, router_waves(TT, 4, WAVES)>(a, stream);
     }
 }
 
