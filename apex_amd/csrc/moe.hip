@@ -69,7 +69,7 @@ __device__ __forceinline__ float uniform_f(float v) {
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct PlanView {
-    int32_t *hdr, *cnt, *off, *act, *pos_of_pair, *pair_of_pos, *tiles;
+    int32_t *hdr, *cnt, *off, *act, *pos_of_pair, *pair_of_pos, *tiles, *groups;
 };
 
 __host__ __device__ inline PlanView plan_view(int32_t *plan, uint32_t E, uint32_t P) {
@@ -80,7 +80,8 @@ __host__ __device__ inline PlanView plan_view(int32_t *plan, uint32_t E, uint32_
     v.act = v.off + E + 1;
     v.pos_of_pair = v.act + E;
     v.pair_of_pos = v.pos_of_pair + P;
-    v.tiles = v.pair_of_pos + P;
+    v.groups = v.pair_of_pos + P;
+    v.tiles = v.groups + 2 * P;
     return v;
 }
 
@@ -90,7 +91,7 @@ __host__ __device__ inline PlanView plan_view(int32_t *plan, uint32_t E, uint32_
 
 // Maximum of a 64-bit key over the wave: DPP within rows of 16 lanes (quad swaps, then
 // half-row and row mirrors pair every lane with one of the other half), then the two
-// cross-row steps by lane shuffles.
+// cross-row steps by VALU lane swaps (v_permlane16_swap / v_permlane32_swap).
 template <int CTRL> __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
     const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
     const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
@@ -103,12 +104,17 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     o = dpp_u64<0x4E>(v);  v = o > v ? o : v;  // quad_perm [2,3,0,1]
     o = dpp_u64<0x141>(v); v = o > v ? o : v;  // row_half_mirror
     o = dpp_u64<0x140>(v); v = o > v ? o : v;  // row_mirror
-#pragma unroll
-    for (int x = 16; x <= 32; x <<= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)v, x, 64);
-        const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), x, 64);
-        o = ((uint64_t)hi << 32) | lo;
-        v = o > v ? o : v;
+    {
+        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        const uint64_t a0 = ((uint64_t)hi[0] << 32) | lo[0], a1 = ((uint64_t)hi[1] << 32) | lo[1];
+        v = a0 > a1 ? a0 : a1;
+    }
+    {
+        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        const uint64_t a0 = ((uint64_t)hi[0] << 32) | lo[0], a1 = ((uint64_t)hi[1] << 32) | lo[1];
+        v = a0 > a1 ? a0 : a1;
     }
     return v;
 }
@@ -150,13 +156,10 @@ __device__ __forceinline__ void route_token_by(Logit logit, uint32_t E, uint32_t
             my_v = __uint_as_float((ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord);
         }
     }
-    const float vmax = __shfl(my_v, 0, 64); // slot 0 holds the largest logit
-    float p = (uint32_t)lane < k ? expf(my_v - vmax) : 0.0f;
-    float z = p;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1)
-        z += __shfl_xor(z, o, 64);
-    my_w = p / z;
+    // slot 0 holds the largest logit
+    const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
+    const float p = (uint32_t)lane < k ? expf(my_v - vmax) : 0.0f;
+    my_w = p / group_sum<64>(p);
 }
 
 // route_token_by over one token's bf16 logits.
@@ -388,9 +391,8 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *logits, 
 // exclusive scans over the experts, so every expert's entries are written in
 // parallel.  `first` receives each expert's first position.
 constexpr int kPlanScans = 5; // pair counts, active flags, class 0/1/2 tile counts
-constexpr int kPlanBatch = 8; // pairs per thread whose loads are issued together
 
-__device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first, bool tiles) {
+__device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first) {
     __shared__ int scan[kPlanScans][kMoeMaxExperts];
     const uint32_t E = a.E, P = a.T * a.k;
     const PlanView v = plan_view(a.plan, E, P);
@@ -433,24 +435,22 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first, bool til
         v.cnt[e] = c;
         if (c > 0)
             v.act[scan[1][e] - 1] = e;
-        if (tiles) {
-            int slot = -1, cls = 0;
-            const int full = c / 256;
-            int t0 = scan[2][e] - val[2];
-            for (int f = 0; f < full; ++f) {
-                int32_t *t = v.tiles + 4 * (t0 + f);
-                t[0] = e, t[1] = off + 256 * f, t[2] = 256, t[3] = 0;
-            }
-            if (rem > 128)
-                slot = t0 + full, cls = 0;
-            else if (rem > 64)
-                slot = n0 + scan[3][e] - 1, cls = 1;
-            else if (rem > 0)
-                slot = n0 + n1 + scan[4][e] - 1, cls = 2;
-            if (slot >= 0) {
-                int32_t *t = v.tiles + 4 * slot;
-                t[0] = e, t[1] = off + 256 * full, t[2] = rem, t[3] = cls;
-            }
+        int slot = -1, cls = 0;
+        const int full = c / 256;
+        int t0 = scan[2][e] - val[2];
+        for (int f = 0; f < full; ++f) {
+            int32_t *t = v.tiles + 4 * (t0 + f);
+            t[0] = e, t[1] = off + 256 * f, t[2] = 256, t[3] = 0;
+        }
+        if (rem > 128)
+            slot = t0 + full, cls = 0;
+        else if (rem > 64)
+            slot = n0 + scan[3][e] - 1, cls = 1;
+        else if (rem > 0)
+            slot = n0 + n1 + scan[4][e] - 1, cls = 2;
+        if (slot >= 0) {
+            int32_t *t = v.tiles + 4 * slot;
+            t[0] = e, t[1] = off + 256 * full, t[2] = rem, t[3] = cls;
         }
     }
     if (tid == 0) {
@@ -460,54 +460,6 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first, bool til
         v.hdr[2] = n0;
     }
     __syncthreads();
-}
-
-// Grouping of the P = T*k pairs by expert in one workgroup of 1024 threads (decode:
-// P <= 256): counts by LDS atomics, plan_scan, then each pair's position in its
-// expert's group by a second round of atomics.
-__device__ void plan_block(const MoeArgs &a, const int32_t *ids, bool tiles) {
-    __shared__ int cnt[kMoeMaxExperts], cur[kMoeMaxExperts];
-    const uint32_t E = a.E, P = a.T * a.k;
-    const PlanView v = plan_view(a.plan, E, P);
-    const int tid = threadIdx.x;
-    if (tid < (int)kMoeMaxExperts)
-        cnt[tid] = 0;
-    __syncthreads();
-    // Pairs in batches of kPlanBatch per thread: the batch's loads are all in flight
-    // before its atomics (a load -> atomic -> store chain per pair is latency-bound).
-    for (uint32_t p0 = 0; p0 < P; p0 += blockDim.x * kPlanBatch) {
-        int e[kPlanBatch];
-#pragma unroll
-        for (int b = 0; b < kPlanBatch; ++b) {
-            const uint32_t p = p0 + b * blockDim.x + tid;
-            e[b] = p < P ? ids[p] : -1;
-        }
-#pragma unroll
-        for (int b = 0; b < kPlanBatch; ++b)
-            if (e[b] >= 0)
-                atomicAdd(&cnt[e[b]], 1);
-    }
-    __syncthreads();
-    plan_scan(a, cnt, cur, tiles);
-    for (uint32_t p0 = 0; p0 < P; p0 += blockDim.x * kPlanBatch) {
-        int e[kPlanBatch], pos[kPlanBatch];
-#pragma unroll
-        for (int b = 0; b < kPlanBatch; ++b) {
-            const uint32_t p = p0 + b * blockDim.x + tid;
-            e[b] = p < P ? ids[p] : -1;
-        }
-#pragma unroll
-        for (int b = 0; b < kPlanBatch; ++b)
-            pos[b] = e[b] >= 0 ? atomicAdd(&cur[e[b]], 1) : 0;
-#pragma unroll
-        for (int b = 0; b < kPlanBatch; ++b) {
-            const uint32_t p = p0 + b * blockDim.x + tid;
-            if (e[b] >= 0) {
-                v.pos_of_pair[p] = pos[b];
-                v.pair_of_pos[pos[b]] = (int32_t)p;
-            }
-        }
-    }
 }
 
 // Prefill grouping, deterministic and free of contended atomics, in three launches.
@@ -593,7 +545,7 @@ __global__ __launch_bounds__(1024) void moe_plan_scan_kernel(MoeArgs a) {
                 cnt[e] = run;
         }
         __syncthreads();
-        plan_scan(a, cnt, first, true);
+        plan_scan(a, cnt, first);
         return;
     }
     int sum = 0;
@@ -629,7 +581,7 @@ __global__ __launch_bounds__(1024) void moe_plan_scan_kernel(MoeArgs a) {
             cnt[e] = run;
     }
     __syncthreads();
-    plan_scan(a, cnt, first, true);
+    plan_scan(a, cnt, first);
 }
 
 __global__ __launch_bounds__(256) void moe_plan_scatter_kernel(MoeArgs a) {
@@ -645,23 +597,122 @@ __global__ __launch_bounds__(256) void moe_plan_scatter_kernel(MoeArgs a) {
     v.pair_of_pos[pos] = (int32_t)p;
 }
 
-// Decode: route all T <= 32 tokens (two per wave) and plan, in one workgroup.
+// Exclusive prefix sum over the 64 lanes of a wave (Kogge-Stone); `total` receives
+// the sum of all lanes.
+__device__ __forceinline__ int wave_excl_scan(int x, int lane, int &total) {
+    int incl = x;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d, 64);
+        if (lane >= d)
+            incl += o;
+    }
+    total = __builtin_amdgcn_readlane(incl, 63);
+    return incl - x;
+}
+
+// Decode plan from the experts' token masks (bit t of mask[e]: token t chose expert e),
+// by one wave: lane l owns experts 4l..4l+3.  Counts, offsets (pairs grouped by expert,
+// experts ascending, each expert's tokens ascending), the active list and the token
+// groups (sizes 4, 3, 2, 1 in that order, see moe_gemv_kernel) -> plan; offsets also
+// -> s_off.
+__device__ void plan_from_masks(const MoeArgs &a, const uint32_t *mask, int32_t *s_off, int lane) {
+    static_assert(kTokenGroup == 4 && kMoeMaxExperts == 256, "4 experts per lane, group sizes 4..1");
+    const uint32_t E = a.E, P = a.T * a.k;
+    const PlanView v = plan_view(a.plan, E, P);
+    int c[4];
+    int sum[6] = {}; // pairs, active experts, groups of 4, of 3, of 2, of 1
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t e = 4 * lane + q;
+        c[q] = e < E ? __popc(mask[e]) : 0;
+        sum[0] += c[q];
+        sum[1] += c[q] > 0;
+        sum[2] += c[q] / 4;
+        sum[3] += c[q] % 4 == 3;
+        sum[4] += c[q] % 4 == 2;
+        sum[5] += c[q] % 4 == 1;
+    }
+    int base[6], total[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+        base[i] = wave_excl_scan(sum[i], lane, total[i]);
+    // first group slot of each class: sizes 4, 3, 2, 1 in that order
+    const int cls0[4] = {0, total[2], total[2] + total[3], total[2] + total[3] + total[4]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t e = 4 * lane + q;
+        if (e >= E)
+            break;
+        const int n = c[q], off = base[0];
+        s_off[e] = off;
+        v.off[e] = off;
+        v.cnt[e] = n;
+        if (n > 0)
+            v.act[base[1]++] = (int32_t)e;
+        for (int f = 0; f < n / 4; ++f) {
+            const int g = cls0[0] + base[2]++;
+            v.groups[2 * g] = (int32_t)e;
+            v.groups[2 * g + 1] = (off + 4 * f) | (4 << 16);
+        }
+        const int r = n % 4;
+        if (r > 0) {
+            const int cls = 4 - r; // 1 (3 tokens) .. 3 (1 token)
+            const int g = cls0[cls] + base[2 + cls]++;
+            v.groups[2 * g] = (int32_t)e;
+            v.groups[2 * g + 1] = (off + 4 * (n / 4)) | (r << 16);
+        }
+        base[0] += n;
+    }
+    if (lane == 0) {
+        v.off[E] = total[0];
+        v.hdr[0] = total[1];
+        v.hdr[1] = 0;
+        v.hdr[2] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            v.hdr[3 + i] = total[2 + i];
+    }
+}
+
+// Decode: route all T <= 32 tokens (one per wave) and plan, in one workgroup, with
+// no atomics whose order matters: each routed pair sets its token's bit in its
+// expert's mask (LDS atomicOr), one wave turns the masks into the plan, and a pair's
+// position is its expert's offset plus the number of its expert's tokens below its
+// own (so positions do not depend on timing).
 __global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
-    __shared__ int32_t s_ids[kMoeGemvMaxPairs]; // the grouping reads the ids from here
+    __shared__ uint32_t s_mask[kMoeMaxExperts];
+    __shared__ int32_t s_off[kMoeMaxExperts];
+    __shared__ int32_t s_ids[kMoeGemvMaxPairs];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const uint32_t k = a.k, P = a.T * k;
+    if (threadIdx.x < kMoeMaxExperts)
+        s_mask[threadIdx.x] = 0;
+    __syncthreads();
     for (uint32_t t = wave; t < a.T; t += blockDim.x / 64) {
         int32_t id;
         float wt;
         route_token_args(a, t, lane, id, wt);
-        if ((uint32_t)lane < a.k) {
-            a.ids[t * a.k + lane] = id;
-            a.w[t * a.k + lane] = wt;
-            s_ids[t * a.k + lane] = id;
+        if ((uint32_t)lane < k) {
+            a.ids[t * k + lane] = id;
+            a.w[t * k + lane] = wt;
+            s_ids[t * k + lane] = id;
+            atomicOr(&s_mask[id], 1u << t);
         }
     }
     __syncthreads();
-    plan_block(a, s_ids, false);
+    if (wave == 0)
+        plan_from_masks(a, s_mask, s_off, lane);
+    __syncthreads();
+    const PlanView v = plan_view(a.plan, a.E, P);
+    for (uint32_t p = threadIdx.x; p < P; p += blockDim.x) {
+        const uint32_t t = p / k;
+        const int e = s_ids[p];
+        const int pos = s_off[e] + __popc(s_mask[e] & ((1u << t) - 1u));
+        v.pos_of_pair[p] = pos;
+        v.pair_of_pos[pos] = (int32_t)p;
+    }
 }
 
 // ---------------------------------------------------------------------------------
@@ -722,46 +773,153 @@ __device__ __forceinline__ void rows_dot(float (&out)[NR], const RowRegs<SLOTS> 
         pass(std::true_type{});
 }
 
-// Grouped GEMV over the active experts' row blocks.  A unit is (active expert, NB
-// row sets of 64/G rows); persistent waves walk the units, and each unit's weight rows
-// stream once for every token routed to its expert.
+// chunk_dot with the chunk's codes already decoded (wd[4 p + j] = elements 8 p + 2 j
+// and 8 p + 2 j + 1).
+__device__ __forceinline__ void chunk_dot_decoded(const bf16x2_t (&wd)[16], f32x2_t s,
+                                                  const XChunk<uint16_t> &x, float &acc) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        float partial = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int p = 2 * b + h;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t xw = x.p[p][j];
+                partial = __builtin_amdgcn_fdot2_f32_bf16(wd[4 * p + j],
+                                                          __builtin_bit_cast(bf16x2_t, xw),
+                                                          partial, false);
+            }
+        }
+        acc = __builtin_fmaf(s[b], partial, acc);
+    }
+}
+
+// Dots of NR weight rows with the activation rows of n <= TG tokens (one group of an
+// expert's positions): each slot's codes are decoded once and dotted with every
+// token's chunk `xslot(t, s)`, so the half-rate conversions are shared by the group.
+// Same arithmetic per (row, token) as rows_dot; NaN results are recomputed with the
+// exact E4M3 decode.
+template <int G, int SLOTS, int NR, int TG, typename XSlot>
+__device__ __forceinline__ void rows_dot_group(float (&out)[TG][NR], const RowRegs<SLOTS> (&w)[NR],
+                                               int n, XSlot xslot) {
+    auto pass = [&](auto exact) {
+#pragma unroll
+        for (int t = 0; t < TG; ++t)
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+                out[t][r] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            bf16x2_t wd[NR][16];
+            f32x2_t sc[NR];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                // decode after the previous slot's dots: one slot of decoded rows live
+                u32x4_t cw = w[r].codes[s];
+                asm volatile("" : "+v"(cw) : "v"(out[0][NR - 1]));
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+                    e2m1x8_to_bf16(cw[p], &wd[r][4 * p]);
+                sc[r] = chunk_scales<decltype(exact)::value>(w[r].scales[s]);
+            }
+#pragma unroll
+            for (int t = 0; t < TG; ++t) {
+                if (t >= n)
+                    break;
+                const XChunk<uint16_t> xc = xslot(t, s);
+#pragma unroll
+                for (int r = 0; r < NR; ++r)
+                    chunk_dot_decoded(wd[r], sc[r], xc, out[t][r]);
+                // one token's x chunk in registers at a time
+                asm volatile("" ::"v"(out[t][NR - 1]) : "memory");
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TG; ++t) {
+            if (t >= n)
+                break;
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+                out[t][r] = group_sum<G>(out[t][r]);
+        }
+    };
+    pass(std::false_type{});
+    bool nan = false;
+#pragma unroll
+    for (int t = 0; t < TG; ++t)
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            nan |= t < n && __builtin_isnan(out[t][r]);
+    if (nan)
+        pass(std::true_type{});
+}
+
+// Grouped GEMV over the routed (token, expert) pairs, in items of equal cost per
+// class that persistent waves walk round-robin, so they get equal shares however
+// unevenly the tokens spread over experts.
+//   TG == 1: item (rb, pos) = row block rb (NB row sets of 64/G rows) of pos's expert
+//     dotted with pos's activation row; item i = (i / P, i % P), so the n positions
+//     of one expert are consecutive and the n items streaming the same weight rows
+//     run on adjacent waves of one workgroup (all but the first read them from L2).
+//   TG > 1 (x in LDS): item (rb, g) = row block rb of group g's expert dotted with the
+//     rows of the group's n <= TG tokens, decoding the weights once for all of them.
+//     Items are dealt class by class (groups of 4 tokens first, then 3, 2, 1), each
+//     class rb-major, round-robin over workgroups first, so every CU and SIMD gets an
+//     equal share of every cost class.
 //   GATE_UP: K = H, gate and up rows side by side, GeGLU -> h[pos][row] (bf16).
 //   else:    K = I, down rows, x = h[pos] -> d[pos][row] (bf16).
 // XLDS: all T activation rows are staged in LDS once per workgroup (piece-major, so
 // a wave's 16-byte reads of one piece of consecutive chunks are conflict-free) and
-// read from there; otherwise each token's row is loaded from global memory (L2).
+// read from there; otherwise each item's row is loaded from global memory (L2).
+// Double-buffering the weights (next item's loads during this item's arithmetic)
+// measured slower at every shape: four waves per SIMD already cover the latency and
+// the second register set costs occupancy or spills.
 constexpr int kGemvBlocksPerCU = 4; // 256-thread workgroups per CU (global x)
-// x in LDS: one workgroup of 16 waves per CU.  Measured on the 16-token decode step:
-// 16 waves without a prefetch register set beat 12 waves with one (the set costs ~30
-// VGPRs); kXLdsPrefetch keeps the double-buffered variant available.
-constexpr int kXLdsThreads = 1024;
-constexpr bool kXLdsPrefetch = false;
+constexpr int kXLdsThreads = 1024;  // x in LDS: one workgroup of 16 waves per CU
 constexpr uint32_t kXLdsBytes = 120 * 1024;
 
-template <bool GATE_UP, int G, int SLOTS, int NB, bool XLDS>
+template <bool GATE_UP, int G, int SLOTS, int NB, bool XLDS, int TG>
 __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 256 : 4) void moe_gemv_kernel(MoeArgs a) {
+    static_assert(TG == 1 || (XLDS && TG == kTokenGroup), "token groups read x from LDS");
     constexpr int R = 64 / G;          // rows per row set
     constexpr int NM = GATE_UP ? 2 : 1;
-    // The plan (at most 256 experts and 256 pairs here) is staged in LDS once, so the
-    // per-unit lookups are LDS reads that never wait behind the weight stream.
-    __shared__ int s_act[kMoeMaxExperts], s_cnt[kMoeMaxExperts], s_off[kMoeMaxExperts];
-    __shared__ uint32_t s_xrow[kMoeGemvMaxPairs]; // activation row of pos (token or pos)
+    constexpr int NR = NM * NB;
+    // TG == 1: s_exp[pos] = expert of grouped position pos.  TG > 1: s_exp[g] = expert
+    // of group g, s_grp[g] = its first position | size << 16.  s_xrow[pos] = activation
+    // row of pos (token or pos).  Staged in LDS so the per-item lookups never wait
+    // behind the weight stream.
+    __shared__ int s_exp[kMoeGemvMaxPairs];
+    __shared__ uint32_t s_grp[TG > 1 ? kMoeGemvMaxPairs : 1];
+    __shared__ uint32_t s_xrow[kMoeGemvMaxPairs];
     extern __shared__ uint4 xl[];                 // XLDS: [T][4 pieces][nchunks + 1]
     const int lane = threadIdx.x & 63;
     const int sub = lane / G, gl = lane % G;
-    const uint32_t E = a.E, P = a.T * a.k, H = a.H, I = a.I;
+    const uint32_t P = a.T * a.k, H = a.H, I = a.I;
     const uint32_t K = GATE_UP ? H : I, rows = GATE_UP ? I : H;
     const int nchunks = (int)(K / 32);
-    const PlanView v = plan_view(a.plan, E, P);
+    const PlanView v = plan_view(a.plan, a.E, P);
     const __amdgpu_buffer_rsrc_t rx =
         GATE_UP ? make_rsrc(a.x, a.T * H * 2) : make_rsrc(a.h, P * I * 2);
-    for (uint32_t i = threadIdx.x; i < E; i += blockDim.x) {
-        s_act[i] = v.act[i];
-        s_cnt[i] = v.cnt[i];
-        s_off[i] = v.off[i];
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
+        const uint32_t pair = (uint32_t)v.pair_of_pos[i];
+        if constexpr (TG == 1)
+            s_exp[i] = a.ids[pair];
+        s_xrow[i] = GATE_UP ? pair / a.k : i;
     }
-    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x)
-        s_xrow[i] = GATE_UP ? (uint32_t)v.pair_of_pos[i] / a.k : i;
+    uint32_t ncls[kTokenGroup] = {}; // TG > 1: groups of size 4, 3, 2, 1
+    uint32_t ng = 0;
+    if constexpr (TG > 1) {
+#pragma unroll
+        for (int q = 0; q < kTokenGroup; ++q) {
+            ncls[q] = uniform(v.hdr[3 + q]);
+            ng += ncls[q];
+        }
+        for (uint32_t i = threadIdx.x; i < ng; i += blockDim.x) {
+            s_exp[i] = v.groups[2 * i];
+            s_grp[i] = (uint32_t)v.groups[2 * i + 1];
+        }
+    }
     if constexpr (XLDS) {
         // entry (t, piece q, chunk c) = bytes [64 c + 16 q, +16) of row t; chunk nchunks
         // of every (t, q) plane is zero (its load lies past the descriptor), so lanes past
@@ -775,12 +933,11 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
             xl[(t * 4 + q) * nc + c] = __builtin_bit_cast(uint4, load_b128(rx, off));
         }
     }
-    const uint32_t U = uniform(v.hdr[0]);
     __syncthreads();
     const uint32_t wave = uniform(threadIdx.x >> 6);
     const uint32_t waves_per_block = blockDim.x / 64;
     const uint32_t per_e = (rows + R * NB - 1) / (R * NB);
-    const uint32_t units = U * per_e;
+    const uint32_t items = per_e * (TG > 1 ? ng : P);
     const bool last_ok = gl + (SLOTS - 1) * G < nchunks;
     const uint32_t last_c = last_ok ? (SLOTS - 1) * G * 16 : kOutOfRange;
     const uint32_t last_s = last_ok ? (SLOTS - 1) * G * 2 : kOutOfRange;
@@ -789,13 +946,34 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     const uint32_t wbytes = rows * K / 2, sbytes = rows * K / 16;
     const uint32_t nw = gridDim.x * waves_per_block;
 
-    // Loads of unit u into `w` (a unit past the end loads nothing).
-    auto issue = [&](RowRegs<SLOTS> (&w)[NM * NB], uint32_t u) {
-        if (u >= units)
+    // item it -> (row block, position or group)
+    auto locate = [&](uint32_t it, uint32_t &rb, uint32_t &j) {
+        if constexpr (TG == 1) {
+            rb = it / P;
+            j = it - rb * P;
+        } else {
+            uint32_t g0 = 0;
+#pragma unroll
+            for (int q = 0; q < kTokenGroup; ++q) {
+                const uint32_t nq = ncls[q];
+                if (it < per_e * nq) {
+                    rb = it / nq;
+                    j = g0 + (it - rb * nq);
+                    return;
+                }
+                it -= per_e * nq;
+                g0 += nq;
+            }
+        }
+    };
+    // Loads of item it's weight rows into `w` (nothing for an item past the end).
+    auto issue = [&](RowRegs<SLOTS> (&w)[NR], uint32_t it) {
+        if (it >= items)
             return;
-        const uint32_t ai = u / per_e;
-        const uint32_t r0 = (u - ai * per_e) * R * NB;
-        const uint8_t *slot = a.slots.base + (size_t)uniform(s_act[ai]) * a.slots.stride;
+        uint32_t rb, j;
+        locate(it, rb, j);
+        const uint32_t r0 = rb * R * NB;
+        const uint8_t *slot = a.slots.base + (size_t)uniform(s_exp[j]) * a.slots.stride;
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -806,67 +984,72 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
                                    K, last_c, last_s);
             }
     };
-    // Every token of unit u's expert against the rows in `w`.
-    auto compute = [&](const RowRegs<SLOTS> (&w)[NM * NB], uint32_t u) {
-        const uint32_t ai = u / per_e;
-        const uint32_t r0 = (u - ai * per_e) * R * NB;
-        const int e = uniform(s_act[ai]);
-        const int n = uniform(s_cnt[e]), p0 = uniform(s_off[e]);
-        for (int i = 0; i < n; ++i) {
-            const int pos = p0 + i;
-            const uint32_t xr = uniform(s_xrow[pos]);
-            float dots[NM * NB];
-            if constexpr (XLDS) {
-                rows_dot<G, SLOTS, NM * NB, true>(dots, w, [&](int s) {
-                    const int c = min(gl + s * G, nchunks); // chunk nchunks is zero
-                    const uint4 *plane = xl + xr * 4 * (nchunks + 1) + c;
-                    XChunk<uint16_t> xc;
+    // x chunk of slot s of activation row xr, from LDS
+    auto lds_x = [&](uint32_t xr, int s) {
+        const int c = min(gl + s * G, nchunks); // chunk nchunks is zero
+        const uint4 *plane = xl + xr * 4 * (nchunks + 1) + c;
+        XChunk<uint16_t> xc;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        xc.p[q] = __builtin_bit_cast(u32x4_t, plane[q * (nchunks + 1)]);
-                    return xc;
-                });
+        for (int q = 0; q < 4; ++q)
+            xc.p[q] = __builtin_bit_cast(u32x4_t, plane[q * (nchunks + 1)]);
+        return xc;
+    };
+    // the bf16 outputs of one (row set b, position pos) from its dots
+    auto store = [&](const float *dots, uint32_t r0, uint32_t pos) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const uint32_t row = r0 + b * R + sub;
+            if (row >= rows)
+                continue;
+            if constexpr (GATE_UP)
+                a.h[(size_t)pos * I + row] = f32_to_bf16_bits(gelu_tanh_fast(dots[b]) * dots[NB + b]);
+            else
+                a.d[(size_t)pos * H + row] = f32_to_bf16_bits(dots[b]);
+        }
+    };
+    // Item it's rows (loaded into `w`) against its activation rows.
+    auto compute = [&](const RowRegs<SLOTS> (&w)[NR], uint32_t it) {
+        uint32_t rb, j;
+        locate(it, rb, j);
+        const uint32_t r0 = rb * R * NB;
+        if constexpr (TG == 1) {
+            const uint32_t xr = uniform(s_xrow[j]);
+            float dots[NR];
+            if constexpr (XLDS) {
+                rows_dot<G, SLOTS, NR, true>(dots, w, [&](int s) { return lds_x(xr, s); });
             } else {
-                rows_dot<G, SLOTS, NM * NB, false>(dots, w, [&](int s) {
+                rows_dot<G, SLOTS, NR, false>(dots, w, [&](int s) {
                     return load_x_slot<G>(rx, xr * K * 2, gl, s, nchunks);
                 });
             }
-            if (gl != 0)
-                continue;
+            if (gl == 0)
+                store(dots, r0, j);
+        } else {
+            const uint32_t gp = uniform(s_grp[j]);
+            const int p0 = (int)(gp & 0xFFFFu), n = (int)(gp >> 16);
+            float dots[TG][NR];
+            rows_dot_group<G, SLOTS, NR, TG>(dots, w, n, [&](int t, int s) {
+                return lds_x(uniform(s_xrow[p0 + t]), s);
+            });
+            if (gl == 0)
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const uint32_t row = r0 + b * R + sub;
-                if (row >= rows)
-                    continue;
-                if constexpr (GATE_UP)
-                    a.h[(size_t)pos * I + row] = f32_to_bf16_bits(gelu_tanh(dots[b]) * dots[NB + b]);
-                else
-                    a.d[(size_t)pos * H + row] = f32_to_bf16_bits(dots[b]);
-            }
+                for (int t = 0; t < TG; ++t) {
+                    if (t >= n)
+                        break;
+                    store(dots[t], r0, p0 + t);
+                }
         }
     };
 
-    const uint32_t u0 = blockIdx.x * waves_per_block + wave;
-    if constexpr (XLDS && kXLdsPrefetch) {
-        // Activations come from LDS, so the next unit's weight loads can be in flight
-        // while this unit computes (two register sets, body unrolled twice so the
-        // buffer indices are constants).
-        RowRegs<SLOTS> wa[NM * NB], wb[NM * NB];
-        issue(wa, u0);
-        for (uint32_t u = u0; u < units; u += 2 * nw) {
-            issue(wb, u + nw);
-            compute(wa, u);
-            if (u + nw >= units)
-                break;
-            issue(wa, u + 2 * nw);
-            compute(wb, u + nw);
-        }
-    } else {
-        for (uint32_t u = u0; u < units; u += nw) {
-            RowRegs<SLOTS> w[NM * NB];
-            issue(w, u);
-            compute(w, u);
-        }
+    // TG == 1: consecutive items (which share weight rows) on the waves of one
+    // workgroup.  TG > 1: consecutive items on consecutive workgroups, so every CU (and
+    // every SIMD) gets an even share of each cost class.
+    const uint32_t first = TG == 1 ? blockIdx.x * waves_per_block + wave
+                                   : wave * gridDim.x + blockIdx.x;
+    for (uint32_t it = first; it < items; it += nw) {
+        RowRegs<SLOTS> w[NR];
+        issue(w, it);
+        compute(w, it);
     }
 }
 
@@ -1077,7 +1260,7 @@ MoeWorkspace moe_workspace(uint32_t T, uint32_t E, uint32_t k, uint32_t H, uint3
     w.w = off;
     off = align256(off + P * 4);
     w.plan = off;
-    off = align256(off + 4 * ((size_t)kMoePlanHeader + 3 * E + 1 + 2 * P + 4 * (size_t)w.max_tiles));
+    off = align256(off + 4 * ((size_t)kMoePlanHeader + 3 * E + 1 + 4 * P + 4 * (size_t)w.max_tiles));
     w.h = off;
     off = align256(off + P * I * 2);
     w.d = off;
@@ -1222,29 +1405,31 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
             hipError_t err = hipSuccess;
             switch (gemv_slots(a.H, 32)) {
             case 1:
-                err = set_lds(moe_gemv_kernel<true, 32, 1, 2, true>, kXLdsBytes, attr[0]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, true>), lgrid, lblock, xbytes, stream, a);
+                err = set_lds(moe_gemv_kernel<true, 32, 1, 2, true, 1>, kXLdsBytes, attr[0]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, true, 1>), lgrid, lblock, xbytes, stream, a);
                 break;
             case 2:
-                err = set_lds(moe_gemv_kernel<true, 32, 2, 1, true>, kXLdsBytes, attr[1]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 1, true>), lgrid, lblock, xbytes, stream, a);
+                err = set_lds(moe_gemv_kernel<true, 32, 2, 1, true, kTokenGroup>, kXLdsBytes, attr[1]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 1, true, kTokenGroup>), lgrid, lblock, xbytes, stream, a);
                 break;
             default:
-                err = set_lds(moe_gemv_kernel<true, 32, 3, 1, true>, kXLdsBytes, attr[2]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, true>), lgrid, lblock, xbytes, stream, a);
+                err = set_lds(moe_gemv_kernel<true, 32, 3, 1, true, kTokenGroup>, kXLdsBytes, attr[2]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, true, kTokenGroup>), lgrid, lblock, xbytes, stream, a);
                 break;
             }
             if (err != hipSuccess)
                 return err;
         } else {
             switch (gemv_slots(a.H, 32)) {
-            case 1: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, false>), grid, block, 0, stream, a); break;
-            case 2: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 2, false>), grid, block, 0, stream, a); break;
-            default: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, false>), grid, block, 0, stream, a); break;
+            case 1: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, false, 1>), grid, block, 0, stream, a); break;
+            case 2: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 2, false, 1>), grid, block, 0, stream, a); break;
+            default: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, false, 1>), grid, block, 0, stream, a); break;
             }
         }
-        // down: 32 lanes per row (one slot for I <= 1024), 8 row sets (16 rows) per unit
-        hipLaunchKernelGGL((moe_gemv_kernel<false, 32, 1, 8, false>), grid, block, 0, stream, a);
+        // down: 32 lanes per row (one slot for I <= 1024), 8 row sets (16 rows) per item;
+        // 8 or 16 lanes per row (fewer idle lanes at 22 chunks) re-read x per fewer rows
+        // and measured slower
+        hipLaunchKernelGGL((moe_gemv_kernel<false, 32, 1, 8, false, 1>), grid, block, 0, stream, a);
         hipLaunchKernelGGL(moe_combine_kernel, dim3(a.T, (a.H + kCombineCols - 1) / kCombineCols),
                            dim3(256), 0, stream, a);
         return hipGetLastError();

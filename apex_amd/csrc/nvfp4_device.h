@@ -109,6 +109,20 @@ __device__ __forceinline__ float gelu_tanh_fast(float g) {
 
 // Sum over aligned groups of G lanes (G in {8, 16, 32, 64}) of a wave64; every lane
 // of a group receives the group total.  DPP within rows of 16, then cross-row swaps.
+// v(l) + v(l ^ 16) and v(l) + v(l ^ 32) by VALU lane swaps (v_permlane16_swap swaps the
+// odd rows of its first operand with the even rows of its second, v_permlane32_swap
+// the upper half of the first with the lower half of the second; with both operands
+// v, lane l of the two results holds v(l) and its partner in row order).  Both lanes
+// of a pair add the same two values in the same order, so they agree bit for bit.
+__device__ __forceinline__ float add_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
     static_assert(G == 8 || G == 16 || G == 32 || G == 64, "group size");
@@ -118,9 +132,9 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 16)
         v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)); // row_mirror
     if constexpr (G >= 32)
-        v += __shfl_xor(v, 16, 64);
+        v = add_xor16(v);
     if constexpr (G >= 64)
-        v += __shfl_xor(v, 32, 64);
+        v = add_xor32(v);
     return v;
 }
 

@@ -99,6 +99,21 @@ def test_moe_odd_shapes(path):
         assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16, (T, E, H, I, k)
 
 
+def test_moe_decode_gemv_variants():
+    """The grouped-GEMV path's other kernel variants: down rows over 16 lanes (I of 30
+    and 32 chunks), gate/up with one and two slots, and x read from global memory
+    (32 tokens of hidden 3072 do not fit the LDS staging), with 256 (token, expert)
+    pairs, the most the path takes."""
+    rng = np.random.default_rng(11)
+    for T, E, H, I, k in [(4, 12, 512, 1024, 2), (5, 9, 1536, 960, 3),
+                          (32, 64, 3072, 256, 8)]:
+        x = synth.normal_bf16(rng, (T, H))
+        logits = synth.normal_bf16(rng, (T, E))
+        slots = synth.expert_slots(rng, E, H, I)
+        got = run_moe(x, logits, slots, k, 1)
+        assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16, (T, E, H, I, k)
+
+
 def test_moe_decode_full_size_both_paths():
     """MoE decode: 16 tokens, hidden 2816, 128 experts, top-8, intermediate 704, seed 0."""
     x, logits, slots = synth.moe_decode_case(seed=0)
