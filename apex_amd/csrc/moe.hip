@@ -119,6 +119,59 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false)); // row_half_mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false)); // row_mirror
+    const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(r16[0], r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max(r32[0], r32[1]);
+}
+
+// route_token_by for bf16 logits, whose key fits 32 bits: the order-preserving image
+// of the 16 logit bits above 0xFFFF - e (larger logit first, then lower expert id,
+// as route_token_by orders), so each of the k rounds is one 32-bit wave maximum.
+__device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, uint32_t k,
+                                            int lane, int32_t &my_id, float &my_w) {
+    uint32_t key[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t e = lane + 64 * q;
+        if (e < E) {
+            const uint32_t u = logits[e] == 0x8000u ? 0u : logits[e]; // -0 ties +0
+            const uint32_t ord = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
+            key[q] = (ord << 16) | (0xFFFFu - e);
+        } else {
+            key[q] = 0; // below every expert's key (their low halves are >= 0xFF00)
+        }
+    }
+    my_id = 0;
+    float my_v = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) {
+        uint32_t best = key[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q)
+            if (64 * q < E)
+                best = max(best, key[q]);
+        best = wave_max_u32(best);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (key[q] == best)
+                key[q] = 0;
+        if ((uint32_t)lane == j) {
+            my_id = (int32_t)(0xFFFFu - (best & 0xFFFFu));
+            const uint32_t ord = best >> 16;
+            my_v = __uint_as_float(((ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu)) << 16);
+        }
+    }
+    // slot 0 holds the largest logit
+    const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
+    const float p = (uint32_t)lane < k ? expf(my_v - vmax) : 0.0f;
+    my_w = p / group_sum<64>(p);
+}
+
 // Top-k of one token's E logits (E <= 256; logit(e) returns expert e's as fp32) by wave
 // lanes 0..63, then softmax over the k; lane j < k returns slot j's expert id and
 // weight.  Keys order by logit, then by lower expert id (the reference tie-break), and
@@ -131,7 +184,8 @@ __device__ __forceinline__ void route_token_by(Logit logit, uint32_t E, uint32_t
     for (int q = 0; q < 4; ++q) {
         const uint32_t e = lane + 64 * q;
         if (e < E) {
-            const uint32_t u = __float_as_uint(logit(e));
+            const uint32_t f = __float_as_uint(logit(e));
+            const uint32_t u = f == 0x80000000u ? 0u : f; // -0 ties +0
             const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
             key[q] = ((uint64_t)ord << 32) | (0xFFFFFFFFu - e);
         } else {
@@ -160,13 +214,6 @@ __device__ __forceinline__ void route_token_by(Logit logit, uint32_t E, uint32_t
     const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
     const float p = (uint32_t)lane < k ? expf(my_v - vmax) : 0.0f;
     my_w = p / group_sum<64>(p);
-}
-
-// route_token_by over one token's bf16 logits.
-__device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, uint32_t k,
-                                            int lane, int32_t &my_id, float &my_w) {
-    route_token_by([&](uint32_t e) { return __uint_as_float((uint32_t)logits[e] << 16); }, E, k,
-                   lane, my_id, my_w);
 }
 
 // Token t of the FFN's logits (fp32 when given, else bf16); lane j < k's weight times
@@ -597,17 +644,20 @@ __global__ __launch_bounds__(256) void moe_plan_scatter_kernel(MoeArgs a) {
     v.pair_of_pos[pos] = (int32_t)p;
 }
 
-// Exclusive prefix sum over the 64 lanes of a wave (Kogge-Stone); `total` receives
-// the sum of all lanes.
+// Exclusive prefix sum over the 64 lanes of a wave; `total` receives the sum of all
+// lanes.  Inclusive scans within rows of 16 by DPP row shifts (lanes shifted in from
+// outside the row read 0), then each row adds the totals of the rows below it.
 __device__ __forceinline__ int wave_excl_scan(int x, int lane, int &total) {
     int incl = x;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(incl, d, 64);
-        if (lane >= d)
-            incl += o;
-    }
-    total = __builtin_amdgcn_readlane(incl, 63);
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true); // row_shr:1
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true); // row_shr:2
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true); // row_shr:4
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true); // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(incl, 15), r1 = __builtin_amdgcn_readlane(incl, 31),
+              r2 = __builtin_amdgcn_readlane(incl, 47), r3 = __builtin_amdgcn_readlane(incl, 63);
+    const int row = lane >> 4;
+    incl += (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+    total = r0 + r1 + r2 + r3;
     return incl - x;
 }
 

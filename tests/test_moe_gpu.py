@@ -51,6 +51,8 @@ def test_route_ties_and_odd_sizes():
     lg[0, :] = synth.bf16_from_f32(np.float32(0.25))      # all tied: ids 0..k-1
     lg[1, [3, 50, 99]] = synth.bf16_from_f32(np.float32(9.0))  # tie at the top
     lg[2, :] = synth.bf16_from_f32(-np.arange(100, dtype=np.float32))
+    lg[3, :] = synth.bf16_from_f32(np.float32(-1.0))      # -0 and +0 tie: lower id first
+    lg[3, 7], lg[3, 2] = 0x0000, 0x8000
     check_route(lg, 8)
     check_route(lg, 1)
     check_route(synth.normal_bf16(rng, (5, 256)), 16)

@@ -66,6 +66,13 @@ def test_route_f32_with_per_expert_scale():
     hip.moe_route_f32(dev(lg), None, ids, w, T, E, k)
     hip.synchronize()
     np.testing.assert_allclose(w.numpy().sum(axis=1), 1.0, rtol=1e-5)
+    # -0 and +0 tie (lower id first), as equal values do
+    z = np.full((1, E), -1.0, np.float32)
+    z[0, 9], z[0, 4] = 0.0, -0.0
+    ids1, w1 = hip.DeviceArray((1, 2), np.int32), hip.DeviceArray((1, 2), np.float32)
+    hip.moe_route_f32(dev(z), None, ids1, w1, 1, E, 2)
+    hip.synchronize()
+    assert ids1.numpy().tolist() == [[4, 9]]
 
 
 @pytest.mark.parametrize("T,path", [(16, 0), (16, 2), (300, 0)])
