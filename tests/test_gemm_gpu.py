@@ -74,6 +74,29 @@ def test_gemm_prefill_full_size_sampled():
     assert rel_l2(lhs, rhs) < TOL_BF16
 
 
+def test_gemm_many_tiles_exact():
+    """416 tiles of 256 x 256 (more than one round of the 256 CUs, the second partial),
+    K of 7 stages.  One-hot rows make every output a single weight, so a tile computed
+    twice, skipped or written to the wrong place shows up exactly.  Random rows then
+    check against the oracle on sampled columns, and a repeat launch must be
+    bit-identical."""
+    rng = np.random.default_rng(12)
+    M, N, K = 256, 416 * 256, 448
+    w = synth.nvfp4_weights(rng, N, K)
+    perm = rng.integers(0, K, size=M)
+    A = np.zeros((M, K), np.float32)
+    A[np.arange(M), perm] = 1.0
+    got = bf16(gemm(synth.bf16_from_f32(A), w))
+    want = oracle.decode(w.codes, w.scales)[:, perm].T + np.float32(0.0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    A = synth.normal_bf16(rng, (M, K))
+    C = gemm(A, w)
+    assert np.array_equal(gemm(A, w), C)
+    ni = np.sort(rng.choice(N, 2048, replace=False))
+    want = oracle.matvec_rows(w.codes, w.scales, bf16(A), ni)
+    assert rel_l2(bf16(C)[:, ni], want) < TOL_BF16
+
+
 def test_gemm_tensor_scale_and_matmul_dispatch():
     """apex_nvfp4_matmul_bf16 switches to the GEMM from 64 tokens; results agree with
     the GEMM entry point, and a power-of-two tensor scale scales the output exactly."""
