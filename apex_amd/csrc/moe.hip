@@ -408,6 +408,84 @@ __global__ __launch_bounds__(64 * WAVES) void moe_router_kernel(MoeRouterArgs a)
     }
 }
 
+// Router logits for few tokens (decode): one workgroup per (token, 16 experts), so the
+// weight stream (E x H bytes) spreads over T * E / 16 workgroups instead of T.  Wave w
+// owns experts e0 + 4w .. e0 + 4w + 3, 16 lanes each; lane j of an expert owns the
+// 64-element groups j, j + 16, ... (K <= 4096: at most 4), whose codes it loads at
+// entry, before the token's row is normalised into LDS (the rmsNormCpu order, as the
+// tiled kernel); per group `scale * sum_k xn q + bias * sum_k xn`, then the 16 lanes'
+// partial logits are summed by DPP.
+constexpr uint32_t kRouterSmallExperts = 16;
+constexpr uint32_t kRouterSmallTokens = 64; // the (token, expert block) form up to this
+constexpr int kRouterSmallSlots = (int)(kRouterMaxHidden / kQGroup / 16);
+
+__global__ __launch_bounds__(256) void moe_router_small_kernel(MoeRouterArgs a) {
+    __shared__ __attribute__((aligned(16))) float xn[kRouterMaxHidden];
+    __shared__ float gsum[kRouterMaxHidden / kQGroup];
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.x, H = a.H, E = a.E, NG = H / kQGroup;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane % 16;
+    const uint32_t e = blockIdx.y * kRouterSmallExperts + 4 * wave + lane / 16;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
+    u32x4_t q4[kRouterSmallSlots][4];
+    uint32_t sb[kRouterSmallSlots];
+#pragma unroll
+    for (int s = 0; s < kRouterSmallSlots; ++s) {
+        const uint32_t g = j + 16 * s;
+        const bool ok = e < E && g < NG;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            q4[s][i] = load_b128(rq, ok ? e * H + g * kQGroup + 16 * i : kOutOfRange);
+        sb[s] = ok ? (uint32_t)a.qs[(size_t)e * NG + g] | ((uint32_t)a.qb[(size_t)e * NG + g] << 16) : 0u;
+    }
+    // the token's row -> LDS, its sum of squares
+    const __amdgpu_buffer_rsrc_t rh = make_rsrc(a.h + (size_t)t * H, H * 4);
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < H / 4; i += blockDim.x) {
+        const u32x4_t v = load_b128(rh, i * 16);
+        *reinterpret_cast<u32x4_t *>(xn + 4 * i) = v;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            ss += __uint_as_float(v[c]) * __uint_as_float(v[c]);
+    }
+    ss = group_sum<64>(ss);
+    if (lane == 0)
+        red[wave] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + a.eps);
+    for (uint32_t i = threadIdx.x; i < H; i += blockDim.x)
+        xn[i] = xn[i] * inv * bf16_bits_to_f32(a.norm_w[i]);
+    __syncthreads();
+    for (uint32_t g = wave; g < NG; g += 4) { // a group of 64 per wave, summed by DPP
+        const float sum = group_sum<64>(xn[g * kQGroup + lane]);
+        if (lane == 0)
+            gsum[g] = sum;
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kRouterSmallSlots; ++s) {
+        const uint32_t g = j + 16 * s;
+        if (g >= NG)
+            break;
+        float aq = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            const uint32_t wv = q4[s][w / 4][w % 4];
+            const float4 xv = *reinterpret_cast<const float4 *>(xn + g * kQGroup + 4 * w);
+            aq = __builtin_fmaf(xv.x, (float)(wv & 0xFFu), aq);
+            aq = __builtin_fmaf(xv.y, (float)((wv >> 8) & 0xFFu), aq);
+            aq = __builtin_fmaf(xv.z, (float)((wv >> 16) & 0xFFu), aq);
+            aq = __builtin_fmaf(xv.w, (float)(wv >> 24), aq);
+        }
+        acc += __uint_as_float(sb[s] << 16) * aq + __uint_as_float(sb[s] & 0xFFFF0000u) * gsum[g];
+    }
+    acc = group_sum<16>(acc);
+    if (j == 0 && e < E)
+        a.logits[(size_t)t * E + e] = acc;
+}
+
 template <int TT, int WAVES> size_t router_lds(const MoeRouterArgs &a) {
     const uint32_t NG = a.H / kQGroup;
     return 4 * ((size_t)TT * a.H + (size_t)TT * NG + (size_t)WAVES * TT * a.E);
@@ -1431,8 +1509,15 @@ hipError_t router_launch_epl(const MoeRouterArgs &a, hipStream_t stream) {
 hipError_t moe_router_logits_launch(const MoeRouterArgs &a, hipStream_t stream) {
     if (a.T == 0)
         return hipSuccess;
-    // few tokens: one token per workgroup of 16 waves (parallelism over tokens and K);
-    // many: tiles of 8 (or, for the widest shapes, 4) tokens share the weight reads
+    // decode sizes: a workgroup per (token, 16 experts); up to 256 tokens one token per
+    // workgroup of 16 waves (parallelism over tokens and K); more: tiles of 8 (or, for
+    // the widest shapes, 4) tokens share the weight reads
+    if (a.T <= kRouterSmallTokens) {
+        hipLaunchKernelGGL(moe_router_small_kernel,
+                           dim3(a.T, (a.E + kRouterSmallExperts - 1) / kRouterSmallExperts),
+                           dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
     if (a.T <= 256)
         return router_launch_epl<1, 16>(a, stream);
     if (router_lds<8, 8>(a) <= kMaxDynLds)
