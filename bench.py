@@ -370,7 +370,7 @@ def time_slot_streaming(repeats=3):
     sec = float(np.median(times))
     return {"value": round(size / sec / 1e9, 2), "unit": "GB/s", "ms_per_step": round(sec * 1e3, 3),
             "bytes": size, "workload": "expert layer file (128 slots x 3,358,720 B) -> HBM, "
-                                       "page-cache source, 16 MiB x 4 pinned staging"}
+                                       "page-cache source, 8 MiB x 8 pinned staging, 4 reader threads"}
 
 
 def vendor_bf16_gemm(M, N, K, steps, warmup):

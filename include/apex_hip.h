@@ -313,9 +313,11 @@ int apex_moe_route_f32(const float *logits, const uint16_t *per_expert_scale, ui
  * slots at a fixed stride) into device memory.  apex_file_to_device copies bytes
  * [file_offset, file_offset + bytes) to dst; apex_experts_to_device copies slot
  * experts[i] (file bytes [experts[i] * stride, + slot_bytes)) to dst + i * dst_stride
- * for i < n_experts (experts is a host array).  Both read chunk_bytes at a time into a
- * ring of n_buffers pinned host buffers while earlier chunks' host-to-device copies
- * run on `stream` (0: 16 MiB, 4 buffers), and return once every copy has completed. */
+ * for i < n_experts (experts is a host array).  Both read chunk_bytes at a time into
+ * n_buffers pinned host buffers (n_buffers / 2 reader threads, two buffers each) while
+ * earlier chunks' host-to-device copies run on `stream` (0: 8 MiB, 8 buffers), and
+ * return once every copy has completed.  The pinned buffers are kept for the process
+ * and reused by later calls of the same shape; calls are serialised. */
 int apex_file_to_device(const char *path, uint64_t file_offset, uint64_t bytes, void *dst,
                         uint64_t chunk_bytes, uint32_t n_buffers, void *stream);
 int apex_experts_to_device(const char *path, uint64_t stride, uint64_t slot_bytes,
