@@ -23,6 +23,7 @@
 //    scale, as the reference kernel does (shaders/matmul.metal:38-46); group sums use
 //    DPP; the per-tensor fp32 scale is applied in the epilogue.
 #pragma once
+#include <algorithm>
 #include "gemv.h"
 #include "nvfp4_device.h"
 
@@ -32,6 +33,9 @@ namespace gemv_detail {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+// Tokens per block with the fused RMSNorm: the per-token sums stay in registers, and the
+// wider blocks of the fp32 kernel are already at the register limit.
+constexpr int kMaxNormTokens = 2;
 
 
 template <typename XT> struct XTraits;
@@ -301,6 +305,62 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < DEPTH - 1; ++i)
             issue(buf[i][0], i);
+        // 3'. fp32 x with norm_w: RMSNorm of each token row on the staged pieces (piece p
+        //     of chunk c holds elements 32c + 4p .. +3), x * inv * w -- the rmsNormCpu order
+        if constexpr (sizeof(XT) == 4 && TT <= kMaxNormTokens) {
+            if (a.norm_w) {
+                __shared__ float red[kMaxNormTokens][kWaves];
+                float ss[TT] = {};
+#pragma unroll
+                for (int i = 0; i < NX; ++i) {
+                    const int q = threadIdx.x + i * kThreads;
+                    const int tt = q / plane, c = (q - tt * plane) / PIECES;
+                    if (q < TT * plane && c < nchunks)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float v = __uint_as_float(xv[i][e]);
+#pragma unroll
+                            for (int u = 0; u < TT; ++u)
+                                if (u == tt)
+                                    ss[u] += v * v;
+                        }
+                }
+#pragma unroll
+                for (int u = 0; u < TT; ++u) {
+                    const float w = group_sum<64>(ss[u]);
+                    if (lane == 0)
+                        red[u][wave] = w;
+                }
+                __syncthreads();
+                float inv[TT];
+#pragma unroll
+                for (int u = 0; u < TT; ++u) {
+                    float tot = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < kWaves; ++w)
+                        tot += red[u][w];
+                    inv[u] = 1.0f / sqrtf(tot / (float)a.K + a.norm_eps);
+                }
+#pragma unroll
+                for (int i = 0; i < NX; ++i) {
+                    const int q = threadIdx.x + i * kThreads;
+                    const int tt = q / plane, rem = q - tt * plane;
+                    const int c = rem / PIECES, p = rem - c * PIECES;
+                    if (q < TT * plane && c < nchunks) {
+                        float s = 0.0f;
+#pragma unroll
+                        for (int u = 0; u < TT; ++u)
+                            if (u == tt)
+                                s = inv[u];
+                        const uint16_t *w = a.norm_w + 32 * c + 4 * p;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            xv[i][e] = __float_as_uint(__uint_as_float(xv[i][e]) * s *
+                                                       bf16_bits_to_f32(w[e]));
+                    }
+                }
+            }
+        }
         // 3. x into LDS, piece-major: entry tt*plane + p*stride_c + c
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
@@ -510,6 +570,8 @@ hipError_t gemv_dispatch(const GemvArgs &a, hipStream_t stream) {
     for (int m = 0; m < ((MODE >= 2) ? 2 : 1); ++m)
         fast = fast && ((uintptr_t)a.codes[m] % 16 == 0) && ((uintptr_t)a.scales[m] % 2 == 0);
     fast = fast && ((uintptr_t)a.x % 16 == 0);
+    if (!fast && a.norm_w)
+        return hipErrorInvalidValue; // the fused RMSNorm lives in the staged-x kernel only
     if (!fast) {
         dim3 grid((a.rows + kWaves - 1) / kWaves, a.tokens);
         hipLaunchKernelGGL((nvfp4_gemv_generic_kernel<XT, MODE>), grid, dim3(kThreads), 0, stream,
@@ -524,6 +586,8 @@ hipError_t gemv_dispatch(const GemvArgs &a, hipStream_t stream) {
         tt *= 2;
     while (tt > 1 && tt * per_token > 32768)
         tt /= 2;
+    if (a.norm_w)
+        tt = std::min(tt, (uint32_t)kMaxNormTokens);
     switch (tt) {
     case 1: return dispatch_shape<XT, MODE, 1>(a, nchunks, stream);
     case 2: return dispatch_shape<XT, MODE, 2>(a, nchunks, stream);

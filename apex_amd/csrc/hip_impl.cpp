@@ -127,15 +127,25 @@ void matmul_impl(const void *x, bool bf16, const uint32_t *codes, const uint8_t 
               "matmul_nvfp4 launch");
 }
 
+// norm_w (fp32 x only): RMS-normalise each x row first (x * inv * norm_w, eps norm_eps).
 void geglu_impl(const void *x, bool bf16, const uint32_t *gc, const uint8_t *gs, float gts,
                 const uint32_t *uc, const uint8_t *us, float uts, void *out, uint32_t tokens,
-                uint32_t rows, uint32_t K, hipStream_t stream) {
+                uint32_t rows, uint32_t K, hipStream_t stream, const uint16_t *norm_w = nullptr,
+                float norm_eps = 0.0f) {
     check_nvfp4_shape(rows, K);
     if (tokens == 0 || rows == 0)
         return;
     require(x && gc && gs && uc && us && out, "null pointer");
+    if (norm_w)
+        require(!bf16 && K % 32 == 0 && K <= 8192 && (uintptr_t)x % 16 == 0 &&
+                    (uintptr_t)gc % 16 == 0 && (uintptr_t)uc % 16 == 0 &&
+                    (uintptr_t)gs % 2 == 0 && (uintptr_t)us % 2 == 0,
+                "geglu with RMSNorm: fp32 x, K a multiple of 32 up to 8192, x and codes "
+                "16-byte aligned, scales 2-byte aligned");
     init_device_tuning();
     apex_hip::GemvArgs a{};
+    a.norm_w = norm_w;
+    a.norm_eps = norm_eps;
     a.x = x;
     a.codes[0] = gc;
     a.codes[1] = uc;
@@ -427,6 +437,23 @@ template <bool BF16> void launch_geglu_nvfp4(const LaunchCtx &c) {
                rows, K, c.stream);
 }
 
+// geglu_nvfp4_rms_norm_f32: x, norm_w, gate codes / scales, up codes / scales, out, K,
+// rows, tokens, gate / up tensor scales, eps.
+void launch_geglu_nvfp4_rms_norm(const LaunchCtx &c) {
+    const uint32_t K = c.u[7], rows = c.u[8], tokens = c.u[9];
+    check_nvfp4_shape(rows, K);
+    need(c, 0, (uint64_t)tokens * K * 4, "geglu_nvfp4_rms_norm input");
+    need(c, 1, (uint64_t)K * 2, "geglu_nvfp4_rms_norm norm weights");
+    need(c, 2, (uint64_t)rows * K / 2, "geglu_nvfp4_rms_norm gate weights");
+    need(c, 3, (uint64_t)rows * K / 16, "geglu_nvfp4_rms_norm gate scales");
+    need(c, 4, (uint64_t)rows * K / 2, "geglu_nvfp4_rms_norm up weights");
+    need(c, 5, (uint64_t)rows * K / 16, "geglu_nvfp4_rms_norm up scales");
+    need(c, 6, (uint64_t)tokens * rows * 4, "geglu_nvfp4_rms_norm output");
+    geglu_impl(c.ptr[0], false, (const uint32_t *)c.ptr[2], (const uint8_t *)c.ptr[3], c.f[10],
+               (const uint32_t *)c.ptr[4], (const uint8_t *)c.ptr[5], c.f[11], c.ptr[6], tokens,
+               rows, K, c.stream, (const uint16_t *)c.ptr[1], c.f[12]);
+}
+
 void launch_gemm_nvfp4_bf16(const LaunchCtx &c) {
     const uint32_t M = c.u[4], N = c.u[5], K = c.u[6];
     check_nvfp4_shape(N, K);
@@ -523,6 +550,7 @@ const KernelSpec kKernels[] = {
     {"matmul_nvfp4_bf16", "BBBBUUUF", 1u << 3, launch_matmul_nvfp4_bf16},
     {"geglu_nvfp4_f32", "BBBBBBUUUFF", 1u << 5, launch_geglu_nvfp4<false>},
     {"geglu_nvfp4_bf16", "BBBBBBUUUFF", 1u << 5, launch_geglu_nvfp4<true>},
+    {"geglu_nvfp4_rms_norm_f32", "BBBBBBBUUUFFF", 1u << 6, launch_geglu_nvfp4_rms_norm},
     {"gemm_nvfp4_bf16", "BBBBUUUF", 1u << 3, launch_gemm_nvfp4_bf16},
     {"dequant_nvfp4_f32", "BBBUUF", 1u << 2, launch_dequant<false>},
     {"dequant_nvfp4_bf16", "BBBUUF", 1u << 2, launch_dequant<true>},
@@ -822,6 +850,18 @@ int apex_nvfp4_geglu_f32(const float *x, const uint32_t *gate_codes, const uint8
     return guard([&] {
         geglu_impl(x, false, gate_codes, gate_scales, gate_tensor_scale, up_codes, up_scales,
                    up_tensor_scale, out, tokens, rows, K, as_stream(stream));
+    });
+}
+
+int apex_nvfp4_geglu_rms_norm_f32(const float *x, const uint16_t *norm_w, float eps,
+                                  const uint32_t *gate_codes, const uint8_t *gate_scales,
+                                  float gate_tensor_scale, const uint32_t *up_codes,
+                                  const uint8_t *up_scales, float up_tensor_scale, float *out,
+                                  uint32_t tokens, uint32_t rows, uint32_t K, void *stream) {
+    return guard([&] {
+        require(norm_w != nullptr, "geglu_rms_norm: norm_w is null");
+        geglu_impl(x, false, gate_codes, gate_scales, gate_tensor_scale, up_codes, up_scales,
+                   up_tensor_scale, out, tokens, rows, K, as_stream(stream), norm_w, eps);
     });
 }
 

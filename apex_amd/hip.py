@@ -73,6 +73,8 @@ _PROTOS = {
     "apex_nvfp4_gemm_bf16": (_I, [_P, _P, _P, _F, _P, _U32, _U32, _U32, _P]),
     "apex_nvfp4_geglu_f32": (_I, [_P, _P, _P, _F, _P, _P, _F, _P, _U32, _U32, _U32, _P]),
     "apex_nvfp4_geglu_bf16": (_I, [_P, _P, _P, _F, _P, _P, _F, _P, _U32, _U32, _U32, _P]),
+    "apex_nvfp4_geglu_rms_norm_f32": (_I, [_P, _P, _F, _P, _P, _F, _P, _P, _F, _P, _U32, _U32,
+                                           _U32, _P]),
     "apex_geglu_f32": (_I, [_P, _P, _P, _U32, _P]),
     "apex_nvfp4_dequant_f32": (_I, [_P, _P, _F, _P, _U32, _U32, _P]),
     "apex_nvfp4_dequant_bf16": (_I, [_P, _P, _F, _P, _U32, _U32, _P]),
@@ -264,6 +266,14 @@ def nvfp4_geglu_f32(x, gc, gs, uc, us, out, tokens, rows, K, gate_scale=1.0, up_
                     stream=None):
     check(lib().apex_nvfp4_geglu_f32(x.ptr, gc.ptr, gs.ptr, gate_scale, uc.ptr, us.ptr, up_scale,
                                      out.ptr, tokens, rows, K, _s(stream)))
+
+
+def nvfp4_geglu_rms_norm_f32(x, norm_w, eps, gc, gs, uc, us, out, tokens, rows, K,
+                             gate_scale=1.0, up_scale=1.0, stream=None):
+    """rms_norm_f32 of each x row (bf16 weights norm_w [K]) fused into the fp32 GeGLU GEMV."""
+    check(lib().apex_nvfp4_geglu_rms_norm_f32(x.ptr, norm_w.ptr, eps, gc.ptr, gs.ptr, gate_scale,
+                                              uc.ptr, us.ptr, up_scale, out.ptr, tokens, rows, K,
+                                              _s(stream)))
 
 
 def nvfp4_geglu_bf16(x, gc, gs, uc, us, out, tokens, rows, K, gate_scale=1.0, up_scale=1.0,

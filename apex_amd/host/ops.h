@@ -110,6 +110,23 @@ inline void gegluNvfp4(Backend &backend, Buffer *input, const Nvfp4Matrix &gate,
                 Dim3{1}, Dim3{256});
 }
 
+// rmsNorm of each fp32 input row (bf16 weights at norm_weights + norm_offset) fused into
+// the fp32 gate/up GeGLU GEMV: one launch in place of rmsNorm + gegluNvfp4.  Needs
+// hidden_dim % 32 == 0 and a 16-byte aligned input.
+inline void gegluNvfp4RmsNorm(Backend &backend, Buffer *input, Buffer *norm_weights,
+                              size_t norm_offset, float eps, const Nvfp4Matrix &gate,
+                              const Nvfp4Matrix &up, Buffer *output, uint32_t tokens,
+                              float gate_scale = 1.0f, float up_scale = 1.0f) {
+    backend.run("geglu_nvfp4_rms_norm_f32",
+                {Arg::buf(input), Arg::buf(norm_weights, norm_offset),
+                 Arg::buf(gate.weights, gate.weights_offset),
+                 Arg::buf(gate.scales, gate.scales_offset), Arg::buf(up.weights, up.weights_offset),
+                 Arg::buf(up.scales, up.scales_offset), Arg::buf(output), Arg::val(gate.hidden_dim),
+                 Arg::val(gate.w_rows), Arg::val(tokens), Arg::val(gate_scale),
+                 Arg::val(up_scale), Arg::val(eps)},
+                Dim3{1}, Dim3{256});
+}
+
 // Prefill GEMM: bf16 A [M, K] x NVFP4 W [N, K]^T -> bf16 C [M, N] on bf16 MFMA.
 inline void gemmNvfp4Bf16(Backend &backend, Buffer *A, const Nvfp4Matrix &W, Buffer *C, uint32_t M,
                           float tensor_scale = 1.0f) {

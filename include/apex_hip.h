@@ -117,6 +117,11 @@ int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
  *   geglu_nvfp4_bf16  B up scales, B output [T,rows], U hidden_dim, U w_rows,
  *                     U tokens, F gate tensor_scale, F up tensor_scale:
  *                     gelu_tanh(gate.x) * (up.x) in one pass (src/ops.h:65-67 fused).
+ *   geglu_nvfp4_rms_norm_f32 B input f32 [T,K], B norm weights bf16 [K], B gate
+ *                     weights, B gate scales, B up weights, B up scales, B output f32
+ *                     [T,rows], U hidden_dim, U w_rows, U tokens, F gate tensor_scale,
+ *                     F up tensor_scale, F eps: rms_norm_f32 of x, then geglu_nvfp4_f32
+ *                     (apex_nvfp4_geglu_rms_norm_f32).
  *   gemm_nvfp4_bf16   B A bf16 [M,K], B weights [N,K/8], B scales [N,K/16], B C bf16
  *                     [M,N], U M, U N, U K, F tensor_scale (apex_nvfp4_gemm_bf16).
  *   dequant_nvfp4_f32 B weights, B scales, B output [rows,K], U hidden_dim,
@@ -209,6 +214,15 @@ int apex_nvfp4_geglu_f32(const float *x, const uint32_t *gate_codes, const uint8
                          float gate_tensor_scale, const uint32_t *up_codes,
                          const uint8_t *up_scales, float up_tensor_scale, float *out,
                          uint32_t tokens, uint32_t rows, uint32_t K, void *stream);
+/* The same after an RMSNorm of each x row (the step before the MLP in the reference's
+ * model, src/ops.h:18-26 rmsNorm then 65-67): x_t * (1 / sqrt(mean(x_t^2) + eps)) * w,
+ * computed inside the GEMV's x staging instead of a separate launch and buffer.
+ * norm_w is bf16 [K]; needs K % 32 == 0, K <= 8192, x and codes 16-byte aligned. */
+int apex_nvfp4_geglu_rms_norm_f32(const float *x, const uint16_t *norm_w, float eps,
+                                  const uint32_t *gate_codes, const uint8_t *gate_scales,
+                                  float gate_tensor_scale, const uint32_t *up_codes,
+                                  const uint8_t *up_scales, float up_tensor_scale, float *out,
+                                  uint32_t tokens, uint32_t rows, uint32_t K, void *stream);
 int apex_nvfp4_geglu_bf16(const uint16_t *x, const uint32_t *gate_codes,
                           const uint8_t *gate_scales, float gate_tensor_scale,
                           const uint32_t *up_codes, const uint8_t *up_scales,

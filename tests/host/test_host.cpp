@@ -142,7 +142,28 @@ void test_dense_mlp(HipBackend &be) {
     const double r3 = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
     report("contents() write before run is uploaded", r3 < 1e-5, "rel_l2 " + std::to_string(r3));
 
-    for (Buffer *b : {dg.buf, du.buf, dd.buf, in, gate_tmp, up_tmp, out, h_tmp, out2})
+    // rmsNorm fused into the gate/up GEMV (norm weights at an offset in a core buffer)
+    const size_t woff = 512;
+    std::vector<uint8_t> core(woff + H * 2);
+    for (uint32_t i = 0; i < H; ++i) {
+        const uint16_t w = to_bf16(1.0f + 0.1f * rng.normal());
+        std::memcpy(core.data() + woff + 2 * i, &w, 2);
+    }
+    Buffer *cb = upload(be, core.data(), core.size(), "core_weights");
+    const float eps = 1e-6f;
+    gegluNvfp4RmsNorm(be, in, cb, woff, eps, dg.m, du.m, h_tmp, T);
+    matmulNvfp4(be, h_tmp, dd.m, out2, T);
+    be.sync();
+    std::vector<float> xn(x.size());
+    orc_rms_norm(x.data(), reinterpret_cast<const uint16_t *>(core.data() + woff), xn.data(), T, H,
+                 eps);
+    orc_dense_mlp(g.codes.data(), g.scales.data(), u.codes.data(), u.scales.data(), d.codes.data(),
+                  d.scales.data(), xn.data(), want.data(), T, H, I);
+    const double r4 = rel_l2(static_cast<float *>(be.contents(out2)), want.data(), want.size());
+    report("gegluNvfp4RmsNorm + matmulNvfp4 vs rmsNorm + denseMlp oracle", r4 < 1e-5,
+           "rel_l2 " + std::to_string(r4));
+
+    for (Buffer *b : {dg.buf, du.buf, dd.buf, in, gate_tmp, up_tmp, out, h_tmp, out2, cb})
         be.release(b);
 }
 

@@ -55,6 +55,7 @@ EXPECTED = {
     "matmul_nvfp4_bf16": "BBBBUUUF",
     "geglu_nvfp4_f32": "BBBBBBUUUFF",
     "geglu_nvfp4_bf16": "BBBBBBUUUFF",
+    "geglu_nvfp4_rms_norm_f32": "BBBBBBBUUUFFF",
     "gemm_nvfp4_bf16": "BBBBUUUF",
     "dequant_nvfp4_f32": "BBBUUF",
     "dequant_nvfp4_bf16": "BBBUUF",

@@ -58,6 +58,47 @@ def test_dense_mlp_fp32_fused(T):
     assert rel_l2(y.numpy(), want(case)) < TOL_REF_GATE
 
 
+@pytest.mark.parametrize("T", [1, 5])
+def test_dense_mlp_fp32_norm_fused(T):
+    """RMSNorm fused into the gate/up GeGLU GEMV, down GEMV (2 launches): the same
+    reference gate; 5 tokens run as blocks of 2, 2 and 1."""
+    case = synth.dense_mlp_case(seed=300 + T, tokens=T)
+    h, nw, g, u, d = case
+    hh, y = hip.DeviceArray((T, I), np.float32), hip.DeviceArray((T, H), np.float32)
+    hip.nvfp4_geglu_rms_norm_f32(dev(h), dev(nw), EPS, dev(g.codes), dev(g.scales), dev(u.codes),
+                                 dev(u.scales), hh, T, I, H)
+    hip.nvfp4_matmul_f32(hh, dev(d.codes), dev(d.scales), y, T, H, I)
+    hip.synchronize()
+    assert rel_l2(y.numpy(), want(case)) < TOL_REF_GATE
+
+
+def test_geglu_norm_fused_matches_separate_norm_and_rejects_bad_layouts():
+    """Odd sizes (K = 320: the last chunk plane of x partly padding, 37 rows) against
+    the separate rms_norm_f32 + geglu_nvfp4_f32 launches, and the fused form's layout
+    requirements (fp32 x, K % 32 == 0) turned into errors, not a wrong result."""
+    rng = np.random.default_rng(7)
+    T, rows, K = 3, 37, 320
+    h = rng.standard_normal((T, K)).astype(np.float32) * 3
+    nw = synth.bf16_from_f32(rng.standard_normal(K).astype(np.float32))
+    g, u = synth.nvfp4_weights(rng, rows, K), synth.nvfp4_weights(rng, rows, K)
+    xn, sep, fused = (hip.DeviceArray((T, K), np.float32), hip.DeviceArray((T, rows), np.float32),
+                      hip.DeviceArray((T, rows), np.float32))
+    hip.rms_norm_f32(dev(h), dev(nw), xn, T, K, EPS)
+    hip.nvfp4_geglu_f32(xn, dev(g.codes), dev(g.scales), dev(u.codes), dev(u.scales), sep, T, rows, K)
+    hip.nvfp4_geglu_rms_norm_f32(dev(h), dev(nw), EPS, dev(g.codes), dev(g.scales), dev(u.codes),
+                                 dev(u.scales), fused, T, rows, K)
+    hip.synchronize()
+    assert rel_l2(fused.numpy(), sep.numpy()) < 1e-6
+    xg = oracle.rms_norm(h, nw, EPS)
+    ref = oracle.geglu(oracle.matvec(g.codes, g.scales, xg), oracle.matvec(u.codes, u.scales, xg))
+    assert rel_l2(fused.numpy(), ref) < TOL_REF_GATE
+    g16 = synth.nvfp4_weights(rng, rows, 16 * 3)   # K = 48: not a multiple of 32
+    with pytest.raises(hip.ApexHipError):
+        hip.nvfp4_geglu_rms_norm_f32(dev(h[:, :48]), dev(nw[:48]), EPS, dev(g16.codes),
+                                     dev(g16.scales), dev(g16.codes), dev(g16.scales), fused,
+                                     T, rows, 48)
+
+
 @pytest.mark.parametrize("T", [1, 96])
 def test_dense_mlp_bf16(T):
     """bf16 activations after the norm: fused GeGLU (GEMV, or MFMA GEMM from 64 tokens)
