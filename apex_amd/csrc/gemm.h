@@ -1,23 +1,39 @@
-// Host-side interface of the NVFP4 prefill GEMM (MFMA regime).
+// Host-side interface of the NVFP4 prefill GEMMs (MFMA regime).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace apex_hip {
 
-// C[M, N] (row stride ldc) = tensor_scale * A[M, K] . W[N, K]^T; A, C bf16 bits.
+// Plain:  C[M, N] = tensor_scale[0] * A . W^T                     (W = codes/scales[0])
+// GeGLU:  C[M, N] = gelu(tensor_scale[0] * A . G^T) * (tensor_scale[1] * A . U^T)
+//         (G = codes/scales[0], U = [1], both [N, K]; shaders/geglu.metal:15-23)
+// A is bf16 [M, a_k] (row stride a_k): a_k = K for bf16 activations, a_k = 2K for the
+// [hi | lo] split of fp32 activations (gemm_split_launch), whose halves both meet W.
+// C is bf16 bits or fp32 (out_f32), row stride ldc.  W: codes uint32 [N, K/8], E4M3
+// scales [N, K/16].
 struct GemmArgs {
     const uint16_t *A;
-    const uint32_t *codes;  // [N, K/8]
-    const uint8_t *scales;  // [N, K/16]
-    uint16_t *C;
-    uint32_t M, N, K, ldc;
-    float tensor_scale;
+    const uint32_t *codes[2];
+    const uint8_t *scales[2];
+    float tensor_scale[2];
+    void *C;
+    uint32_t M, N, K, ldc, a_k;
+    bool geglu, out_f32;
 };
 
-// K % 64 == 0 and operands within the 2 GiB buffer-descriptor range.
-bool gemm_supported(uint32_t M, uint32_t N, uint32_t K);
+// K % 64 == 0 and operands within the 2 GiB buffer-descriptor range (A of a_k columns).
+bool gemm_supported(uint32_t M, uint32_t N, uint32_t K, uint32_t a_k, bool out_f32);
 
 hipError_t gemm_launch(const GemmArgs &a, hipStream_t stream);
+
+// fp32 activations X [M, K] (row stride K) -> split [M, 2K] bf16: hi = bf16(x) and
+// lo = bf16(x - hi), both rounded to nearest even (lo = 0 where hi is not finite), so
+// x = hi + lo + r with |r| <= 2^-17 |x|.  With norm_w (bf16 [K]), x is first
+// RMS-normalised over its row: x * (1 / sqrt(mean(x^2) + eps)) * norm_w[k].
+size_t gemm_split_bytes(uint32_t M, uint32_t K);
+hipError_t gemm_split_launch(const float *X, const uint16_t *norm_w, float eps, uint16_t *split,
+                             uint32_t M, uint32_t K, hipStream_t stream);
 
 } // namespace apex_hip

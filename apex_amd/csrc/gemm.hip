@@ -1,10 +1,22 @@
-// NVFP4 prefill GEMM for gfx950: C[M,N] = A[M,K] . W[N,K]^T (x tensor_scale), A and C
-// bf16, W NVFP4 (codes uint32 [N, K/8], E4M3 scales [N, K/16]), fp32 accumulation.
+// NVFP4 prefill GEMMs for gfx950, fp32 accumulation:
+//   plain  C[M,N] = A[M,K] . W[N,K]^T (x tensor_scale)
+//   GeGLU  C[M,N] = gelu(A . G^T) * (A . U^T), gate and up in one tile
+// with A bf16 -- or fp32 activations split into bf16 hi + lo halves -- W NVFP4 (codes
+// uint32 [N, K/8], E4M3 scales [N, K/16]) and C bf16 or fp32.
 //
 // The reference computes prefill as one GEMV per token (src/ops.h:44, grid.y =
 // tokens, shaders/matmul.metal:18); here it is a dense MFMA contraction on 256 x 256
 // tiles (gemm_core.h: W dequantised exactly to bf16 in registers from LDS-staged codes,
-// v_mfma_f32_32x32x16_bf16, fp32 accumulation).
+// v_mfma_f32_32x32x16_bf16, fp32 accumulation).  A GeGLU tile's 256 W rows are 128
+// gate and 128 up rows of the same 128 output columns, interleaved by 32, so each wave
+// holds both halves of its outputs and the activation is applied before the store.
+//
+// fp32 activations (the reference's fp32 contract, src/ops.h:34-46): x = hi + lo + r
+// with hi, lo bf16 and |r| <= 2^-17 |x|; A = [hi | lo] along K (2K columns) and W's K
+// position wraps at K, so one tile loop sums hi . w + lo . w.  Every W element is
+// exact in bf16 and every bf16 product exact in fp32, so the result carries fp32
+// accumulation error plus r (rel ~1e-6), inside the reference's 1e-5 gate; it costs
+// twice the MFMA work of a bf16 GEMM and one pass over X.
 //
 // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so
 // workgroup g works on tile (g % 8) * tiles_per_xcd + g / 8, tiles M-fastest: the tiles
@@ -20,67 +32,142 @@ using namespace gemm_core;
 constexpr int WC = 4;                     // 1 x 4 waves (the 2 x 2 layout measured slower)
 constexpr int MT = 8;                     // 32-row MFMA tiles per wave
 constexpr int BM = Layout<MT, WC>::kBM;   // 256
+constexpr uint32_t kGegluCols = BN / 2;   // output columns of a GeGLU tile
 
-// 16-byte epilogue stores need 8-column row pieces at 16-byte aligned addresses.
-__device__ __forceinline__ bool uniform_wide(const GemmArgs &a) {
-    return a.N % 8 == 0 && a.ldc % 8 == 0 && ((uintptr_t)a.C & 15) == 0;
+template <bool GEGLU, bool F32> __device__ __forceinline__ bool uniform_wide(const GemmArgs &a) {
+    // 16-byte stores: 8 bf16 or 4 fp32 columns at 16-byte aligned addresses
+    constexpr uint32_t q = F32 ? 4 : 8;
+    return a.N % q == 0 && a.ldc % q == 0 && ((uintptr_t)a.C & 15) == 0;
 }
 
+template <bool GEGLU, bool F32>
 __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr uint32_t TN = GEGLU ? kGegluCols : BN;
 
     const uint32_t tiles_m = (a.M + BM - 1) / BM;
-    const uint32_t tiles_n = (a.N + BN - 1) / BN;
+    const uint32_t tiles_n = (a.N + TN - 1) / TN;
     const uint32_t tiles = tiles_m * tiles_n;
     const uint32_t per_xcd = (tiles + 7) / 8;
     const uint32_t t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (t >= tiles)
         return;
     const uint32_t m0 = (t % tiles_m) * BM;
-    const uint32_t n0 = (t / tiles_m) * BN;
+    const uint32_t n0 = (t / tiles_m) * TN;
 
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, a.M * a.K * 2);
-    const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.codes, a.N * (a.K / 2));
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scales, a.N * (a.K / 16));
-    const uint32_t K = a.K;
+    const uint32_t K = a.K, ak = a.a_k;
     const uint32_t M = a.M, N = a.N;
-    auto a_row = [=](int r) { return m0 + r < M ? (m0 + r) * K * 2 : kOut; };
-    auto w_code = [=](int r) { return n0 + r < N ? (n0 + r) * (K / 2) : kOut; };
-    auto w_scale = [=](int r) { return n0 + r < N ? (n0 + r) * (K / 16) : kOut; };
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, M * ak * 2);
+    const __amdgpu_buffer_rsrc_t rc[2] = {make_rsrc(a.codes[0], N * (K / 2)),
+                                          make_rsrc(a.codes[GEGLU ? 1 : 0], N * (K / 2))};
+    const __amdgpu_buffer_rsrc_t rs[2] = {make_rsrc(a.scales[0], N * (K / 16)),
+                                          make_rsrc(a.scales[GEGLU ? 1 : 0], N * (K / 16))};
+    auto a_row = [=](int r) { return m0 + r < M ? (m0 + r) * ak * 2 : kOut; };
+    // W tile row r -> row of its matrix: plain n0 + r; GeGLU n0 + 32 (r / 64) + r % 32
+    // (the matrix, (r / 32) % 2, is the descriptor's)
+    auto w_row = [=](int r) { return GEGLU ? n0 + 32 * (r / 64) + r % 32 : n0 + r; };
+    auto w_code = [=](int r) { return w_row(r) < N ? w_row(r) * (K / 2) : kOut; };
+    auto w_scale = [=](int r) { return w_row(r) < N ? w_row(r) * (K / 16) : kOut; };
 
     Acc<MT, WC> acc;
-    gemm_tile<MT, WC>(lds, ra, rc, rs, K, a_row, w_code, w_scale, acc);
+    gemm_tile<MT, WC>(lds, ra, rc, rs, ak, a_row, w_code, w_scale, acc, K);
 
-    store_tile_bf16<MT, WC>(acc, a.C, a.ldc, m0, n0, M, N, a.tensor_scale, uniform_wide(a));
+    const bool wide = uniform_wide<GEGLU, F32>(a);
+    if constexpr (GEGLU) {
+        using OutT = std::conditional_t<F32, float, uint16_t>;
+        store_tile_geglu<MT, OutT>(acc, static_cast<OutT *>(a.C) + (size_t)m0 * a.ldc, a.ldc,
+                                   M - m0, n0, N, a.tensor_scale[0], a.tensor_scale[1], wide);
+    } else if constexpr (F32) {
+        store_tile_f32<MT, WC>(acc, static_cast<float *>(a.C), a.ldc, m0, n0, M, N,
+                               a.tensor_scale[0], wide);
+    } else {
+        store_tile_bf16<MT, WC>(acc, static_cast<uint16_t *>(a.C), a.ldc, m0, n0, M, N,
+                                a.tensor_scale[0], wide);
+    }
 }
 
-hipError_t launch(const GemmArgs &a, hipStream_t stream) {
-    const uint32_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+template <bool GEGLU, bool F32> hipError_t launch_kernel(const GemmArgs &a, hipStream_t stream) {
+    constexpr uint32_t TN = GEGLU ? kGegluCols : BN;
+    const uint32_t tiles = ((a.M + BM - 1) / BM) * ((a.N + TN - 1) / TN);
     const uint32_t grid = 8 * ((tiles + 7) / 8);
     constexpr size_t lds = Layout<MT, WC>::kLds;
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)nvfp4_gemm_kernel,
+        hipError_t e = hipFuncSetAttribute((const void *)nvfp4_gemm_kernel<GEGLU, F32>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess)
             return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(nvfp4_gemm_kernel, dim3(grid), dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL((nvfp4_gemm_kernel<GEGLU, F32>), dim3(grid), dim3(kThreads), lds, stream, a);
     return hipGetLastError();
+}
+
+// One workgroup per row: optional RMS statistics, then hi / lo of every element.
+constexpr int kSplitThreads = 256;
+
+__device__ __forceinline__ uint16_t bf16_rne(float x) { return f32_to_bf16_bits(x); }
+
+__global__ __launch_bounds__(kSplitThreads) void split_bf16_kernel(const float *X,
+                                                                   const uint16_t *norm_w,
+                                                                   float eps, uint16_t *out,
+                                                                   uint32_t K) {
+    const float *x = X + (size_t)blockIdx.x * K;
+    uint16_t *hi = out + (size_t)blockIdx.x * 2 * K;
+    uint16_t *lo = hi + K;
+    float inv = 1.0f;
+    if (norm_w) {
+        __shared__ float red[kSplitThreads / 64];
+        float ss = 0.0f;
+        for (uint32_t k = threadIdx.x; k < K; k += kSplitThreads)
+            ss += x[k] * x[k];
+        ss = group_sum<64>(ss);
+        if ((threadIdx.x & 63) == 0)
+            red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kSplitThreads / 64; ++w)
+            total += red[w];
+        inv = 1.0f / sqrtf(total / (float)K + eps);
+    }
+    for (uint32_t k = threadIdx.x; k < K; k += kSplitThreads) {
+        float v = x[k];
+        if (norm_w)
+            v = v * inv * __uint_as_float((uint32_t)norm_w[k] << 16);
+        const uint16_t h = bf16_rne(v);
+        const float hf = __uint_as_float((uint32_t)h << 16);
+        hi[k] = h;
+        lo[k] = __builtin_isfinite(hf) ? bf16_rne(v - hf) : (uint16_t)0;
+    }
 }
 
 } // namespace
 
-bool gemm_supported(uint32_t M, uint32_t N, uint32_t K) {
-    return K % BK == 0 && K > 0 && (uint64_t)M * K * 2 < (1ull << 31) &&
-           (uint64_t)N * (K / 2) < (1ull << 31) && M > 0 && N > 0;
+bool gemm_supported(uint32_t M, uint32_t N, uint32_t K, uint32_t a_k, bool out_f32) {
+    const uint64_t esz = out_f32 ? 4 : 2;
+    return K % BK == 0 && K > 0 && M > 0 && N > 0 && (a_k == K || a_k == 2 * K) &&
+           (uint64_t)M * a_k * 2 < (1ull << 31) && (uint64_t)N * (K / 2) < (1ull << 31) &&
+           (uint64_t)BM * N * esz < (1ull << 31);
 }
 
 hipError_t gemm_launch(const GemmArgs &a, hipStream_t stream) {
-    if (!gemm_supported(a.M, a.N, a.K))
+    if (!gemm_supported(a.M, a.N, a.K, a.a_k, a.out_f32))
         return hipErrorInvalidValue;
-    return launch(a, stream);
+    if (a.geglu)
+        return a.out_f32 ? launch_kernel<true, true>(a, stream) : launch_kernel<true, false>(a, stream);
+    return a.out_f32 ? launch_kernel<false, true>(a, stream) : launch_kernel<false, false>(a, stream);
+}
+
+size_t gemm_split_bytes(uint32_t M, uint32_t K) { return (size_t)M * 2 * K * 2; }
+
+hipError_t gemm_split_launch(const float *X, const uint16_t *norm_w, float eps, uint16_t *split,
+                             uint32_t M, uint32_t K, hipStream_t stream) {
+    if (M == 0 || K == 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(split_bf16_kernel, dim3(M), dim3(kSplitThreads), 0, stream, X, norm_w, eps,
+                       split, K);
+    return hipGetLastError();
 }
 
 } // namespace apex_hip

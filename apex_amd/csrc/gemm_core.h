@@ -9,7 +9,11 @@
 // inside the A descriptor, `w_code(r)` / `w_scale(r)` the byte offsets of W tile row r
 // inside the code / scale descriptors, each 0x80000000 (out of range: reads zeros)
 // for rows that do not exist.  That is how the grouped GEMMs gather token rows and
-// place gate and up rows side by side.
+// place gate and up rows side by side.  W tile rows with (r % 64) < 32 are read through
+// the descriptors rc[0] / rs[0], the others through rc[1] / rs[1] (gate and up matrices
+// in separate buffers; pass the same descriptor twice for one matrix).  W's K position
+// is the stage's, less kw_wrap once it reaches kw_wrap: an A of [hi | lo] halves along
+// K (2K columns) meets the same W twice.
 //
 // gfx950's scaled-FP4 MFMA uses MXFP4 (32-element blocks, E8M0 scales), which cannot
 // express NVFP4's 16-element E4M3 blocks, so W is dequantised to bf16 -- exactly:
@@ -25,8 +29,10 @@
 //    ring of kStages stage buffers, kStages-1 stages ahead of the MFMAs.  A rows are
 //    128 bytes per stage with 16-byte pieces XOR-swizzled by (row / 2) % 8, so the 32
 //    lanes reading one piece of 32 consecutive rows spread over all banks.
-//  * W's packed codes (32 bytes per row per stage) and scales (4 bytes) ride the same
-//    ring with the same DMA loads; each wave reads its B fragments' code words from
+//  * W's packed codes (32 bytes per row per stage) and scales (4 bytes; tile row r at
+//    entry 128 ((r / 32) % 2) + 32 (r / 64) + r % 32, so every 64-entry DMA load reads
+//    one matrix) ride the same ring with the same DMA loads; each wave reads its B
+//    fragments' code words from
 //    LDS and dequantises them in registers right before its MFMAs
 //    (cvt_scalef32_pk_f32_fp4, x E4M3 scale, keep the exact high halves as bf16).
 //    The packed form keeps W's LDS traffic 4x smaller than a bf16 copy.
@@ -122,9 +128,10 @@ template <int WC> __device__ __forceinline__ int wave_col0() {
 
 template <int MT, int WC, typename ARow, typename WCode, typename WScale>
 __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t ra,
-                                          __amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rs,
-                                          uint32_t K, ARow a_row, WCode w_code, WScale w_scale,
-                                          Acc<MT, WC> &acc) {
+                                          const __amdgpu_buffer_rsrc_t (&rc)[2],
+                                          const __amdgpu_buffer_rsrc_t (&rs)[2], uint32_t K,
+                                          ARow a_row, WCode w_code, WScale w_scale,
+                                          Acc<MT, WC> &acc, uint32_t kw_wrap = 0xFFFFFFFFu) {
     constexpr int NT = 8 / WC;
     constexpr int WR = 4 / WC;
     constexpr int kAStage = Layout<MT, WC>::kAStage;
@@ -155,7 +162,8 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     // W codes: 16-byte slot q of the stage holds half (q%2) ^ ((q/16)%2) of tile row
     // q/2 -- rows 8..15 of every 16 swap halves, so the 16 lanes reading one half of 16
     // consecutive rows hit distinct bank groups; wave w copies slots [128w, 128w+128)
-    // with 2 DMA loads.  Scales: wave w copies rows [64w, 64w+64), 4 bytes each.
+    // with 2 DMA loads (load i: rows 64w + 32i + 0..31, all of matrix i).  Scales: wave w
+    // copies entries [64w, 64w+64), 4 bytes each: rows of matrix w / 2.
     uint32_t wc_off[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -165,13 +173,15 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         const uint32_t ro = w_code(trow);
         wc_off[i] = ro == kOut ? kOut : ro + half * 16;
     }
-    const uint32_t ws_off = w_scale(wave * 64 + lane);
+    const int se = wave * 64 + lane;   // scale entry -> tile row
+    const uint32_t ws_off = w_scale(64 * ((se % 128) / 32) + 32 * (se / 128) + se % 32);
 
     // The stage's K position rides in the scalar offset: the per-lane offsets are fixed
     // for the whole tile (a valid row plus k0 stays inside its row; an out-of-range
     // lane offset stays out of range).
     auto load_stage = [&](int buf, uint32_t k0) {
         uint8_t *base = lds + buf * kStage;
+        const uint32_t kw = k0 >= kw_wrap ? k0 - kw_wrap : k0;
 #pragma unroll
         for (int i = 0; i < kALoads; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -180,11 +190,11 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rc, (lds_void_t *)(base + kAStage + (wave * 128 + i * 64) * 16), 16, wc_off[i],
-                (int)(k0 / 2), 0, kWCpol);
+                rc[i], (lds_void_t *)(base + kAStage + (wave * 128 + i * 64) * 16), 16,
+                wc_off[i], (int)(kw / 2), 0, kWCpol);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (lds_void_t *)(base + kAStage + kWCode + wave * 64 * 4), 4, ws_off, (int)(k0 / 16),
-            0, kWCpol);
+            rs[wave / 2], (lds_void_t *)(base + kAStage + kWCode + wave * 64 * 4), 4, ws_off,
+            (int)(kw / 16), 0, kWCpol);
     };
 
 #pragma unroll
@@ -210,7 +220,8 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
             // 2h+1), slot 2r + (h ^ ((r/8)%2))
             const int r = wn + 32 * j + frow;
             wcode[j] = *reinterpret_cast<const u32x4_t *>(lwc + (2 * r + (h ^ ((r >> 3) & 1))) * 16);
-            const uint32_t sb = *reinterpret_cast<const uint16_t *>(lws + r * 4 + 2 * h);
+            const int se = 128 * ((r >> 5) & 1) + 32 * (r >> 6) + (r & 31);
+            const uint32_t sb = *reinterpret_cast<const uint16_t *>(lws + se * 4 + 2 * h);
             wsc[j] = f32x2_t{e4m3_to_f32(sb), e4m3_to_f32(sb >> 8)};
         }
     };
@@ -245,12 +256,15 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
             for (int i = 0; i < MT; ++i)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(B[j], A[i], acc[i][j], 0, 0, 0);
     };
-    // One MFMA, then up to two VALU ops and one LDS read, for the MT*NT MFMAs of a step.
+    // One MFMA, then up to three VALU ops and one LDS read, for the MT*NT MFMAs of a
+    // step.  Three slots leave room for the dequantisation of the smaller tiles (MT 4
+    // and 2 dequantise 2x and 4x as much per MFMA): 1.4 % faster MoE prefill than two,
+    // the same dense GEMM; four was slower.
     auto interleave = [&]() {
 #pragma unroll
         for (int m = 0; m < MT * NT; ++m) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0); // VALU
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0); // VALU
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
         }
         // Close the region: the next step's MFMAs must not be pulled into this one's
@@ -351,6 +365,105 @@ __device__ __forceinline__ void store_tile_bf16(const Acc<MT, WC> &acc, uint16_t
                 __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(acc[i][j][e] * scale), rc,
                                                       (int)off, 0, 0);
             }
+}
+
+// fp32 output of a tile (times `scale`), placed as store_tile_bf16 places it: a lane's
+// runs of 4 consecutive columns go out as 16-byte stores when `wide` (N and ldc
+// multiples of 4, C 16-byte aligned), otherwise one 4-byte store per element.
+template <int MT, int WC>
+__device__ __forceinline__ void store_tile_f32(const Acc<MT, WC> &acc, float *C, uint32_t ldc,
+                                               uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
+                                               float scale, bool wide) {
+    constexpr int NT = 8 / WC;
+    const int lane = threadIdx.x & 63;
+    const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)threadIdx.x >> 6);
+    const uint32_t cm = 32 * MT * (wave / WC) + (lane & 31);
+    const uint32_t cq = 32 * NT * (wave % WC) + 4 * (lane >> 5);
+    const uint64_t bytes = (uint64_t)(M - m0) * ldc * 4;
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(C + (size_t)m0 * ldc + n0, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t c = cq + 32 * j + 8 * g;
+                const uint32_t ro = (cm + 32 * i) * ldc;
+                if (wide) {
+                    u32x4_t v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        v[e] = __float_as_uint(acc[i][j][4 * g + e] * scale);
+                    const uint32_t off = n0 + c < N ? (ro + c) * 4 : kOut;
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rc, (int)off, 0, 0);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t off = n0 + c + e < N ? (ro + c + e) * 4 : kOut;
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            __float_as_uint(acc[i][j][4 * g + e] * scale), rc, (int)off, 0, 0);
+                    }
+                }
+            }
+}
+
+// GeGLU epilogue of a 1 x 4 tile whose W rows interleave two matrices by 32 (tile row r:
+// gate if (r / 32) % 2 == 0, else up; h column c0 + 32 (r / 64) + r % 32), so acc[i][0]
+// and acc[i][1] of a wave hold gate and up of the same h columns c0 + 32 wave +
+// 8 (e / 4) + 4 (lane / 32) + e % 4, token row 32 i + lane % 32:
+//   out[r][c] = gelu_tanh(gate_scale * gate) * (up_scale * up), r < nrows, c < ncols,
+// `out` at the tile's first token row, row stride ldc (shaders/geglu.metal:15-23).
+// OutT uint16_t (bf16 bits, round to nearest even) or float.  `wide`: 16-byte stores
+// (bf16: ncols and ldc multiples of 8; fp32: of 4; out 16-byte aligned), else one
+// store per element.
+template <int MT, typename OutT>
+__device__ __forceinline__ void store_tile_geglu(const Acc<MT, 4> &acc, OutT *out, uint32_t ldc,
+                                                 uint32_t nrows, uint32_t c0, uint32_t ncols,
+                                                 float gate_scale, float up_scale, bool wide) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t wcol = c0 + 32 * (threadIdx.x >> 6);  // the wave's first h column
+    const uint32_t row = lane & 31;
+    const uint64_t bytes = (uint64_t)nrows * ldc * sizeof(OutT);
+    const __amdgpu_buffer_rsrc_t rh =
+        make_rsrc(out, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        f32x16_t v;
+#pragma unroll
+        for (int q = 0; q < 16; ++q)
+            v[q] = gelu_tanh_fast(acc[i][0][q] * gate_scale) * (acc[i][1][q] * up_scale);
+        const uint32_t ro = (row + 32 * i) * ldc;
+        if (wide && sizeof(OutT) == 2) {
+            u32x4_t o[2];
+            pack_bf16_cols(v, o);
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint32_t c = wcol + 8 * (lane >> 5) + 16 * p;
+                const uint32_t off = c < ncols ? (ro + c) * 2 : kOut;
+                __builtin_amdgcn_raw_buffer_store_b128(o[p], rh, (int)off, 0, 0);
+            }
+        } else if (wide) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t c = wcol + 8 * g + 4 * (lane >> 5);
+                const uint32_t off = c < ncols ? (ro + c) * 4 : kOut;
+                const u32x4_t w = {__float_as_uint(v[4 * g]), __float_as_uint(v[4 * g + 1]),
+                                   __float_as_uint(v[4 * g + 2]), __float_as_uint(v[4 * g + 3])};
+                __builtin_amdgcn_raw_buffer_store_b128(w, rh, (int)off, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t c = wcol + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                const uint32_t off = c < ncols ? (ro + c) * (uint32_t)sizeof(OutT) : kOut;
+                if constexpr (sizeof(OutT) == 2)
+                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v[e]), rh, (int)off, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[e]), rh, (int)off, 0, 0);
+            }
+        }
+    }
 }
 
 } // namespace gemm_core

@@ -15,7 +15,6 @@ struct GemvArgs {
     void *out;                  // [tokens, out_stride] fp32 or bf16 bits
     uint32_t rows, K, tokens, out_stride;
     uint32_t sets_per_wave;     // filled by the launcher
-    uint32_t mapping;           // row-set order: 0 grid-strided, 1 per-wave ranges, 2 per-workgroup ranges
     // fp32 x only: when set, each x row is RMS-normalised first, x * (1 / sqrt(mean(x^2)
     // + norm_eps)) * norm_w (bf16 [K]), as the separate rms_norm_f32 would
     const uint16_t *norm_w;

@@ -538,7 +538,6 @@ hipError_t launch_fast(const GemvArgs &args, int nchunks, hipStream_t stream) {
         return hipErrorInvalidValue;
     GemvArgs a = args;
     a.sets_per_wave = kmax;
-    a.mapping = 0;
     if (kGemvDepth >= 3)
         hipLaunchKernelGGL((nvfp4_gemv_kernel<XT, MODE, G, SLOTS, TT, 3>), dim3(grid),
                            dim3(kThreads), lds, stream, a);

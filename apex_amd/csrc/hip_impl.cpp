@@ -75,9 +75,10 @@ void check_nvfp4_shape(uint32_t rows, uint32_t K) {
 // Direct-entry implementations (shared by the registry launchers)
 // ------------------------------------------------------------------------------------
 
-// Tokens from which a bf16 product runs as an MFMA GEMM instead of a GEMV: below it
-// the weights dominate the traffic and the GEMV streams them at the HBM rate.
-constexpr uint32_t kGemmMinTokens = 64;
+// Tokens from which the dense products (matmul, GeGLU) run as MFMA GEMMs instead of
+// GEMVs, [bf16 activations, fp32 activations]; 0 = by size (use_dense_gemm).  Set by
+// apex_hip_set_gemm_min_tokens.
+uint32_t g_gemm_min_tokens[2] = {0, 0};
 
 // Pinned staging for file -> device streaming: 8 buffers of 8 MiB, i.e. 4 reader threads
 // with a read and a copy in flight each (64 MiB pinned, kept between calls); measured
@@ -91,10 +92,82 @@ void gemm_impl(const uint16_t *A, const uint32_t *codes, const uint8_t *scales, 
     if (M == 0 || N == 0)
         return;
     require(A && codes && scales && C, "null pointer");
-    require(apex_hip::gemm_supported(M, N, K),
+    require(apex_hip::gemm_supported(M, N, K, K, false),
             "gemm: K must be a multiple of 64 and operands below 2 GiB");
     init_device_tuning();
-    apex_hip::GemmArgs g{A, codes, scales, C, M, N, K, N, ts};
+    apex_hip::GemmArgs g{};
+    g.A = A;
+    g.codes[0] = g.codes[1] = codes;
+    g.scales[0] = g.scales[1] = scales;
+    g.tensor_scale[0] = g.tensor_scale[1] = ts;
+    g.C = C;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.ldc = N;
+    g.a_k = K;
+    hip_check(apex_hip::gemm_launch(g, stream), "gemm_nvfp4 launch");
+}
+
+// Whether a dense product of `tokens` rows runs as an MFMA GEMM.  The GEMV streams W
+// once per block of up to 8 tokens; a GEMM tile runs K / 64 stages one after another,
+// so a grid of few tiles is bound by that chain (2112 x 2816: ~60 us bf16, ~120 us
+// fp32, whatever the token count up to 256).  Measured crossovers (gfx950): with at
+// least 64 tiles (21504 x 5376) the GEMM is faster from 16 tokens for GeGLU and from 32
+// for matmul; with fewer (2112 x 2816: 9 matmul / 17 GeGLU tiles) from 64 tokens for
+// GeGLU and from 128 for matmul.
+bool use_dense_gemm(uint32_t tokens, uint32_t rows, uint32_t K, bool bf16, bool geglu) {
+    if (!apex_hip::gemm_supported(tokens, rows, K, bf16 ? K : 2 * K, !bf16))
+        return false;
+    if (const uint32_t fixed = g_gemm_min_tokens[bf16 ? 0 : 1])
+        return tokens >= fixed;
+    const uint32_t cols = geglu ? 128 : 256;   // output columns of a tile
+    const uint64_t tiles = (uint64_t)((tokens + 255) / 256) * ((rows + cols - 1) / cols);
+    if (tiles >= 64)
+        return tokens >= (geglu ? 16u : 32u);
+    return tokens >= (geglu ? 64u : 128u);
+}
+
+// The MFMA GEMM for matmul (geglu false: W = c0/s0) or GeGLU (gate c0/s0, up c1/s1):
+// bf16 x directly; fp32 x (optionally RMS-normalised by norm_w first) through its
+// bf16 hi / lo split, held in a stream-ordered scratch allocation for the call.
+void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, bool geglu,
+                const uint32_t *c0, const uint8_t *s0, float ts0, const uint32_t *c1,
+                const uint8_t *s1, float ts1, void *out, uint32_t M, uint32_t N, uint32_t K,
+                hipStream_t stream) {
+    apex_hip::GemmArgs g{};
+    g.codes[0] = c0;
+    g.scales[0] = s0;
+    g.codes[1] = geglu ? c1 : c0;
+    g.scales[1] = geglu ? s1 : s0;
+    g.tensor_scale[0] = ts0;
+    g.tensor_scale[1] = ts1;
+    g.C = out;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.ldc = N;
+    g.geglu = geglu;
+    g.out_f32 = !bf16;
+    if (bf16) {
+        g.A = static_cast<const uint16_t *>(x);
+        g.a_k = K;
+        hip_check(apex_hip::gemm_launch(g, stream), "gemm_nvfp4 launch");
+        return;
+    }
+    void *split = nullptr;
+    hip_check(hipMallocAsync(&split, apex_hip::gemm_split_bytes(M, K), stream),
+              "fp32 GEMM split buffer");
+    struct Release {
+        void *p;
+        hipStream_t s;
+        ~Release() { (void)hipFreeAsync(p, s); }
+    } release{split, stream};
+    hip_check(apex_hip::gemm_split_launch(static_cast<const float *>(x), norm_w, eps,
+                                          static_cast<uint16_t *>(split), M, K, stream),
+              "fp32 GEMM split launch");
+    g.A = static_cast<const uint16_t *>(split);
+    g.a_k = 2 * K;
     hip_check(apex_hip::gemm_launch(g, stream), "gemm_nvfp4 launch");
 }
 
@@ -106,9 +179,9 @@ void matmul_impl(const void *x, bool bf16, const uint32_t *codes, const uint8_t 
         return;
     require(x && codes && scales && out, "null pointer");
     init_device_tuning();
-    if (bf16 && tokens >= kGemmMinTokens && apex_hip::gemm_supported(tokens, rows, K)) {
-        gemm_impl(static_cast<const uint16_t *>(x), codes, scales, ts, static_cast<uint16_t *>(out),
-                  tokens, rows, K, stream);
+    if (use_dense_gemm(tokens, rows, K, bf16, false)) {
+        dense_gemm(x, bf16, nullptr, 0.0f, false, codes, scales, ts, nullptr, nullptr, 1.0f, out,
+                   tokens, rows, K, stream);
         return;
     }
     apex_hip::GemvArgs a{};
@@ -136,13 +209,19 @@ void geglu_impl(const void *x, bool bf16, const uint32_t *gc, const uint8_t *gs,
     if (tokens == 0 || rows == 0)
         return;
     require(x && gc && gs && uc && us && out, "null pointer");
+    require(!(norm_w && bf16), "geglu with RMSNorm: fp32 x only");
+    init_device_tuning();
+    if (use_dense_gemm(tokens, rows, K, bf16, true)) {
+        dense_gemm(x, bf16, norm_w, norm_eps, true, gc, gs, gts, uc, us, uts, out, tokens, rows,
+                   K, stream);
+        return;
+    }
     if (norm_w)
-        require(!bf16 && K % 32 == 0 && K <= 8192 && (uintptr_t)x % 16 == 0 &&
+        require(K % 32 == 0 && K <= 8192 && (uintptr_t)x % 16 == 0 &&
                     (uintptr_t)gc % 16 == 0 && (uintptr_t)uc % 16 == 0 &&
                     (uintptr_t)gs % 2 == 0 && (uintptr_t)us % 2 == 0,
                 "geglu with RMSNorm: fp32 x, K a multiple of 32 up to 8192, x and codes "
                 "16-byte aligned, scales 2-byte aligned");
-    init_device_tuning();
     apex_hip::GemvArgs a{};
     a.norm_w = norm_w;
     a.norm_eps = norm_eps;
@@ -1038,6 +1117,13 @@ int apex_hip_read_probe(const void *ptr, size_t bytes, uint32_t *sink, void *str
 }
 
 int apex_hip_read_probe_sink_words(void) { return 8 * apex_hip::kNumCUs; }
+
+int apex_hip_set_gemm_min_tokens(uint32_t bf16_tokens, uint32_t f32_tokens) {
+    return guard([&] {
+        g_gemm_min_tokens[0] = bf16_tokens;
+        g_gemm_min_tokens[1] = f32_tokens;
+    });
+}
 
 int apex_hip_set_gemv_waves_per_cu(int waves) {
     return guard([&] {

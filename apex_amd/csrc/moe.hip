@@ -1209,32 +1209,12 @@ __device__ __forceinline__ void gateup_tile(const MoeArgs &a, uint8_t *lds, cons
         const uint32_t col = c0 + 32 * (r / 64) + r % 32;
         return col < I ? ((r & 32) ? us : gs) + col * (H / 16) : kOut;
     };
+    const __amdgpu_buffer_rsrc_t rw2[2] = {rw, rw};
     Acc<MT, 4> acc;
-    gemm_tile<MT, 4>(lds, ra, rw, rw, H, a_row, w_code, w_scale, acc);
-    // h[row0 + r][col] = gelu(gate) * up, branch-free: the store descriptor ends at
-    // row nrows, columns past I get an out-of-range offset.  acc[i][0] / acc[i][1] hold
-    // gate / up of the same h columns (c0 + 32 wave + 8 (e / 4) + 4 (lane / 32) + e % 4)
-    // of token row 32 i + lane % 32; I is a multiple of 64, so 8-column pieces never
-    // straddle it.
-    const int lane = threadIdx.x & 63;
-    const uint32_t col = c0 + 32 * (threadIdx.x >> 6) + 8 * (lane >> 5);
-    const uint32_t row = lane & 31;
-    const __amdgpu_buffer_rsrc_t rh = make_rsrc(a.h + (size_t)row0 * I, nrows * I * 2);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        f32x16_t v;
-#pragma unroll
-        for (int q = 0; q < 16; ++q)
-            v[q] = gelu_tanh_fast(acc[i][0][q]) * acc[i][1][q];
-        u32x4_t o[2];
-        pack_bf16_cols(v, o);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const uint32_t c = col + 16 * p;
-            const uint32_t off = c < I ? ((row + 32 * i) * I + c) * 2 : kOut;
-            __builtin_amdgcn_raw_buffer_store_b128(o[p], rh, (int)off, 0, 0);
-        }
-    }
+    gemm_tile<MT, 4>(lds, ra, rw2, rw2, H, a_row, w_code, w_scale, acc);
+    // h[row0 + r][col] = gelu(gate) * up, 16-byte stores (I is a multiple of 64, so
+    // 8-column pieces never straddle it); the store descriptor ends at row nrows.
+    store_tile_geglu<MT, uint16_t>(acc, a.h + (size_t)row0 * I, I, nrows, c0, I, 1.0f, 1.0f, true);
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup b on XCD b % 8).
@@ -1280,8 +1260,9 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
     auto a_row = [=](int r) { return (uint32_t)r < nrows ? (row0 + r) * I * 2 : kOut; };
     auto w_code = [=](int r) { return n0 + r < H ? dw + (n0 + r) * (I / 2) : kOut; };
     auto w_scale = [=](int r) { return n0 + r < H ? ds + (n0 + r) * (I / 16) : kOut; };
+    const __amdgpu_buffer_rsrc_t rw2[2] = {rw, rw};
     Acc<MT, 4> acc;
-    gemm_tile<MT, 4>(lds, ra, rw, rw, I, a_row, w_code, w_scale, acc);
+    gemm_tile<MT, 4>(lds, ra, rw2, rw2, I, a_row, w_code, w_scale, acc);
     store_tile_bf16<MT, 4>(acc, a.d + (size_t)row0 * H, H, 0, n0, nrows, H, 1.0f, true);
 }
 

@@ -98,6 +98,7 @@ _PROTOS = {
     "apex_hip_read_probe": (_I, [_P, _SZ, _P, _P]),
     "apex_hip_read_probe_sink_words": (_I, []),
     "apex_hip_set_gemv_waves_per_cu": (_I, [_I]),
+    "apex_hip_set_gemm_min_tokens": (_I, [_U32, _U32]),
     "apex_moe_route_bf16": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
     "apex_moe_workspace_bytes": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
     "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
@@ -327,6 +328,11 @@ def read_probe_sink_words() -> int:
 
 def set_gemv_waves_per_cu(waves: int) -> None:
     check(lib().apex_hip_set_gemv_waves_per_cu(waves))
+
+
+def set_gemm_min_tokens(bf16_tokens: int = 0, f32_tokens: int = 0) -> None:
+    """Tokens from which the dense matmul / GeGLU run as MFMA GEMMs (0: by size)."""
+    check(lib().apex_hip_set_gemm_min_tokens(bf16_tokens, f32_tokens))
 
 
 # ---- MoE expert FFN --------------------------------------------------------------

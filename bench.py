@@ -22,6 +22,8 @@ the path, each timed the same way (HIP events around back-to-back steps):
                 intermediate 704, Zipf(1.1) routing -> TFLOP/s vs the 2.5 PFLOP/s
                 dense bf16 MFMA peak (flops of the routed pairs only);
   gemm_prefill  dense prefill GEMM bf16 [2048,5376] x NVFP4 [21504x5376]^T -> TFLOP/s;
+  geglu_prefill / matmul_prefill_f32  the same weight shape through the fused GeGLU
+                (bf16 x) and the fp32 matmul (fp32 x, bf16 hi + lo split) -> TFLOP/s;
   moe_decode    MoE decode: 16 tokens, same experts -> GB/s of the distinct experts'
                 weights + activations (expert slots rotated over copies > MALL).
 --calibrate runs, before the timed steps, one streaming read of 1 GiB and one 256 MiB
@@ -240,6 +242,38 @@ def time_gemm_prefill(steps, warmup, M=2048, N=21504, K=5376):
             "yardstick_vendor_bf16_gemm_tflops": vendor_bf16_gemm(M, N, K, steps, warmup)}
 
 
+def time_dense_prefill(steps, warmup, T=2048, N=21504, K=5376):
+    """Prefill through the reference-named dense ops at the headline weight shape:
+    the fused GeGLU with bf16 activations (gate and up in one MFMA GEMM) and the fp32
+    matmul (the reference's fp32 contract: x split into bf16 hi + lo, twice the MFMA
+    work).  TFLOP/s count the useful products only, 2 T N K per matrix."""
+    rng = np.random.default_rng(0)
+    g, u = synth.nvfp4_weights(rng, N, K), synth.nvfp4_weights(rng, N, K)
+    dw = [hip.DeviceArray.from_numpy(a) for a in (g.codes, g.scales, u.codes, u.scales)]
+    xb = hip.DeviceArray.from_numpy(synth.normal_bf16(rng, (T, K)))
+    xf = hip.DeviceArray.from_numpy(rng.standard_normal((T, K)).astype(np.float32))
+    hb, yf = hip.DeviceArray((T, N), np.uint16), hip.DeviceArray((T, N), np.float32)
+    stream = hip.Stream()
+    out = {}
+    for name, flops, fn, text in [
+        ("geglu_prefill", 4.0 * T * N * K,
+         lambda i: hip.nvfp4_geglu_bf16(xb, *dw, hb, T, N, K, stream=stream),
+         f"prefill fused GeGLU: x bf16 [{T},{K}], gate/up NVFP4 [{N}x{K}] -> bf16 [{T},{N}]"),
+        ("matmul_prefill_f32", 2.0 * T * N * K,
+         lambda i: hip.nvfp4_matmul_f32(xf, dw[0], dw[1], yf, T, N, K, stream=stream),
+         f"prefill matmul, fp32 contract: x fp32 [{T},{K}] x NVFP4 [{N}x{K}]^T -> fp32 "
+         f"[{T},{N}] (bf16 hi + lo split, 2x MFMA work)")]:
+        sec = time_steps(fn, steps, warmup, stream)
+        tf = flops / sec / 1e12
+        out[name] = {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
+                     "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(flops),
+                     "workload": text}
+    stream.close()
+    for a in dw + [xb, xf, hb, yf]:
+        a.close()
+    return out
+
+
 def time_norms(steps, warmup, T=4096, H=2816, heads=16, D=256):
     """The two normalisation kernels at prefill size: RMSNorm of x fp32 [4096, 2816]
     and per-head RMSNorm + RoPE of q fp32 [4096, 16, 256] (128 rotated pairs).  Both
@@ -433,7 +467,8 @@ def main(argv=None):
     ap.add_argument("--calibrate", action="store_true",
                     help="run the known-size read and copy kernels first (counter scaling)")
     ap.add_argument("--only", choices=["moe_prefill", "gemm_prefill", "moe_decode", "norms",
-                                       "dense_mlp_decode", "router", "slot_streaming"],
+                                       "dense_mlp_decode", "router", "slot_streaming",
+                                       "dense_prefill"],
                     help="profiling aid: time one secondary workload and print its record only")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -447,7 +482,8 @@ def main(argv=None):
         fn = {"moe_prefill": time_moe_prefill, "gemm_prefill": time_gemm_prefill,
               "moe_decode": time_moe_decode, "norms": time_norms,
               "dense_mlp_decode": time_dense_mlp_decode, "router": time_router,
-              "slot_streaming": lambda steps, warmup: time_slot_streaming()}[args.only]
+              "slot_streaming": lambda steps, warmup: time_slot_streaming(),
+              "dense_prefill": time_dense_prefill}[args.only]
         print(json.dumps({args.only: fn(args.steps, args.warmup)}), flush=True)
         return 0
     r = time_geglu(args.steps, args.warmup)
@@ -488,6 +524,7 @@ def main(argv=None):
         line["secondary"] = {
             "moe_prefill": time_moe_prefill(sec_steps, sec_warm),
             "gemm_prefill": time_gemm_prefill(sec_steps, sec_warm),
+            **time_dense_prefill(sec_steps, sec_warm),
             "moe_decode": time_moe_decode(max(1, args.steps // 10), max(1, args.warmup // 10)),
         }
         line["secondary"].update(time_norms(max(1, args.steps // 10), max(1, args.warmup // 10)))

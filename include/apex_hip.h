@@ -190,13 +190,17 @@ int apex_hip_validate_run(const char *kernel, const apex_hip_arg *args, size_t n
  * -------------------------------------------------------------------------------*/
 
 /* shaders/matmul.metal:4-53 / src/tests/cpu_ref.h:48-63: out[t, r] = sum_k W[r,k] x[t,k]
- * with fp32 activations and outputs. */
+ * with fp32 activations and outputs.  A GEMV for few tokens; for more (K % 64 == 0,
+ * apex_hip_set_gemm_min_tokens) an MFMA GEMM on x split into bf16 hi + lo halves
+ * (|x - hi - lo| <= 2^-17 |x|), which allocates its split buffer (tokens * K * 4
+ * bytes) stream-ordered for the call. */
 int apex_nvfp4_matmul_f32(const float *x, const uint32_t *codes, const uint8_t *scales,
                           float tensor_scale, float *out, uint32_t tokens, uint32_t rows,
                           uint32_t K, void *stream);
 
 /* Same product with bf16 activations and bf16 outputs (fp32 accumulation): a GEMV
- * for few tokens, the MFMA GEMM below from 64 tokens (when K % 64 == 0). */
+ * for few tokens, the MFMA GEMM below for more (K % 64 == 0,
+ * apex_hip_set_gemm_min_tokens). */
 int apex_nvfp4_matmul_bf16(const uint16_t *x, const uint32_t *codes, const uint8_t *scales,
                            float tensor_scale, uint16_t *out, uint32_t tokens, uint32_t rows,
                            uint32_t K, void *stream);
@@ -209,15 +213,18 @@ int apex_nvfp4_gemm_bf16(const uint16_t *A, const uint32_t *codes, const uint8_t
                          float tensor_scale, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
                          void *stream);
 
-/* src/ops.h:65-67 fused: out[t, r] = gelu_tanh(Wg[r].x_t) * (Wu[r].x_t). */
+/* src/ops.h:65-67 fused: out[t, r] = gelu_tanh(Wg[r].x_t) * (Wu[r].x_t).  Like the
+ * matmuls: a GEMV for few tokens, for more (K % 64 == 0) one MFMA GEMM whose tiles hold
+ * gate and up rows of the same outputs (fp32 x: through its bf16 hi + lo split). */
 int apex_nvfp4_geglu_f32(const float *x, const uint32_t *gate_codes, const uint8_t *gate_scales,
                          float gate_tensor_scale, const uint32_t *up_codes,
                          const uint8_t *up_scales, float up_tensor_scale, float *out,
                          uint32_t tokens, uint32_t rows, uint32_t K, void *stream);
 /* The same after an RMSNorm of each x row (the step before the MLP in the reference's
  * model, src/ops.h:18-26 rmsNorm then 65-67): x_t * (1 / sqrt(mean(x_t^2) + eps)) * w,
- * computed inside the GEMV's x staging instead of a separate launch and buffer.
- * norm_w is bf16 [K]; needs K % 32 == 0, K <= 8192, x and codes 16-byte aligned. */
+ * computed inside the GEMV's x staging (or the GEMM's split pass) instead of a
+ * separate launch and buffer.  norm_w is bf16 [K]; the GEMV form needs K % 32 == 0,
+ * K <= 8192, x and codes 16-byte aligned. */
 int apex_nvfp4_geglu_rms_norm_f32(const float *x, const uint16_t *norm_w, float eps,
                                   const uint32_t *gate_codes, const uint8_t *gate_scales,
                                   float gate_tensor_scale, const uint32_t *up_codes,
@@ -284,6 +291,13 @@ int apex_hip_read_probe_sink_words(void);
 
 /* Launch tuning of the GEMV kernels: target resident waves per CU (default 12). */
 int apex_hip_set_gemv_waves_per_cu(int waves);
+
+/* Tokens from which apex_nvfp4_matmul_* and apex_nvfp4_geglu_* (and their registry
+ * kernels) run as MFMA GEMMs instead of GEMVs, for bf16 and for fp32 activations
+ * (0 = by size, the default: GeGLU from 16 tokens and matmul from 32 when the GEMM has
+ * at least 64 tiles of 256 tokens x 128 (GeGLU) or 256 (matmul) outputs, else from 64
+ * and 128).  Process-wide; results agree within the stated tolerances either way. */
+int apex_hip_set_gemm_min_tokens(uint32_t bf16_tokens, uint32_t f32_tokens);
 
 /* ---- MoE expert FFN (no reference kernel) ------------------------------------------
  * Semantics: tools/dump_reference.py:208-219 (router top-k, experts combined with the

@@ -101,9 +101,9 @@ def test_geglu_norm_fused_matches_separate_norm_and_rejects_bad_layouts():
 
 @pytest.mark.parametrize("T", [1, 96])
 def test_dense_mlp_bf16(T):
-    """bf16 activations after the norm: fused GeGLU (GEMV, or MFMA GEMM from 64 tokens)
-    and down projection; the oracle runs the same composition on the bf16-rounded
-    normed input."""
+    """bf16 activations after the norm: fused GeGLU and down projection (96 tokens: the
+    GeGLU as an MFMA GEMM, the down projection's 11 tiles still a GEMV); the oracle runs
+    the same composition on the bf16-rounded normed input."""
     case = synth.dense_mlp_case(seed=200 + T, tokens=T)
     h, nw, g, u, d = case
     x = oracle.rms_norm(h, nw, EPS)

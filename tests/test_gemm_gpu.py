@@ -5,7 +5,7 @@ import pytest
 
 import oracle
 from apex_amd import hip, synth
-from tests.helpers import TOL_BF16, bf16, rel_l2
+from tests.helpers import TOL_BF16, TOL_REF_GATE, bf16, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -97,9 +97,11 @@ def test_gemm_many_tiles_exact():
     assert rel_l2(bf16(C)[:, ni], want) < TOL_BF16
 
 
-def test_gemm_tensor_scale_and_matmul_dispatch():
-    """apex_nvfp4_matmul_bf16 switches to the GEMM from 64 tokens; results agree with
-    the GEMM entry point, and a power-of-two tensor scale scales the output exactly."""
+def test_gemm_tensor_scale_and_matmul_dispatch(gemm_threshold):
+    """apex_nvfp4_matmul_bf16 switches to the GEMM (here from 64 tokens); results agree
+    with the GEMM entry point, and a power-of-two tensor scale scales the output
+    exactly."""
+    hip.set_gemm_min_tokens(64, 0)
     rng = np.random.default_rng(3)
     w = synth.nvfp4_weights(rng, 448, 1024)
     A = synth.normal_bf16(rng, (96, 1024))
@@ -110,3 +112,108 @@ def test_gemm_tensor_scale_and_matmul_dispatch():
     assert np.array_equal(out.numpy(), C1)
     C2 = gemm(A, w, 0.5)
     assert np.array_equal(bf16(C2), bf16(C1) * np.float32(0.5))
+
+
+# ---- dense matmul / GeGLU through the MFMA GEMM (from 64 tokens), bf16 and fp32 ----
+
+
+@pytest.fixture
+def gemm_threshold():
+    """Dense matmul / GeGLU through the GEMM at every token count (the size rule picks
+    GEMV or GEMM by grid size); restores the rule afterwards."""
+    hip.set_gemm_min_tokens(1, 1)
+    yield
+    hip.set_gemm_min_tokens(0, 0)
+
+
+def run_matmul_f32(X, w, ts=1.0):
+    T, K = X.shape
+    out = hip.DeviceArray((T, w.rows), np.float32)
+    hip.nvfp4_matmul_f32(dev(X), dev(w.codes), dev(w.scales), out, T, w.rows, K, ts)
+    hip.synchronize()
+    return out.numpy()
+
+
+def run_geglu(x, g, u, f32, gs=1.0, us=1.0, norm=None):
+    T, K = x.shape
+    out = hip.DeviceArray((T, g.rows), np.float32 if f32 else np.uint16)
+    args = (dev(g.codes), dev(g.scales), dev(u.codes), dev(u.scales), out, T, g.rows, K)
+    if norm is not None:
+        hip.nvfp4_geglu_rms_norm_f32(dev(x), dev(norm[0]), norm[1], *args, gate_scale=gs, up_scale=us)
+    elif f32:
+        hip.nvfp4_geglu_f32(dev(x), *args, gate_scale=gs, up_scale=us)
+    else:
+        hip.nvfp4_geglu_bf16(dev(x), *args, gate_scale=gs, up_scale=us)
+    hip.synchronize()
+    return out.numpy() if f32 else bf16(out.numpy())
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 448, 512), (64, 100, 320), (129, 37, 64)])
+def test_matmul_f32_split_gemm_one_hot_exact(M, N, K, gemm_threshold):
+    """fp32 activations through the bf16 hi + lo split GEMM: a one-hot row splits into
+    hi = 1, lo = 0, so C[m, n] = W[n, p(m)] exactly (also N not a multiple of 4: one
+    fp32 store per element)."""
+    rng = np.random.default_rng(M + N)
+    w = synth.nvfp4_weights(rng, N, K)
+    perm = rng.integers(0, K, size=M)
+    X = np.zeros((M, K), np.float32)
+    X[np.arange(M), perm] = 1.0
+    got = run_matmul_f32(X, w)
+    want = oracle.decode(w.codes, w.scales)[:, perm].T + np.float32(0.0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 448, 1024), (64, 2112, 2816), (100, 36, 128)])
+def test_matmul_f32_gemm_matches_oracle_and_gemv(M, N, K, gemm_threshold):
+    """The split GEMM meets the reference's fp32 gate (rel L2 < 1e-5) against the fp64
+    oracle, and agrees with the fp32 GEMV on the same inputs; a tensor scale of 0.5
+    halves the output exactly."""
+    rng = np.random.default_rng(3 * M + N)
+    w = synth.nvfp4_weights(rng, N, K)
+    X = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    got = run_matmul_f32(X, w)
+    want = oracle.matvec(w.codes, w.scales, X)
+    assert rel_l2(got, want) < TOL_REF_GATE
+    assert np.array_equal(run_matmul_f32(X, w, 0.5), got * np.float32(0.5))
+    hip.set_gemm_min_tokens(0, 1 << 20)   # GEMV for every size
+    gemv = run_matmul_f32(X, w)
+    assert rel_l2(got, gemv) < TOL_REF_GATE
+
+
+@pytest.mark.parametrize("T,rows,K", [(300, 448, 1024), (64, 100, 320), (97, 37, 192)])
+def test_geglu_gemm_bf16_and_f32(T, rows, K, gemm_threshold):
+    """GeGLU GEMM tiles hold 128 gate and 128 up rows of the same outputs: 448 rows end
+    in a half-empty tile, 100 and 37 rows need per-element stores.  bf16 against the
+    oracle on the bf16 inputs (1e-2), fp32 at the reference gate (1e-5); tensor scales
+    apply per matrix."""
+    rng = np.random.default_rng(T + rows + K)
+    g, u = synth.nvfp4_weights(rng, rows, K), synth.nvfp4_weights(rng, rows, K)
+    x = synth.normal_bf16(rng, (T, K))
+    xf = bf16(x)
+    want = oracle.geglu(oracle.matvec(g.codes, g.scales, xf), oracle.matvec(u.codes, u.scales, xf))
+    assert rel_l2(run_geglu(x, g, u, False), want) < TOL_BF16
+    assert rel_l2(run_geglu(xf, g, u, True), want) < TOL_REF_GATE
+    want_s = oracle.geglu(oracle.matvec(g.codes, g.scales, xf, 0.5),
+                          oracle.matvec(u.codes, u.scales, xf, 2.0))
+    assert rel_l2(run_geglu(xf, g, u, True, 0.5, 2.0), want_s) < TOL_REF_GATE
+    hip.set_gemm_min_tokens(1 << 20, 1 << 20)
+    assert rel_l2(run_geglu(xf, g, u, True), want) < TOL_REF_GATE
+
+
+def test_geglu_rms_norm_gemm_matches_oracle(gemm_threshold):
+    """RMSNorm folded into the split pass: 200 tokens of the Gemma dense shape (hidden
+    2816, intermediate 2112) against rms_norm + GeGLU in the oracle, and against the
+    GEMV form of the same entry point."""
+    rng = np.random.default_rng(21)
+    T, rows, K, eps = 200, 2112, 2816, 1e-6
+    x = (rng.standard_normal((T, K)) * 3).astype(np.float32)
+    nw = synth.bf16_from_f32((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    g, u = synth.nvfp4_weights(rng, rows, K), synth.nvfp4_weights(rng, rows, K)
+    got = run_geglu(x, g, u, True, norm=(nw, eps))
+    xn = oracle.rms_norm(x, nw, eps)
+    ids = np.sort(rng.choice(rows, 256, replace=False))
+    want = oracle.geglu(oracle.matvec_rows(g.codes, g.scales, xn, ids),
+                        oracle.matvec_rows(u.codes, u.scales, xn, ids))
+    assert rel_l2(got[:, ids], want) < TOL_REF_GATE
+    hip.set_gemm_min_tokens(0, 1 << 20)
+    assert rel_l2(run_geglu(x, g, u, True, norm=(nw, eps)), got) < TOL_REF_GATE
