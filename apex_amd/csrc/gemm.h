@@ -28,6 +28,15 @@ bool gemm_supported(uint32_t M, uint32_t N, uint32_t K, uint32_t a_k, bool out_f
 
 hipError_t gemm_launch(const GemmArgs &a, hipStream_t stream);
 
+// Split-K form for grids of few tiles: S workgroups per tile each run a contiguous
+// range of K stages (for a_k = 2K none crosses from the hi half to the lo half) and
+// store fp32 partials, part[S][M][N] (GeGLU: gate and up, part[S][2][M][N]); a second
+// kernel sums them in split order and applies the epilogue.  gemm_splitk_splits gives
+// the split count for a's shape (1: run gemm_launch).
+uint32_t gemm_splitk_splits(const GemmArgs &a);
+size_t gemm_splitk_bytes(const GemmArgs &a, uint32_t splits);
+hipError_t gemm_splitk_launch(const GemmArgs &a, uint32_t splits, float *part, hipStream_t stream);
+
 // fp32 activations X [M, K] (row stride K) -> split [M, 2K] bf16: hi = bf16(x) and
 // lo = bf16(x - hi), both rounded to nearest even (lo = 0 where hi is not finite), so
 // x = hi + lo + r with |r| <= 2^-17 |x|.  With norm_w (bf16 [K]), x is first

@@ -25,6 +25,8 @@
 #include "gemm.h"
 #include "gemm_core.h"
 
+#include <algorithm>
+
 namespace apex_hip {
 namespace {
 
@@ -103,6 +105,150 @@ template <bool GEGLU, bool F32> hipError_t launch_kernel(const GemmArgs &a, hipS
     return hipGetLastError();
 }
 
+// ---- split-K ------------------------------------------------------------------
+
+// GeGLU partials of a tile: acc[i][0] (gate) / acc[i][1] (up) of h columns c0 + 32 wave
+// + 8 (e / 4) + 4 (lane / 32) + e % 4, token row m0 + 32 i + lane % 32, into gate / up
+// [M, N] fp32.
+template <int MT>
+__device__ __forceinline__ void store_geglu_partials(const Acc<MT, 4> &acc, float *gate, float *up,
+                                                     uint32_t M, uint32_t N, uint32_t m0,
+                                                     uint32_t c0) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t wcol = c0 + 32 * (threadIdx.x >> 6);
+    const uint32_t row = lane & 31;
+    const uint64_t bytes = (uint64_t)(M - m0) * N * 4;
+    const uint32_t nb = bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u;
+    const __amdgpu_buffer_rsrc_t rd[2] = {make_rsrc(gate + (size_t)m0 * N, nb),
+                                          make_rsrc(up + (size_t)m0 * N, nb)};
+    const bool wide = N % 4 == 0;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t c = wcol + 8 * g + 4 * (lane >> 5);
+                const uint32_t ro = (row + 32 * i) * N;
+                if (wide) {
+                    const u32x4_t v = {__float_as_uint(acc[i][j][4 * g]),
+                                       __float_as_uint(acc[i][j][4 * g + 1]),
+                                       __float_as_uint(acc[i][j][4 * g + 2]),
+                                       __float_as_uint(acc[i][j][4 * g + 3])};
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rd[j], (int)(c < N ? (ro + c) * 4 : kOut),
+                                                           0, 0);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            __float_as_uint(acc[i][j][4 * g + e]), rd[j],
+                            (int)(c + e < N ? (ro + c + e) * 4 : kOut), 0, 0);
+                }
+            }
+}
+
+// Workgroup b: tile b / S, split b % S.  Split s of a tile covers the stages
+// [s nh / Sh, (s + 1) nh / Sh) of half s / Sh (Sh = S / halves splits per half of nh
+// stages; one half for bf16 A, two -- hi, lo -- for split fp32 A), so its W columns
+// are its A columns less K in the lo half.
+template <bool GEGLU>
+__global__ __launch_bounds__(kThreads) void nvfp4_gemm_splitk_kernel(GemmArgs a, float *part,
+                                                                     uint32_t S) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr uint32_t TN = GEGLU ? kGegluCols : BN;
+    const uint32_t tiles_m = (a.M + BM - 1) / BM;
+    const uint32_t t = blockIdx.x / S, s = blockIdx.x % S;
+    const uint32_t m0 = (t % tiles_m) * BM;
+    const uint32_t n0 = (t / tiles_m) * TN;
+
+    const uint32_t K = a.K, ak = a.a_k;
+    const uint32_t M = a.M, N = a.N;
+    const uint32_t halves = ak / K;
+    const uint32_t sh_n = S / halves, nh = K / BK;
+    const uint32_t half = s / sh_n, sh = s % sh_n;
+    const uint32_t st0 = sh * nh / sh_n, st1 = (sh + 1) * nh / sh_n;
+    const uint32_t kw0 = st0 * BK;              // W column of the split's first stage
+    const uint32_t ka0 = half * K + kw0;        // A column
+    const uint32_t len = (st1 - st0) * BK;
+
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, M * ak * 2);
+    const __amdgpu_buffer_rsrc_t rc[2] = {make_rsrc(a.codes[0], N * (K / 2)),
+                                          make_rsrc(a.codes[GEGLU ? 1 : 0], N * (K / 2))};
+    const __amdgpu_buffer_rsrc_t rs[2] = {make_rsrc(a.scales[0], N * (K / 16)),
+                                          make_rsrc(a.scales[GEGLU ? 1 : 0], N * (K / 16))};
+    auto a_row = [=](int r) { return m0 + r < M ? ((m0 + r) * ak + ka0) * 2 : kOut; };
+    auto w_row = [=](int r) { return GEGLU ? n0 + 32 * (r / 64) + r % 32 : n0 + r; };
+    auto w_code = [=](int r) { return w_row(r) < N ? w_row(r) * (K / 2) + kw0 / 2 : kOut; };
+    auto w_scale = [=](int r) { return w_row(r) < N ? w_row(r) * (K / 16) + kw0 / 16 : kOut; };
+
+    Acc<MT, WC> acc;
+    gemm_tile<MT, WC>(lds, ra, rc, rs, len, a_row, w_code, w_scale, acc);
+
+    const size_t mn = (size_t)M * N;
+    if constexpr (GEGLU)
+        store_geglu_partials<MT>(acc, part + (2 * s) * mn, part + (2 * s + 1) * mn, M, N, m0, n0);
+    else
+        store_tile_f32<MT, WC>(acc, part + s * mn, N, m0, n0, M, N, 1.0f,
+                               N % 4 == 0);
+}
+
+// C = epilogue(sum over s = 0 .. S-1 of the partials, in that order).
+template <bool GEGLU, bool F32>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *part, uint32_t S, GemmArgs a) {
+    const size_t mn = (size_t)a.M * a.N;
+    for (size_t q = blockIdx.x * 256ull + threadIdx.x; q < mn; q += (size_t)gridDim.x * 256) {
+        float v;
+        if constexpr (GEGLU) {
+            float g = 0.0f, u = 0.0f;
+            for (uint32_t s = 0; s < S; ++s) {
+                g += part[2 * s * mn + q];
+                u += part[(2 * s + 1) * mn + q];
+            }
+            v = gelu_tanh_fast(g * a.tensor_scale[0]) * (u * a.tensor_scale[1]);
+        } else {
+            float acc = 0.0f;
+            for (uint32_t s = 0; s < S; ++s)
+                acc += part[s * mn + q];
+            v = acc * a.tensor_scale[0];
+        }
+        const size_t m = q / a.N, n = q - m * a.N;
+        const size_t o = m * a.ldc + n;
+        if constexpr (F32)
+            static_cast<float *>(a.C)[o] = v;
+        else
+            static_cast<uint16_t *>(a.C)[o] = f32_to_bf16_bits(v);
+    }
+}
+
+template <bool GEGLU> hipError_t launch_splitk(const GemmArgs &a, uint32_t S, float *part,
+                                               hipStream_t stream) {
+    constexpr uint32_t TN = GEGLU ? kGegluCols : BN;
+    const uint32_t tiles = ((a.M + BM - 1) / BM) * ((a.N + TN - 1) / TN);
+    constexpr size_t lds = Layout<MT, WC>::kLds;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)nvfp4_gemm_splitk_kernel<GEGLU>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess)
+            return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((nvfp4_gemm_splitk_kernel<GEGLU>), dim3(tiles * S), dim3(kThreads), lds,
+                       stream, a, part, S);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return e;
+    const size_t mn = (size_t)a.M * a.N;
+    const uint32_t grid = (uint32_t)std::min<size_t>((mn + 255) / 256, 256 * 8);
+    if (a.out_f32)
+        hipLaunchKernelGGL((splitk_reduce_kernel<GEGLU, true>), dim3(grid), dim3(256), 0, stream,
+                           part, S, a);
+    else
+        hipLaunchKernelGGL((splitk_reduce_kernel<GEGLU, false>), dim3(grid), dim3(256), 0, stream,
+                           part, S, a);
+    return hipGetLastError();
+}
+
 // One workgroup per row: optional RMS statistics, then hi / lo of every element.
 constexpr int kSplitThreads = 256;
 
@@ -157,6 +303,34 @@ hipError_t gemm_launch(const GemmArgs &a, hipStream_t stream) {
     if (a.geglu)
         return a.out_f32 ? launch_kernel<true, true>(a, stream) : launch_kernel<true, false>(a, stream);
     return a.out_f32 ? launch_kernel<false, true>(a, stream) : launch_kernel<false, false>(a, stream);
+}
+
+// Splits when the tiles fill under half the CUs: enough that tiles x S covers the 256
+// CUs, each split at least 8 stages, a multiple of the halves of A.
+uint32_t gemm_splitk_splits(const GemmArgs &a) {
+    const uint32_t tn = a.geglu ? kGegluCols : BN;
+    const uint32_t tiles = ((a.M + BM - 1) / BM) * ((a.N + tn - 1) / tn);
+    if (tiles >= 128 || a.K == 0 || a.a_k % a.K != 0)
+        return 1;
+    const uint32_t halves = a.a_k / a.K;
+    const uint32_t per_half = (a.K / BK) / 8;   // splits of >= 8 stages in a half
+    uint32_t s = std::min((256 + tiles - 1) / tiles, per_half * halves);
+    s -= s % halves;
+    return s >= 2 ? s : 1;
+}
+
+size_t gemm_splitk_bytes(const GemmArgs &a, uint32_t splits) {
+    return (size_t)splits * (a.geglu ? 2 : 1) * a.M * a.N * 4;
+}
+
+hipError_t gemm_splitk_launch(const GemmArgs &a, uint32_t splits, float *part,
+                              hipStream_t stream) {
+    if (!gemm_supported(a.M, a.N, a.K, a.a_k, a.out_f32) || splits < 1 ||
+        splits % (a.a_k / a.K) != 0 || splits / (a.a_k / a.K) > a.K / BK ||
+        (uint64_t)a.M * a.N * 4 >= (1ull << 31))
+        return hipErrorInvalidValue;
+    return a.geglu ? launch_splitk<true>(a, splits, part, stream)
+                   : launch_splitk<false>(a, splits, part, stream);
 }
 
 size_t gemm_split_bytes(uint32_t M, uint32_t K) { return (size_t)M * 2 * K * 2; }

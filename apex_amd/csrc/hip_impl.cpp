@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -86,51 +87,46 @@ uint32_t g_gemm_min_tokens[2] = {0, 0};
 constexpr uint64_t kFileChunk = 8ull << 20;
 constexpr uint32_t kFileBuffers = 8;
 
-void gemm_impl(const uint16_t *A, const uint32_t *codes, const uint8_t *scales, float ts,
-               uint16_t *C, uint32_t M, uint32_t N, uint32_t K, hipStream_t stream) {
-    check_nvfp4_shape(N, K);
-    if (M == 0 || N == 0)
+// The device's default stream-ordered memory pool keeps the blocks freed into it
+// (release threshold unlimited), so per-call scratch is reused instead of going back to
+// the driver at every synchronisation (measured: up to 50 us per call otherwise).
+// Once per device.
+void keep_pool_blocks() {
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
         return;
-    require(A && codes && scales && C, "null pointer");
-    require(apex_hip::gemm_supported(M, N, K, K, false),
-            "gemm: K must be a multiple of 64 and operands below 2 GiB");
-    init_device_tuning();
-    apex_hip::GemmArgs g{};
-    g.A = A;
-    g.codes[0] = g.codes[1] = codes;
-    g.scales[0] = g.scales[1] = scales;
-    g.tensor_scale[0] = g.tensor_scale[1] = ts;
-    g.C = C;
-    g.M = M;
-    g.N = N;
-    g.K = K;
-    g.ldc = N;
-    g.a_k = K;
-    hip_check(apex_hip::gemm_launch(g, stream), "gemm_nvfp4 launch");
+    const uint64_t bit = 1ull << dev;
+    if (done.load() & bit)
+        return;
+    hipMemPool_t pool;
+    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+        uint64_t threshold = UINT64_MAX;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
+    }
+    done.fetch_or(bit);
 }
 
-// Whether a dense product of `tokens` rows runs as an MFMA GEMM.  The GEMV streams W
-// once per block of up to 8 tokens; a GEMM tile runs K / 64 stages one after another,
-// so a grid of few tiles is bound by that chain (2112 x 2816: ~60 us bf16, ~120 us
-// fp32, whatever the token count up to 256).  Measured crossovers (gfx950): with at
-// least 64 tiles (21504 x 5376) the GEMM is faster from 16 tokens for GeGLU and from 32
-// for matmul; with fewer (2112 x 2816: 9 matmul / 17 GeGLU tiles) from 64 tokens for
-// GeGLU and from 128 for matmul.
-bool use_dense_gemm(uint32_t tokens, uint32_t rows, uint32_t K, bool bf16, bool geglu) {
-    if (!apex_hip::gemm_supported(tokens, rows, K, bf16 ? K : 2 * K, !bf16))
-        return false;
-    if (const uint32_t fixed = g_gemm_min_tokens[bf16 ? 0 : 1])
-        return tokens >= fixed;
-    const uint32_t cols = geglu ? 128 : 256;   // output columns of a tile
-    const uint64_t tiles = (uint64_t)((tokens + 255) / 256) * ((rows + cols - 1) / cols);
-    if (tiles >= 64)
-        return tokens >= (geglu ? 16u : 32u);
-    return tokens >= (geglu ? 64u : 128u);
-}
+// Device memory for one call, allocated and released in stream order (the release is
+// queued behind the kernels that use it).
+struct ScratchAsync {
+    void *p = nullptr;
+    hipStream_t s = nullptr;
+    void allocate(size_t bytes, hipStream_t stream, const char *what) {
+        keep_pool_blocks();
+        s = stream;
+        hip_check(hipMallocAsync(&p, bytes, stream), what);
+    }
+    ~ScratchAsync() {
+        if (p)
+            (void)hipFreeAsync(p, s);
+    }
+};
 
 // The MFMA GEMM for matmul (geglu false: W = c0/s0) or GeGLU (gate c0/s0, up c1/s1):
 // bf16 x directly; fp32 x (optionally RMS-normalised by norm_w first) through its
-// bf16 hi / lo split, held in a stream-ordered scratch allocation for the call.
+// bf16 hi / lo split, held in a stream-ordered scratch allocation for the call.  Grids
+// of few tiles run split-K (fp32 partials, likewise allocated for the call).
 void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, bool geglu,
                 const uint32_t *c0, const uint8_t *s0, float ts0, const uint32_t *c1,
                 const uint8_t *s1, float ts1, void *out, uint32_t M, uint32_t N, uint32_t K,
@@ -149,26 +145,56 @@ void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, boo
     g.ldc = N;
     g.geglu = geglu;
     g.out_f32 = !bf16;
+    ScratchAsync split, part;
     if (bf16) {
         g.A = static_cast<const uint16_t *>(x);
         g.a_k = K;
-        hip_check(apex_hip::gemm_launch(g, stream), "gemm_nvfp4 launch");
+    } else {
+        split.allocate(apex_hip::gemm_split_bytes(M, K), stream, "fp32 GEMM split buffer");
+        hip_check(apex_hip::gemm_split_launch(static_cast<const float *>(x), norm_w, eps,
+                                              static_cast<uint16_t *>(split.p), M, K, stream),
+                  "fp32 GEMM split launch");
+        g.A = static_cast<const uint16_t *>(split.p);
+        g.a_k = 2 * K;
+    }
+    const uint32_t splits = apex_hip::gemm_splitk_splits(g);
+    if (splits > 1) {
+        part.allocate(apex_hip::gemm_splitk_bytes(g, splits), stream, "split-K partials");
+        hip_check(apex_hip::gemm_splitk_launch(g, splits, static_cast<float *>(part.p), stream),
+                  "gemm_nvfp4 split-K launch");
         return;
     }
-    void *split = nullptr;
-    hip_check(hipMallocAsync(&split, apex_hip::gemm_split_bytes(M, K), stream),
-              "fp32 GEMM split buffer");
-    struct Release {
-        void *p;
-        hipStream_t s;
-        ~Release() { (void)hipFreeAsync(p, s); }
-    } release{split, stream};
-    hip_check(apex_hip::gemm_split_launch(static_cast<const float *>(x), norm_w, eps,
-                                          static_cast<uint16_t *>(split), M, K, stream),
-              "fp32 GEMM split launch");
-    g.A = static_cast<const uint16_t *>(split);
-    g.a_k = 2 * K;
     hip_check(apex_hip::gemm_launch(g, stream), "gemm_nvfp4 launch");
+}
+
+void gemm_impl(const uint16_t *A, const uint32_t *codes, const uint8_t *scales, float ts,
+               uint16_t *C, uint32_t M, uint32_t N, uint32_t K, hipStream_t stream) {
+    check_nvfp4_shape(N, K);
+    if (M == 0 || N == 0)
+        return;
+    require(A && codes && scales && C, "null pointer");
+    require(apex_hip::gemm_supported(M, N, K, K, false),
+            "gemm: K must be a multiple of 64 and operands below 2 GiB");
+    init_device_tuning();
+    dense_gemm(A, true, nullptr, 0.0f, false, codes, scales, ts, nullptr, nullptr, 1.0f, C, M, N, K,
+               stream);
+}
+
+// Whether a dense product of `tokens` rows runs as an MFMA GEMM.  The GEMV streams W
+// once per block of up to 8 tokens; the GEMM's cost is set by its tiles (grids of few
+// tiles run split-K).  Measured crossovers (gfx950, split-K in place): with at least 64
+// tiles (21504 x 5376) the GEMM is faster from 16 tokens; with fewer (2112 x 2816: 9
+// matmul / 17 GeGLU tiles) from 32 tokens for GeGLU and 64 for matmul.
+bool use_dense_gemm(uint32_t tokens, uint32_t rows, uint32_t K, bool bf16, bool geglu) {
+    if (!apex_hip::gemm_supported(tokens, rows, K, bf16 ? K : 2 * K, !bf16))
+        return false;
+    if (const uint32_t fixed = g_gemm_min_tokens[bf16 ? 0 : 1])
+        return tokens >= fixed;
+    const uint32_t cols = geglu ? 128 : 256;   // output columns of a tile
+    const uint64_t tiles = (uint64_t)((tokens + 255) / 256) * ((rows + cols - 1) / cols);
+    if (tiles >= 64)
+        return tokens >= 16;
+    return tokens >= (geglu ? 32u : 64u);
 }
 
 void matmul_impl(const void *x, bool bf16, const uint32_t *codes, const uint8_t *scales,

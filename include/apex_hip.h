@@ -294,9 +294,11 @@ int apex_hip_set_gemv_waves_per_cu(int waves);
 
 /* Tokens from which apex_nvfp4_matmul_* and apex_nvfp4_geglu_* (and their registry
  * kernels) run as MFMA GEMMs instead of GEMVs, for bf16 and for fp32 activations
- * (0 = by size, the default: GeGLU from 16 tokens and matmul from 32 when the GEMM has
- * at least 64 tiles of 256 tokens x 128 (GeGLU) or 256 (matmul) outputs, else from 64
- * and 128).  Process-wide; results agree within the stated tolerances either way. */
+ * (0 = by size, the default: from 16 tokens when the GEMM has at least 64 tiles of 256
+ * tokens x 128 (GeGLU) or 256 (matmul) outputs, else GeGLU from 32 and matmul from 64).
+ * Process-wide; results agree within the stated tolerances either way.  The GEMMs'
+ * per-call scratch (fp32 split, split-K partials) comes from the device's default
+ * stream-ordered memory pool, whose freed blocks the library keeps for reuse. */
 int apex_hip_set_gemm_min_tokens(uint32_t bf16_tokens, uint32_t f32_tokens);
 
 /* ---- MoE expert FFN (no reference kernel) ------------------------------------------

@@ -217,3 +217,26 @@ def test_geglu_rms_norm_gemm_matches_oracle(gemm_threshold):
     assert rel_l2(got[:, ids], want) < TOL_REF_GATE
     hip.set_gemm_min_tokens(0, 1 << 20)
     assert rel_l2(run_geglu(x, g, u, True, norm=(nw, eps)), got) < TOL_REF_GATE
+
+
+@pytest.mark.parametrize("M,N,K", [(200, 301, 2048), (37, 64, 1024)])
+def test_split_k_one_hot_exact(M, N, K, gemm_threshold):
+    """Grids of few tiles run split-K: each workgroup sums a range of K stages into fp32
+    partials and a second pass adds them in split order.  One-hot rows put each output's
+    single product in one split (zeros in the others), so the bf16 GEMM and the fp32
+    split GEMM (hi / lo halves in separate splits) return W[n, p(m)] exactly; random
+    rows match the oracle."""
+    rng = np.random.default_rng(M * N)
+    w = synth.nvfp4_weights(rng, N, K)
+    perm = rng.integers(0, K, size=M)
+    X = np.zeros((M, K), np.float32)
+    X[np.arange(M), perm] = 1.0
+    want = oracle.decode(w.codes, w.scales)[:, perm].T + np.float32(0.0)
+    got_b = bf16(gemm(synth.bf16_from_f32(X), w))
+    assert np.array_equal(got_b.view(np.uint32), want.view(np.uint32))
+    got_f = run_matmul_f32(X, w)
+    assert np.array_equal(got_f.view(np.uint32), want.view(np.uint32))
+    A = synth.normal_bf16(rng, (M, K))
+    assert rel_l2(bf16(gemm(A, w)), oracle.matvec(w.codes, w.scales, bf16(A))) < TOL_BF16
+    Xr = rng.standard_normal((M, K)).astype(np.float32)
+    assert rel_l2(run_matmul_f32(Xr, w), oracle.matvec(w.codes, w.scales, Xr)) < TOL_REF_GATE
