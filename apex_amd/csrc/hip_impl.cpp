@@ -5,7 +5,8 @@
 
 #include <hip/hip_runtime.h>
 
-#include <atomic>
+#include <map>
+#include <mutex>
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -87,46 +88,42 @@ uint32_t g_gemm_min_tokens[2] = {0, 0};
 constexpr uint64_t kFileChunk = 8ull << 20;
 constexpr uint32_t kFileBuffers = 8;
 
-// The device's default stream-ordered memory pool keeps the blocks freed into it
-// (release threshold unlimited), so per-call scratch is reused instead of going back to
-// the driver at every synchronisation (measured: up to 50 us per call otherwise).
-// Once per device.
-void keep_pool_blocks() {
-    static std::atomic<uint64_t> done{0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-        return;
-    const uint64_t bit = 1ull << dev;
-    if (done.load() & bit)
-        return;
-    hipMemPool_t pool;
-    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-        uint64_t threshold = UINT64_MAX;
-        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
-    }
-    done.fetch_or(bit);
-}
-
-// Device memory for one call, allocated and released in stream order (the release is
-// queued behind the kernels that use it).
-struct ScratchAsync {
-    void *p = nullptr;
-    hipStream_t s = nullptr;
-    void allocate(size_t bytes, hipStream_t stream, const char *what) {
-        keep_pool_blocks();
-        s = stream;
-        hip_check(hipMallocAsync(&p, bytes, stream), what);
-    }
-    ~ScratchAsync() {
-        if (p)
-            (void)hipFreeAsync(p, s);
-    }
+// Per-call scratch of the dense GEMMs (slot 0: the fp32 split, slot 1: split-K
+// partials), kept per (device, stream) and grown on demand.  Calls on one stream run in
+// order, so reusing that stream's buffers needs no synchronisation; growing waits for
+// the stream, frees the old buffer and allocates the new one.  Held until the process
+// ends.  (Stream-ordered hipMallocAsync / hipFreeAsync per call measured 40-330 us of
+// host time per call once two sizes alternate.)
+struct StreamScratch {
+    void *p[2] = {nullptr, nullptr};
+    size_t bytes[2] = {0, 0};
 };
+std::mutex g_scratch_mu;
+std::map<std::pair<int, hipStream_t>, StreamScratch> g_scratch;
+
+void *stream_scratch(int slot, size_t bytes, hipStream_t stream) {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    StreamScratch &e = g_scratch[{dev, stream}];
+    if (e.bytes[slot] < bytes) {
+        if (e.p[slot]) {
+            hip_check(hipStreamSynchronize(stream), "scratch resize: stream sync");
+            hip_check(hipFree(e.p[slot]), "scratch resize: free");
+            e.p[slot] = nullptr;
+            e.bytes[slot] = 0;
+        }
+        const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+        hip_check(hipMalloc(&e.p[slot], want), "GEMM scratch allocation");
+        e.bytes[slot] = want;
+    }
+    return e.p[slot];
+}
 
 // The MFMA GEMM for matmul (geglu false: W = c0/s0) or GeGLU (gate c0/s0, up c1/s1):
 // bf16 x directly; fp32 x (optionally RMS-normalised by norm_w first) through its
-// bf16 hi / lo split, held in a stream-ordered scratch allocation for the call.  Grids
-// of few tiles run split-K (fp32 partials, likewise allocated for the call).
+// bf16 hi / lo split, held in the stream's scratch.  Grids of few tiles run split-K
+// (fp32 partials, likewise in the stream's scratch).
 void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, bool geglu,
                 const uint32_t *c0, const uint8_t *s0, float ts0, const uint32_t *c1,
                 const uint8_t *s1, float ts1, void *out, uint32_t M, uint32_t N, uint32_t K,
@@ -145,22 +142,23 @@ void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, boo
     g.ldc = N;
     g.geglu = geglu;
     g.out_f32 = !bf16;
-    ScratchAsync split, part;
     if (bf16) {
         g.A = static_cast<const uint16_t *>(x);
         g.a_k = K;
     } else {
-        split.allocate(apex_hip::gemm_split_bytes(M, K), stream, "fp32 GEMM split buffer");
-        hip_check(apex_hip::gemm_split_launch(static_cast<const float *>(x), norm_w, eps,
-                                              static_cast<uint16_t *>(split.p), M, K, stream),
+        auto *split = static_cast<uint16_t *>(
+            stream_scratch(0, apex_hip::gemm_split_bytes(M, K), stream));
+        hip_check(apex_hip::gemm_split_launch(static_cast<const float *>(x), norm_w, eps, split,
+                                              M, K, stream),
                   "fp32 GEMM split launch");
-        g.A = static_cast<const uint16_t *>(split.p);
+        g.A = split;
         g.a_k = 2 * K;
     }
     const uint32_t splits = apex_hip::gemm_splitk_splits(g);
     if (splits > 1) {
-        part.allocate(apex_hip::gemm_splitk_bytes(g, splits), stream, "split-K partials");
-        hip_check(apex_hip::gemm_splitk_launch(g, splits, static_cast<float *>(part.p), stream),
+        auto *part = static_cast<float *>(
+            stream_scratch(1, apex_hip::gemm_splitk_bytes(g, splits), stream));
+        hip_check(apex_hip::gemm_splitk_launch(g, splits, part, stream),
                   "gemm_nvfp4 split-K launch");
         return;
     }
@@ -182,19 +180,19 @@ void gemm_impl(const uint16_t *A, const uint32_t *codes, const uint8_t *scales, 
 
 // Whether a dense product of `tokens` rows runs as an MFMA GEMM.  The GEMV streams W
 // once per block of up to 8 tokens; the GEMM's cost is set by its tiles (grids of few
-// tiles run split-K).  Measured crossovers (gfx950, split-K in place): with at least 64
-// tiles (21504 x 5376) the GEMM is faster from 16 tokens; with fewer (2112 x 2816: 9
-// matmul / 17 GeGLU tiles) from 32 tokens for GeGLU and 64 for matmul.
+// tiles run split-K).  Measured crossovers (gfx950, split-K in place): GeGLU from 16
+// tokens (2112 x 2816 bf16: 21.5 vs 22.4 us at 16, 39.6 vs 23.4 at 32); matmul from 16
+// with at least 64 tiles (21504 x 5376: 106 vs 75 us) and from 32 with fewer
+// (2112 x 2816: 14.1 vs 21.7 us at 16, 24.5 vs 21.8 at 32).
 bool use_dense_gemm(uint32_t tokens, uint32_t rows, uint32_t K, bool bf16, bool geglu) {
     if (!apex_hip::gemm_supported(tokens, rows, K, bf16 ? K : 2 * K, !bf16))
         return false;
     if (const uint32_t fixed = g_gemm_min_tokens[bf16 ? 0 : 1])
         return tokens >= fixed;
-    const uint32_t cols = geglu ? 128 : 256;   // output columns of a tile
-    const uint64_t tiles = (uint64_t)((tokens + 255) / 256) * ((rows + cols - 1) / cols);
-    if (tiles >= 64)
+    if (geglu)
         return tokens >= 16;
-    return tokens >= (geglu ? 32u : 64u);
+    const uint64_t tiles = (uint64_t)((tokens + 255) / 256) * ((rows + 255) / 256);
+    return tokens >= (tiles >= 64 ? 16u : 32u);
 }
 
 void matmul_impl(const void *x, bool bf16, const uint32_t *codes, const uint8_t *scales,

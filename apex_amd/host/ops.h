@@ -84,8 +84,9 @@ inline void denseMlp(Backend &backend, Buffer *input, const Nvfp4Matrix &gate_we
 
 // ---- additional ops of the HIP backend ------------------------------------------------
 
-// bf16 [tokens, hidden_dim] -> bf16 [tokens, w_rows], fp32 accumulation.  From 64
-// tokens it runs as the MFMA GEMM, below as the bandwidth-bound GEMV.
+// bf16 [tokens, hidden_dim] -> bf16 [tokens, w_rows], fp32 accumulation.  Few tokens
+// run as the bandwidth-bound GEMV, more as the MFMA GEMM (apex_hip_set_gemm_min_tokens);
+// matmulNvfp4 and gegluNvfp4 switch the same way.
 inline void matmulNvfp4Bf16(Backend &backend, Buffer *input, const Nvfp4Matrix &W, Buffer *output,
                             uint32_t tokens, float tensor_scale = 1.0f) {
     backend.run("matmul_nvfp4_bf16",

@@ -271,7 +271,35 @@ def time_dense_prefill(steps, warmup, T=2048, N=21504, K=5376):
     stream.close()
     for a in dw + [xb, xf, hb, yf]:
         a.close()
+    out["dense_mlp_prefill_f32"] = time_dense_mlp_prefill(steps, warmup)
     return out
+
+
+def time_dense_mlp_prefill(steps, warmup, T=512, H=2816, I=2112):
+    """The Gemma dense MLP block at prefill, fp32 (the reference contract): RMSNorm
+    folded into the fused GeGLU GEMM's split pass, then the down GEMM (split-K: this
+    shape has few tiles).  FLOPs 2 T (2 I H + H I)."""
+    h, nw, g, u, d = synth.dense_mlp_case(seed=0, tokens=T, H=H, I=I)
+    arrs = [hip.DeviceArray.from_numpy(a) for a in (h, nw, g.codes, g.scales, u.codes, u.scales,
+                                                    d.codes, d.scales)]
+    dh, dnw, gc, gs, uc, us, dc, ds = arrs
+    hh, y = hip.DeviceArray((T, I), np.float32), hip.DeviceArray((T, H), np.float32)
+    stream = hip.Stream()
+
+    def step(i):
+        hip.nvfp4_geglu_rms_norm_f32(dh, dnw, 1e-6, gc, gs, uc, us, hh, T, I, H, stream=stream)
+        hip.nvfp4_matmul_f32(hh, dc, ds, y, T, H, I, stream=stream)
+
+    sec = time_steps(step, steps, warmup, stream)
+    stream.close()
+    for a in arrs + [hh, y]:
+        a.close()
+    flops = 2.0 * T * (2 * I * H + H * I)
+    tf = flops / sec / 1e12
+    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
+            "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(flops),
+            "workload": f"dense MLP prefill, fp32: {T} tokens, RMSNorm [{H}] fused into GeGLU "
+                        f"NVFP4 [{I}x{H}] x2, down NVFP4 [{H}x{I}] (GEMMs: split pass, split-K)"}
 
 
 def time_norms(steps, warmup, T=4096, H=2816, heads=16, D=256):

@@ -167,6 +167,37 @@ void test_dense_mlp(HipBackend &be) {
         be.release(b);
 }
 
+// The reference-named launches at a prefill token count, where matmul_nvfp4 and the
+// fused GeGLU run as MFMA GEMMs (fp32 x through its bf16 hi + lo split; split-K for
+// these few tiles): the same reference gate as the decode sizes.
+void test_dense_prefill(HipBackend &be) {
+    Rng rng{11};
+    const uint32_t H = 1024, I = 512, T = 128;
+    HostMatrix g = random_matrix(rng, I, H), u = random_matrix(rng, I, H), d = random_matrix(rng, H, I);
+    std::vector<float> x((size_t)T * H);
+    for (auto &v : x)
+        v = rng.normal();
+    std::vector<float> want((size_t)T * H);
+    orc_dense_mlp(g.codes.data(), g.scales.data(), u.codes.data(), u.scales.data(), d.codes.data(),
+                  d.scales.data(), x.data(), want.data(), T, H, I);
+    DevMatrix dg = upload_matrix(be, g), du = upload_matrix(be, u), dd = upload_matrix(be, d);
+    Buffer *in = upload(be, x.data(), x.size() * 4, "activations");
+    Buffer *gate_tmp = be.allocate((size_t)T * I * 4, "scratch");
+    Buffer *up_tmp = be.allocate((size_t)T * I * 4, "scratch");
+    Buffer *out = be.allocate((size_t)T * H * 4, "scratch");
+    denseMlp(be, in, dg.m, du.m, dd.m, gate_tmp, up_tmp, out, T);
+    be.sync();
+    double r = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
+    report("denseMlp fp32 at 128 tokens (GEMMs) vs oracle", r < 1e-5, "rel_l2 " + std::to_string(r));
+    denseMlpFused(be, in, dg.m, du.m, dd.m, gate_tmp, out, T);
+    be.sync();
+    r = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
+    report("denseMlpFused fp32 at 128 tokens (GEMMs) vs oracle", r < 1e-5,
+           "rel_l2 " + std::to_string(r));
+    for (Buffer *b : {dg.buf, du.buf, dd.buf, in, gate_tmp, up_tmp, out})
+        be.release(b);
+}
+
 void test_bf16_ops(HipBackend &be) {
     Rng rng{2};
     const uint32_t K = 1024, N = 384;
@@ -469,6 +500,7 @@ int main(int argc, char **argv) {
     HipBackend be(0);
     std::printf("device: %s\n", be.deviceName());
     test_dense_mlp(be);
+    test_dense_prefill(be);
     test_bf16_ops(be);
     test_moe(be);
     test_norms(be);
