@@ -27,6 +27,12 @@ __device__ __forceinline__ float bf16_weight(const uint16_t *w, uint32_t i) {
     return bf16_bits_to_f32(w[i]);
 }
 
+// Rows of up to 256 * kRegQuads * 4 elements (16-byte aligned) stay in registers
+// between the sum of squares and the scaling, and the weight loads are issued with the
+// row's: one pass over HBM with every load in flight before the reduction.  The
+// per-thread sums run in the same order as the two-pass loop, so results are identical.
+constexpr int kRegQuads = 4;
+
 __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormArgs a) {
     __shared__ float part[4];
     const uint32_t row = blockIdx.x;
@@ -35,6 +41,42 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormArgs a) {
     const uint32_t n = a.n, tid = threadIdx.x;
     const bool vec = n % 4 == 0 && ((uintptr_t)x | (uintptr_t)y) % 16 == 0 && (uintptr_t)a.w % 8 == 0;
     float ss = 0.0f;
+    if (vec && n / 4 <= 256u * kRegQuads) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        const uint2 *w4 = reinterpret_cast<const uint2 *>(a.w);
+        float4 v[kRegQuads];
+        uint2 wb[kRegQuads];
+#pragma unroll
+        for (int r = 0; r < kRegQuads; ++r) {
+            const uint32_t i = tid + 256 * r;
+            const bool ok = i < n / 4;
+            v[r] = ok ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            wb[r] = ok ? w4[i] : make_uint2(0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < kRegQuads; ++r)
+            ss += v[r].x * v[r].x + v[r].y * v[r].y + v[r].z * v[r].z + v[r].w * v[r].w;
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0)
+            part[tid >> 6] = ss;
+        __syncthreads();
+        const float total = part[0] + part[1] + part[2] + part[3];
+        const float inv = 1.0f / sqrtf(total / (float)n + a.eps);
+        float4 *y4 = reinterpret_cast<float4 *>(y);
+#pragma unroll
+        for (int r = 0; r < kRegQuads; ++r) {
+            const uint32_t i = tid + 256 * r;
+            if (i < n / 4) {
+                float4 o;
+                o.x = v[r].x * inv * __uint_as_float(wb[r].x << 16);
+                o.y = v[r].y * inv * __uint_as_float(wb[r].x & 0xFFFF0000u);
+                o.z = v[r].z * inv * __uint_as_float(wb[r].y << 16);
+                o.w = v[r].w * inv * __uint_as_float(wb[r].y & 0xFFFF0000u);
+                y4[i] = o;
+            }
+        }
+        return;
+    }
     if (vec) {
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
         for (uint32_t i = tid; i < n / 4; i += 256) {
