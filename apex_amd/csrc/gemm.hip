@@ -249,42 +249,101 @@ template <bool GEGLU> hipError_t launch_splitk(const GemmArgs &a, uint32_t S, fl
     return hipGetLastError();
 }
 
-// One workgroup per row: optional RMS statistics, then hi / lo of every element.
+// One workgroup per row: optional RMS statistics, then hi / lo of every element.  Rows
+// of up to 256 * kSplitQuads * 4 elements (16-byte aligned x, 8-byte aligned norm_w)
+// stay in registers, read with 16-byte loads and written as 8-byte pieces of 4 bf16;
+// other rows take the element loop.
 constexpr int kSplitThreads = 256;
+constexpr int kSplitQuads = 8;
 
 __device__ __forceinline__ uint16_t bf16_rne(float x) { return f32_to_bf16_bits(x); }
+
+// hi / lo of one value (lo = 0 where hi is not finite)
+__device__ __forceinline__ void split_one(float v, uint16_t &h, uint16_t &l) {
+    h = bf16_rne(v);
+    const float hf = __uint_as_float((uint32_t)h << 16);
+    l = __builtin_isfinite(hf) ? bf16_rne(v - hf) : (uint16_t)0;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = group_sum<64>(v);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSplitThreads / 64; ++w)
+        total += red[w];
+    return total;
+}
 
 __global__ __launch_bounds__(kSplitThreads) void split_bf16_kernel(const float *X,
                                                                    const uint16_t *norm_w,
                                                                    float eps, uint16_t *out,
                                                                    uint32_t K) {
+    __shared__ float red[kSplitThreads / 64];
     const float *x = X + (size_t)blockIdx.x * K;
     uint16_t *hi = out + (size_t)blockIdx.x * 2 * K;
     uint16_t *lo = hi + K;
+    const uint32_t tid = threadIdx.x;
+    const bool vec = K % 4 == 0 && K / 4 <= kSplitThreads * kSplitQuads &&
+                     (uintptr_t)x % 16 == 0 && (uintptr_t)hi % 8 == 0 &&
+                     (!norm_w || (uintptr_t)norm_w % 8 == 0);
+    if (vec) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        const uint2 *w4 = reinterpret_cast<const uint2 *>(norm_w);
+        float4 v[kSplitQuads];
+        uint2 wb[kSplitQuads];
+#pragma unroll
+        for (int r = 0; r < kSplitQuads; ++r) {
+            const uint32_t i = tid + kSplitThreads * r;
+            const bool ok = i < K / 4;
+            v[r] = ok ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            wb[r] = ok && norm_w ? w4[i] : make_uint2(0, 0);
+        }
+        if (norm_w) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int r = 0; r < kSplitQuads; ++r)
+                ss += v[r].x * v[r].x + v[r].y * v[r].y + v[r].z * v[r].z + v[r].w * v[r].w;
+            const float inv = 1.0f / sqrtf(block_sum(ss, red) / (float)K + eps);
+#pragma unroll
+            for (int r = 0; r < kSplitQuads; ++r) {
+                v[r].x = v[r].x * inv * __uint_as_float(wb[r].x << 16);
+                v[r].y = v[r].y * inv * __uint_as_float(wb[r].x & 0xFFFF0000u);
+                v[r].z = v[r].z * inv * __uint_as_float(wb[r].y << 16);
+                v[r].w = v[r].w * inv * __uint_as_float(wb[r].y & 0xFFFF0000u);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kSplitQuads; ++r) {
+            const uint32_t i = tid + kSplitThreads * r;
+            if (i >= K / 4)
+                continue;
+            uint16_t h[4], l[4];
+            split_one(v[r].x, h[0], l[0]);
+            split_one(v[r].y, h[1], l[1]);
+            split_one(v[r].z, h[2], l[2]);
+            split_one(v[r].w, h[3], l[3]);
+            reinterpret_cast<uint2 *>(hi)[i] =
+                make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
+            reinterpret_cast<uint2 *>(lo)[i] =
+                make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16);
+        }
+        return;
+    }
     float inv = 1.0f;
     if (norm_w) {
-        __shared__ float red[kSplitThreads / 64];
         float ss = 0.0f;
-        for (uint32_t k = threadIdx.x; k < K; k += kSplitThreads)
+        for (uint32_t k = tid; k < K; k += kSplitThreads)
             ss += x[k] * x[k];
-        ss = group_sum<64>(ss);
-        if ((threadIdx.x & 63) == 0)
-            red[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        float total = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kSplitThreads / 64; ++w)
-            total += red[w];
-        inv = 1.0f / sqrtf(total / (float)K + eps);
+        inv = 1.0f / sqrtf(block_sum(ss, red) / (float)K + eps);
     }
-    for (uint32_t k = threadIdx.x; k < K; k += kSplitThreads) {
+    for (uint32_t k = tid; k < K; k += kSplitThreads) {
         float v = x[k];
         if (norm_w)
             v = v * inv * __uint_as_float((uint32_t)norm_w[k] << 16);
-        const uint16_t h = bf16_rne(v);
-        const float hf = __uint_as_float((uint32_t)h << 16);
-        hi[k] = h;
-        lo[k] = __builtin_isfinite(hf) ? bf16_rne(v - hf) : (uint16_t)0;
+        split_one(v, hi[k], lo[k]);
     }
 }
 
