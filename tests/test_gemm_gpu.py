@@ -240,3 +240,21 @@ def test_split_k_one_hot_exact(M, N, K, gemm_threshold):
     assert rel_l2(bf16(gemm(A, w)), oracle.matvec(w.codes, w.scales, bf16(A))) < TOL_BF16
     Xr = rng.standard_normal((M, K)).astype(np.float32)
     assert rel_l2(run_matmul_f32(Xr, w), oracle.matvec(w.codes, w.scales, Xr)) < TOL_REF_GATE
+
+
+def test_split_pass_long_rows_and_tensor_scales(gemm_threshold):
+    """fp32 rows longer than the split pass keeps in registers (K = 8256) take its
+    element loop, with and without the RMSNorm folded in; GeGLU tensor scales and the
+    matmul tensor scale apply on the split path as on the GEMV."""
+    rng = np.random.default_rng(31)
+    T, rows, K, eps = 40, 96, 8256, 1e-6
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    nw = synth.bf16_from_f32((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    g, u = synth.nvfp4_weights(rng, rows, K), synth.nvfp4_weights(rng, rows, K)
+    want = oracle.geglu(oracle.matvec(g.codes, g.scales, x, 0.25),
+                        oracle.matvec(u.codes, u.scales, x, 4.0))
+    assert rel_l2(run_geglu(x, g, u, True, 0.25, 4.0), want) < TOL_REF_GATE
+    xn = oracle.rms_norm(x, nw, eps)
+    want_n = oracle.geglu(oracle.matvec(g.codes, g.scales, xn), oracle.matvec(u.codes, u.scales, xn))
+    assert rel_l2(run_geglu(x, g, u, True, norm=(nw, eps)), want_n) < TOL_REF_GATE
+    assert rel_l2(run_matmul_f32(x, g, 2.0), oracle.matvec(g.codes, g.scales, x, 2.0)) < TOL_REF_GATE
