@@ -24,6 +24,7 @@
 // buffer descriptors: rows past M or N read zeros; stores are guarded.
 #include "gemm.h"
 #include "gemm_core.h"
+#include "lds_attr.h"
 
 #include <algorithm>
 
@@ -93,14 +94,9 @@ template <bool GEGLU, bool F32> hipError_t launch_kernel(const GemmArgs &a, hipS
     const uint32_t tiles = ((a.M + BM - 1) / BM) * ((a.N + TN - 1) / TN);
     const uint32_t grid = 8 * ((tiles + 7) / 8);
     constexpr size_t lds = Layout<MT, WC>::kLds;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)nvfp4_gemm_kernel<GEGLU, F32>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess)
-            return e;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> attr_set{0};
+    if (hipError_t e = allow_dynamic_lds(nvfp4_gemm_kernel<GEGLU, F32>, lds, attr_set); e != hipSuccess)
+        return e;
     hipLaunchKernelGGL((nvfp4_gemm_kernel<GEGLU, F32>), dim3(grid), dim3(kThreads), lds, stream, a);
     return hipGetLastError();
 }
@@ -225,14 +221,9 @@ template <bool GEGLU> hipError_t launch_splitk(const GemmArgs &a, uint32_t S, fl
     constexpr uint32_t TN = GEGLU ? kGegluCols : BN;
     const uint32_t tiles = ((a.M + BM - 1) / BM) * ((a.N + TN - 1) / TN);
     constexpr size_t lds = Layout<MT, WC>::kLds;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)nvfp4_gemm_splitk_kernel<GEGLU>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess)
-            return e;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> attr_set{0};
+    if (hipError_t e = allow_dynamic_lds(nvfp4_gemm_splitk_kernel<GEGLU>, lds, attr_set); e != hipSuccess)
+        return e;
     hipLaunchKernelGGL((nvfp4_gemm_splitk_kernel<GEGLU>), dim3(tiles * S), dim3(kThreads), lds,
                        stream, a, part, S);
     hipError_t e = hipGetLastError();

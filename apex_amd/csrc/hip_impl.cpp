@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <cstdio>
@@ -49,8 +50,8 @@ template <class F> int guard(F &&f) {
 
 // CU count of the current device, read once per process for launch sizing.
 void init_device_tuning() {
-    static bool done = false;
-    if (done)
+    static std::atomic<bool> done{false};
+    if (done.load())
         return;
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) == hipSuccess &&

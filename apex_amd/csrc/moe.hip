@@ -41,6 +41,7 @@
 
 #include "gemm_core.h"
 #include "gemv_kernels.h"
+#include "lds_attr.h"
 #include "moe.h"
 
 namespace apex_hip {
@@ -1345,14 +1346,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
     *reinterpret_cast<u32x4_t *>(a.y + (size_t)t * H + c) = o;
 }
 
-template <typename F> hipError_t set_lds(F *kernel, size_t bytes, bool &done) {
-    if (done)
-        return hipSuccess;
-    const hipError_t e =
-        hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-    if (e == hipSuccess)
-        done = true;
-    return e;
+template <typename F> hipError_t set_lds(F *kernel, size_t bytes, std::atomic<uint64_t> &done) {
+    return allow_dynamic_lds(kernel, bytes, done);
 }
 
 uint32_t gemv_slots(uint32_t K, int G) { return (K / 32 + G - 1) / G; }
@@ -1455,7 +1450,7 @@ bool moe_router_supported(const MoeRouterArgs &a, const char **why) {
 
 template <int TT, int EPL, int WAVES>
 hipError_t router_launch(const MoeRouterArgs &a, hipStream_t stream) {
-    static bool set = false;
+    static std::atomic<uint64_t> set{0};
     const size_t lds = router_lds<TT, WAVES>(a);
     hipError_t e = set_lds(moe_router_kernel<TT, EPL, WAVES>, lds, set);
     if (e != hipSuccess)
@@ -1516,7 +1511,7 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
         // CU), else read per token from global memory
         const uint32_t xbytes = a.T * (a.H / 32 + 1) * 64;
         if (xbytes <= kXLdsBytes) {
-            static bool attr[3] = {};
+            static std::atomic<uint64_t> attr[3] = {};
             const dim3 lgrid((uint32_t)kNumCUs), lblock(kXLdsThreads);
             hipError_t err = hipSuccess;
             switch (gemv_slots(a.H, 32)) {
@@ -1550,7 +1545,7 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
                            dim3(256), 0, stream, a);
         return hipGetLastError();
     }
-    static bool lds_gateup = false, lds_down = false;
+    static std::atomic<uint64_t> lds_gateup{0}, lds_down{0};
     hipError_t err = set_lds(moe_gateup_gemm_kernel, kMaxLds, lds_gateup);
     if (err == hipSuccess)
         err = set_lds(moe_down_gemm_kernel, kDownLds, lds_down);
