@@ -500,8 +500,8 @@ def main(argv=None):
                     help="profiling aid: time one secondary workload and print its record only")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path to time; run with "
+              "--gpus 1", file=sys.stderr)
         return 2
 
     if args.calibrate:

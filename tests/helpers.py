@@ -5,7 +5,7 @@ import numpy as np
 
 from apex_amd import synth
 
-# north-star tolerances (rel L2, src/tests/cpu_ref.h:27-46 metric) against the fp64 oracle
+# parity tolerances (rel L2, src/tests/cpu_ref.h:27-46 metric) against the fp64 oracle
 TOL_F32 = 1e-3
 TOL_BF16 = 1e-2
 # the reference's own parity gate for fp32 outputs (src/tests/dense_mlp.cpp:113)
