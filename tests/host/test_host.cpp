@@ -203,7 +203,9 @@ void test_bf16_ops(HipBackend &be) {
     const uint32_t K = 1024, N = 384;
     HostMatrix w = random_matrix(rng, N, K);
     DevMatrix dw = upload_matrix(be, w);
-    for (uint32_t T : {1u, 5u, 96u}) { // GEMV below 64 tokens, MFMA GEMM from 64
+    HostMatrix u = random_matrix(rng, N, K);
+    DevMatrix du = upload_matrix(be, u);
+    for (uint32_t T : {1u, 5u, 96u}) { // GEMV for few tokens, MFMA GEMM for 96
         std::vector<uint16_t> xb((size_t)T * K);
         std::vector<float> xf((size_t)T * K);
         for (size_t i = 0; i < xb.size(); ++i) {
@@ -216,16 +218,28 @@ void test_bf16_ops(HipBackend &be) {
         Buffer *out = be.allocate((size_t)T * N * 2, "scratch");
         matmulNvfp4Bf16(be, in, dw.m, out, T);
         be.sync();
-        const auto *ob = static_cast<const uint16_t *>(be.contents(out));
+        const uint16_t *ob = static_cast<const uint16_t *>(be.contents(out));
         std::vector<float> got((size_t)T * N);
         for (size_t i = 0; i < got.size(); ++i)
             got[i] = from_bf16(ob[i]);
         const double r = rel_l2(got.data(), want.data(), want.size());
         report("matmulNvfp4Bf16 T=" + std::to_string(T), r < 1e-2, "rel_l2 " + std::to_string(r));
+        // fused GeGLU through the registry (gate = w, up = u), bf16 in and out
+        std::vector<float> upv((size_t)T * N);
+        orc_matvec_nvfp4(u.codes.data(), u.scales.data(), xf.data(), upv.data(), T, N, K, 1.0f);
+        orc_geglu(want.data(), upv.data(), want.data(), want.size());
+        gegluNvfp4(be, in, dw.m, du.m, out, T, /*bf16=*/true);
+        be.sync();
+        ob = static_cast<const uint16_t *>(be.contents(out));
+        for (size_t i = 0; i < got.size(); ++i)
+            got[i] = from_bf16(ob[i]);
+        const double rg = rel_l2(got.data(), want.data(), want.size());
+        report("gegluNvfp4 bf16 T=" + std::to_string(T), rg < 1e-2, "rel_l2 " + std::to_string(rg));
         be.release(in);
         be.release(out);
     }
     be.release(dw.buf);
+    be.release(du.buf);
 }
 
 void test_moe(HipBackend &be) {
