@@ -7,6 +7,7 @@
 
 #include <atomic>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <cstdio>
 #include <cstring>
@@ -89,42 +90,80 @@ uint32_t g_gemm_min_tokens[2] = {0, 0};
 constexpr uint64_t kFileChunk = 8ull << 20;
 constexpr uint32_t kFileBuffers = 8;
 
-// Per-call scratch of the dense GEMMs (slot 0: the fp32 split, slot 1: split-K
-// partials), kept per (device, stream) and grown on demand.  Calls on one stream run in
-// order, so reusing that stream's buffers needs no synchronisation; growing waits for
-// the stream, frees the old buffer and allocates the new one.  Held until the process
-// ends.  (Stream-ordered hipMallocAsync / hipFreeAsync per call measured 40-330 us of
-// host time per call once two sizes alternate.)
-struct StreamScratch {
+// Scratch of the dense GEMMs (slot 0: the fp32 split, slot 1: split-K partials), one
+// set per device, grown on demand and held until the process ends.  A call holds the
+// device's lease while it enqueues the kernels that use the scratch; at the end it
+// records an event on its stream, and a later call on another stream makes its stream
+// wait for that event first (on the GPU, no host synchronisation), so uses from any
+// streams and threads run one after another.  Growing waits for the last user's
+// stream, frees the old buffer and allocates the new one.  (Stream-ordered
+// hipMallocAsync / hipFreeAsync per call measured 40-330 us of host time per call
+// once two sizes alternate.)
+struct DeviceScratch {
+    std::mutex mu;
     void *p[2] = {nullptr, nullptr};
     size_t bytes[2] = {0, 0};
+    hipEvent_t done = nullptr;        // recorded after the last use
+    hipStream_t last = nullptr;       // stream of the last use
+    bool used = false;
 };
-std::mutex g_scratch_mu;
-std::map<std::pair<int, hipStream_t>, StreamScratch> g_scratch;
 
-void *stream_scratch(int slot, size_t bytes, hipStream_t stream) {
-    int dev = 0;
-    hip_check(hipGetDevice(&dev), "hipGetDevice");
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    StreamScratch &e = g_scratch[{dev, stream}];
-    if (e.bytes[slot] < bytes) {
-        if (e.p[slot]) {
-            hip_check(hipStreamSynchronize(stream), "scratch resize: stream sync");
-            hip_check(hipFree(e.p[slot]), "scratch resize: free");
-            e.p[slot] = nullptr;
-            e.bytes[slot] = 0;
-        }
-        const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-        hip_check(hipMalloc(&e.p[slot], want), "GEMM scratch allocation");
-        e.bytes[slot] = want;
-    }
-    return e.p[slot];
+DeviceScratch &device_scratch(int dev) {
+    static std::mutex mu;
+    static std::map<int, std::unique_ptr<DeviceScratch>> all;
+    std::lock_guard<std::mutex> lock(mu);
+    auto &e = all[dev];
+    if (!e)
+        e = std::make_unique<DeviceScratch>();
+    return *e;
 }
+
+class ScratchLease {
+  public:
+    explicit ScratchLease(hipStream_t stream) : s_(stream) {
+        int dev = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        d_ = &device_scratch(dev);
+        lock_ = std::unique_lock<std::mutex>(d_->mu);
+        if (!d_->done)
+            hip_check(hipEventCreateWithFlags(&d_->done, hipEventDisableTiming),
+                      "GEMM scratch event");
+        if (d_->used && d_->last != s_)
+            hip_check(hipStreamWaitEvent(s_, d_->done, 0), "GEMM scratch: wait for last use");
+    }
+    void *get(int slot, size_t bytes) {
+        if (d_->bytes[slot] < bytes) {
+            if (d_->p[slot]) {
+                hip_check(hipStreamSynchronize(s_), "GEMM scratch resize: stream sync");
+                hip_check(hipFree(d_->p[slot]), "GEMM scratch resize: free");
+                d_->p[slot] = nullptr;
+                d_->bytes[slot] = 0;
+            }
+            const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+            hip_check(hipMalloc(&d_->p[slot], want), "GEMM scratch allocation");
+            d_->bytes[slot] = want;
+        }
+        taken_ = true;
+        return d_->p[slot];
+    }
+    ~ScratchLease() {
+        if (taken_ && hipEventRecord(d_->done, s_) == hipSuccess) {
+            d_->last = s_;
+            d_->used = true;
+        }
+    }
+
+  private:
+    hipStream_t s_;
+    DeviceScratch *d_ = nullptr;
+    std::unique_lock<std::mutex> lock_;
+    bool taken_ = false;
+};
 
 // The MFMA GEMM for matmul (geglu false: W = c0/s0) or GeGLU (gate c0/s0, up c1/s1):
 // bf16 x directly; fp32 x (optionally RMS-normalised by norm_w first) through its
-// bf16 hi / lo split, held in the stream's scratch.  Grids of few tiles run split-K
-// (fp32 partials, likewise in the stream's scratch).
+// bf16 hi / lo split, held in the device's GEMM scratch.  Grids of few tiles run
+// split-K (fp32 partials, likewise in that scratch).
 void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, bool geglu,
                 const uint32_t *c0, const uint8_t *s0, float ts0, const uint32_t *c1,
                 const uint8_t *s1, float ts1, void *out, uint32_t M, uint32_t N, uint32_t K,
@@ -143,12 +182,13 @@ void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, boo
     g.ldc = N;
     g.geglu = geglu;
     g.out_f32 = !bf16;
+    ScratchLease scratch(stream);
     if (bf16) {
         g.A = static_cast<const uint16_t *>(x);
         g.a_k = K;
     } else {
-        auto *split = static_cast<uint16_t *>(
-            stream_scratch(0, apex_hip::gemm_split_bytes(M, K), stream));
+        auto *split =
+            static_cast<uint16_t *>(scratch.get(0, apex_hip::gemm_split_bytes(M, K)));
         hip_check(apex_hip::gemm_split_launch(static_cast<const float *>(x), norm_w, eps, split,
                                               M, K, stream),
                   "fp32 GEMM split launch");
@@ -157,8 +197,7 @@ void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, boo
     }
     const uint32_t splits = apex_hip::gemm_splitk_splits(g);
     if (splits > 1) {
-        auto *part = static_cast<float *>(
-            stream_scratch(1, apex_hip::gemm_splitk_bytes(g, splits), stream));
+        auto *part = static_cast<float *>(scratch.get(1, apex_hip::gemm_splitk_bytes(g, splits)));
         hip_check(apex_hip::gemm_splitk_launch(g, splits, part, stream),
                   "gemm_nvfp4 split-K launch");
         return;

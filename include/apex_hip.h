@@ -192,7 +192,8 @@ int apex_hip_validate_run(const char *kernel, const apex_hip_arg *args, size_t n
 /* shaders/matmul.metal:4-53 / src/tests/cpu_ref.h:48-63: out[t, r] = sum_k W[r,k] x[t,k]
  * with fp32 activations and outputs.  A GEMV for few tokens; for more (K % 64 == 0,
  * apex_hip_set_gemm_min_tokens) an MFMA GEMM on x split into bf16 hi + lo halves
- * (|x - hi - lo| <= 2^-17 |x|) held in the stream's scratch (tokens * K * 4 bytes). */
+ * (|x - hi - lo| <= 2^-17 |x|) held in the device's GEMM scratch (tokens * K * 4
+ * bytes). */
 int apex_nvfp4_matmul_f32(const float *x, const uint32_t *codes, const uint8_t *scales,
                           float tensor_scale, float *out, uint32_t tokens, uint32_t rows,
                           uint32_t K, void *stream);
@@ -297,9 +298,8 @@ int apex_hip_set_gemv_waves_per_cu(int waves);
  * least 64 tiles of 256 tokens x 256 outputs, else from 32).
  * Process-wide; results agree within the stated tolerances either way.  The GEMMs'
  * scratch (fp32 split, split-K partials) is device memory the library keeps per
- * (device, stream), grown on demand (growing synchronises that stream) and held until
- * the process ends; calls issued on one stream from several host threads at once must
- * not overlap. */
+ * device, grown on demand (growing synchronises the calling stream) and held until the
+ * process ends; uses from different streams are ordered on the GPU by an event. */
 int apex_hip_set_gemm_min_tokens(uint32_t bf16_tokens, uint32_t f32_tokens);
 
 /* ---- MoE expert FFN (no reference kernel) ------------------------------------------

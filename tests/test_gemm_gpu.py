@@ -258,3 +258,26 @@ def test_split_pass_long_rows_and_tensor_scales(gemm_threshold):
     want_n = oracle.geglu(oracle.matvec(g.codes, g.scales, xn), oracle.matvec(u.codes, u.scales, xn))
     assert rel_l2(run_geglu(x, g, u, True, norm=(nw, eps)), want_n) < TOL_REF_GATE
     assert rel_l2(run_matmul_f32(x, g, 2.0), oracle.matvec(g.codes, g.scales, x, 2.0)) < TOL_REF_GATE
+
+
+def test_gemm_scratch_shared_by_two_streams(gemm_threshold):
+    """The fp32 GEMM's split / split-K scratch is one set per device: calls of
+    alternating sizes on two streams (the larger ones grow it) are ordered by the
+    scratch's event, and every result meets the reference gate."""
+    rng = np.random.default_rng(41)
+    N, K = 300, 1024
+    w = synth.nvfp4_weights(rng, N, K)
+    dc, ds = dev(w.codes), dev(w.scales)
+    s1, s2 = hip.Stream(), hip.Stream()
+    keep = []
+    for T, s in [(64, s1), (200, s2), (64, s2), (480, s1), (200, s1), (64, s2)]:
+        X = rng.standard_normal((T, K)).astype(np.float32)
+        dx, out = dev(X), hip.DeviceArray((T, N), np.float32)
+        hip.nvfp4_matmul_f32(dx, dc, ds, out, T, N, K, stream=s)
+        keep.append((X, dx, out))
+    s1.synchronize()
+    s2.synchronize()
+    for X, dx, out in keep:
+        assert rel_l2(out.numpy(), oracle.matvec(w.codes, w.scales, X)) < TOL_REF_GATE, X.shape
+    s1.close()
+    s2.close()
