@@ -24,6 +24,8 @@ the path, each timed the same way (HIP events around back-to-back steps):
   gemm_prefill  dense prefill GEMM bf16 [2048,5376] x NVFP4 [21504x5376]^T -> TFLOP/s;
   geglu_prefill / matmul_prefill_f32  the same weight shape through the fused GeGLU
                 (bf16 x) and the fp32 matmul (fp32 x, bf16 hi + lo split) -> TFLOP/s;
+  dense_mlp_prefill_f32  the Gemma dense MLP block (hidden 2816, intermediate 2112) at
+                512 tokens, fp32, RMSNorm folded in -> TFLOP/s;
   moe_decode    MoE decode: 16 tokens, same experts -> GB/s of the distinct experts'
                 weights + activations (expert slots rotated over copies > MALL).
 --calibrate runs, before the timed steps, one streaming read of 1 GiB and one 256 MiB
