@@ -121,9 +121,11 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormArgs a) {
 // CU holds at most 32 waves, so the loads a wave keeps in flight set the rate: two
 // tokens per wave measured 4.29-4.39 -> 4.73 TB/s; four (67 VGPRs, fewer waves) gained
 // nothing.
-constexpr int kHeadsPerBlock = 8;
+// Heads per workgroup: 16 when there are that many (one table per 16 heads: 4.78-4.85
+// against 4.61-4.63 TB/s with 8 at 16 heads), else 8.
 constexpr int kTokensPerBlock = 2;
 
+template <int kHeadsPerBlock>
 __global__ __launch_bounds__(64 * kHeadsPerBlock) void head_norm_rope_kernel(HeadNormRopeArgs a) {
     constexpr int kMaxPerLane = kHeadNormMaxDim / 2 / 64; // pairs per lane
     constexpr int TB = kTokensPerBlock;
@@ -203,9 +205,13 @@ hipError_t head_norm_rope_launch(const HeadNormRopeArgs &a, hipStream_t stream) 
         return hipSuccess;
     if (a.head_dim == 0 || a.head_dim % 2 || a.head_dim > kHeadNormMaxDim || a.rope_pairs > a.head_dim / 2)
         return hipErrorInvalidValue;
-    const uint64_t groups = (a.heads + kHeadsPerBlock - 1) / kHeadsPerBlock;
+    const uint32_t hpb = a.heads >= 16 ? 16 : 8;
+    const uint64_t groups = (a.heads + hpb - 1) / hpb;
     const dim3 grid((uint32_t)((a.tokens + kTokensPerBlock - 1) / kTokensPerBlock * groups));
-    hipLaunchKernelGGL(head_norm_rope_kernel, grid, dim3(64 * kHeadsPerBlock), 0, stream, a);
+    if (hpb == 16)
+        hipLaunchKernelGGL(head_norm_rope_kernel<16>, grid, dim3(64 * 16), 0, stream, a);
+    else
+        hipLaunchKernelGGL(head_norm_rope_kernel<8>, grid, dim3(64 * 8), 0, stream, a);
     return hipGetLastError();
 }
 
