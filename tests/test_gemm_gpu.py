@@ -281,3 +281,26 @@ def test_gemm_scratch_shared_by_two_streams(gemm_threshold):
         assert rel_l2(out.numpy(), oracle.matvec(w.codes, w.scales, X)) < TOL_REF_GATE, X.shape
     s1.close()
     s2.close()
+
+
+@pytest.mark.parametrize("T", [15, 16, 31, 32, 33])
+def test_dense_dispatch_boundaries_by_size(T):
+    """The default size rule changes path at 16 (GeGLU) and 32 (matmul, grids of few
+    tiles) tokens; either side of each boundary meets the same gates: fp32 matmul and
+    GeGLU at 1e-5, bf16 at 1e-2."""
+    hip.set_gemm_min_tokens(0, 0)
+    rng = np.random.default_rng(50 + T)
+    N, K = 448, 1024
+    g, u = synth.nvfp4_weights(rng, N, K), synth.nvfp4_weights(rng, N, K)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    assert rel_l2(run_matmul_f32(X, g), oracle.matvec(g.codes, g.scales, X)) < TOL_REF_GATE
+    want = oracle.geglu(oracle.matvec(g.codes, g.scales, X), oracle.matvec(u.codes, u.scales, X))
+    assert rel_l2(run_geglu(X, g, u, True), want) < TOL_REF_GATE
+    xb = synth.bf16_from_f32(X)
+    xf = bf16(xb)
+    want_b = oracle.geglu(oracle.matvec(g.codes, g.scales, xf), oracle.matvec(u.codes, u.scales, xf))
+    assert rel_l2(run_geglu(xb, g, u, False), want_b) < TOL_BF16
+    out = hip.DeviceArray((T, N), np.uint16)
+    hip.nvfp4_matmul_bf16(dev(xb), dev(g.codes), dev(g.scales), out, T, N, K)
+    hip.synchronize()
+    assert rel_l2(bf16(out.numpy()), oracle.matvec(g.codes, g.scales, xf)) < TOL_BF16
