@@ -1482,6 +1482,163 @@ hipError_t router_launch_epl(const MoeRouterArgs &a, hipStream_t stream) {
     }
 }
 
+namespace {
+
+// Router logits on bf16 MFMA.  Workgroup: 4 waves = 128 tokens x 32 experts (wave w:
+// tokens t0 + 32 w + 0..31), the column groups [g0, g1) of its split.  Per group the
+// 8-bit codes (exact in bf16) multiply the hi and lo halves of x on the MFMAs into a
+// fresh accumulator (sum of q x over the group), the lane pair sums x over the group,
+// and the total gains s * sum(q x) + b * sum(x) in fp32 -- the reference's grouping
+// (orc_moe_router_logits_q8).  Accumulator element el of lane l: token l % 32, expert
+// 8 (el / 4) + 4 (l / 32) + el % 4 of the block (codes are the first MFMA operand).
+constexpr uint32_t kRouterMfmaGroups = kRouterMaxHidden / kQGroup;
+
+__global__ __launch_bounds__(256) void moe_router_mfma_kernel(MoeRouterArgs a, const uint16_t *split,
+                                                              float *part, uint32_t S) {
+    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    __shared__ float s_sc[kRouterMfmaGroups][32], s_bi[kRouterMfmaGroups][32];
+    const uint32_t T = a.T, E = a.E, H = a.H, NG = H / kQGroup;
+    const uint32_t eb = (E + 31) / 32;
+    // Workgroups are dealt round-robin over the 8 XCDs: workgroup b takes unit
+    // (b % 8) * per_xcd + b / 8, expert block fastest, so the expert blocks that share
+    // one (token block, split) slice of x run one after another on one XCD and read it
+    // through one L2 (round-robin order: from HBM once per expert block, 4x the bytes).
+    const uint32_t units = ((T + 127) / 128) * eb * S;
+    const uint32_t per_xcd = (units + 7) / 8;
+    const uint32_t u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (u >= units)
+        return;
+    const uint32_t e0 = (u % eb) * 32;
+    const uint32_t s = (u / eb) % S, t0 = (u / eb / S) * 128;
+    const uint32_t g0 = s * NG / S, g1 = (s + 1) * NG / S;
+    for (uint32_t i = threadIdx.x; i < (g1 - g0) * 32; i += blockDim.x) {
+        const uint32_t g = g0 + i / 32, el = i % 32, e = e0 + el;
+        const bool ok = e < E;
+        s_sc[i / 32][el] = ok ? bf16_bits_to_f32(a.qs[(size_t)e * NG + g]) : 0.0f;
+        s_bi[i / 32][el] = ok ? bf16_bits_to_f32(a.qb[(size_t)e * NG + g]) : 0.0f;
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t h = lane >> 5, r = lane & 31;
+    const uint32_t token = t0 + 32 * wave + r;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(split, T * 2 * H * 2);
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
+    const uint32_t arow = token < T ? token * 2 * H * 2 : kOutOfRange;
+    const uint32_t qrow = e0 + r < E ? (e0 + r) * H : kOutOfRange;
+    f32x16_t tot;
+#pragma unroll
+    for (int el = 0; el < 16; ++el)
+        tot[el] = 0.0f;
+    // One group's loads: per k-step the hi and lo pieces of x and 8 codes.
+    struct GroupRegs {
+        u32x4_t ahi[4], alo[4];
+        u32x2_t q[4];
+    };
+    auto load_group = [&](GroupRegs &G, uint32_t g) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint32_t k = kQGroup * g + 16 * ks + 8 * h;
+            const bool ok = g < g1;
+            G.ahi[ks] = load_b128(ra, arow == kOutOfRange || !ok ? kOutOfRange : arow + k * 2);
+            G.alo[ks] = load_b128(ra, arow == kOutOfRange || !ok ? kOutOfRange : arow + (H + k) * 2);
+            G.q[ks] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                rq, (int)(qrow == kOutOfRange || !ok ? kOutOfRange : qrow + k), 0, 0));
+        }
+    };
+    auto compute_group = [&](const GroupRegs &G, uint32_t g) {
+        f32x16_t acc;
+#pragma unroll
+        for (int el = 0; el < 16; ++el)
+            acc[el] = 0.0f;
+        float sx = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            u32x4_t qb;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t word = G.q[ks][p / 2], sh = 16 * (p % 2);
+                const float lo = (float)((word >> sh) & 0xFFu), hi = (float)((word >> (sh + 8)) & 0xFFu);
+                qb[p] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+            }
+            const bf16x8_t qv = __builtin_bit_cast(bf16x8_t, qb);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qv, __builtin_bit_cast(bf16x8_t, G.ahi[ks]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qv, __builtin_bit_cast(bf16x8_t, G.alo[ks]), acc, 0, 0, 0);
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                sx += (__uint_as_float(G.ahi[ks][p] << 16) + __uint_as_float(G.ahi[ks][p] & 0xFFFF0000u)) +
+                      (__uint_as_float(G.alo[ks][p] << 16) + __uint_as_float(G.alo[ks][p] & 0xFFFF0000u));
+        }
+        sx = add_xor32(sx);   // the other half of the group's columns
+#pragma unroll
+        for (int el = 0; el < 16; ++el) {
+            const uint32_t ex = 8 * (el / 4) + 4 * h + el % 4;
+            tot[el] += s_sc[g - g0][ex] * acc[el] + s_bi[g - g0][ex] * sx;
+        }
+    };
+    // Two register sets: group g + 1's loads are in flight while group g is computed.
+    GroupRegs buf[2];
+    load_group(buf[0], g0);
+    for (uint32_t g = g0; g < g1; g += 2) {
+        load_group(buf[1], g + 1);
+        compute_group(buf[0], g);
+        if (g + 1 >= g1)
+            break;
+        load_group(buf[0], g + 2);
+        compute_group(buf[1], g + 1);
+    }
+    if (token >= T)
+        return;
+    float *out = part + ((size_t)s * T + token) * E;
+#pragma unroll
+    for (int el = 0; el < 16; ++el) {
+        const uint32_t e = e0 + 8 * (el / 4) + 4 * h + el % 4;
+        if (e < E)
+            out[e] = tot[el];
+    }
+}
+
+// logits[t][e] = sum over s = 0 .. S-1 of part[s][t][e], in that order.
+__global__ __launch_bounds__(256) void moe_router_partials_kernel(const float *part, uint32_t S,
+                                                                  float *logits, size_t n) {
+    for (size_t q = blockIdx.x * 256ull + threadIdx.x; q < n; q += (size_t)gridDim.x * 256) {
+        float acc = 0.0f;
+        for (uint32_t s = 0; s < S; ++s)
+            acc += part[s * n + q];
+        logits[q] = acc;
+    }
+}
+
+} // namespace
+
+// Splits so that the workgroups cover the CUs about twice, at least 4 groups each.
+uint32_t moe_router_mfma_splits(const MoeRouterArgs &a) {
+    const uint32_t blocks = ((a.T + 127) / 128) * ((a.E + 31) / 32);
+    const uint32_t ng = a.H / kQGroup;
+    uint32_t s = (512 + blocks - 1) / blocks;
+    s = s < ng / 4 ? s : ng / 4;
+    return s >= 1 ? s : 1;
+}
+
+hipError_t moe_router_mfma_launch(const MoeRouterArgs &a, const uint16_t *split, float *part,
+                                  uint32_t splits, hipStream_t stream) {
+    if (a.T == 0)
+        return hipSuccess;
+    if (splits < 1 || splits > a.H / kQGroup || (uint64_t)a.T * a.H * 4 >= (1ull << 31))
+        return hipErrorInvalidValue;
+    const uint32_t units = ((a.T + 127) / 128) * ((a.E + 31) / 32) * splits;
+    hipLaunchKernelGGL(moe_router_mfma_kernel, dim3(8 * ((units + 7) / 8)), dim3(256), 0, stream,
+                       a, split, part, splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return e;
+    const size_t n = (size_t)a.T * a.E;
+    const uint32_t grid = (uint32_t)((n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048);
+    hipLaunchKernelGGL(moe_router_partials_kernel, dim3(grid), dim3(256), 0, stream, part, splits,
+                       a.logits, n);
+    return hipGetLastError();
+}
+
 hipError_t moe_router_logits_launch(const MoeRouterArgs &a, hipStream_t stream) {
     if (a.T == 0)
         return hipSuccess;

@@ -30,8 +30,11 @@ def router_logits(h, rw):
 
 
 @pytest.mark.parametrize("T,E,H", [(1, 128, 2816), (16, 128, 2816), (300, 128, 2816),
-                                   (33, 64, 256), (9, 200, 4096), (257, 8, 64)])
+                                   (33, 64, 256), (9, 200, 4096), (257, 8, 64),
+                                   (600, 128, 2816), (515, 200, 1024), (512, 8, 4096)])
 def test_router_logits_match_oracle(T, E, H):
+    """From 512 tokens the MFMA form runs (x split into bf16 hi + lo, codes exact in
+    bf16, split-K partials summed in order), below the VALU kernels."""
     h, rw = synth.router_case(seed=T + E, tokens=T, E=E, H=H)
     print(f"router logits T={T} E={E} H={H}", flush=True)
     got = router_logits(h, rw)
