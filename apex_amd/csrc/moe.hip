@@ -1498,6 +1498,11 @@ __global__ __launch_bounds__(256) void moe_router_mfma_kernel(MoeRouterArgs a, c
     typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
     typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
     __shared__ float s_sc[kRouterMfmaGroups][32], s_bi[kRouterMfmaGroups][32];
+    // the block's codes of the split's groups as bf16 (exact): [group][expert][72]
+    // (rows padded from 64 to 72 elements so the 32 lanes' 16-byte reads spread over
+    // the banks)
+    extern __shared__ u32x4_t s_codes[];
+    constexpr uint32_t kRow = 72 / 8;   // 16-byte pieces per expert row
     const uint32_t T = a.T, E = a.E, H = a.H, NG = H / kQGroup;
     const uint32_t eb = (E + 31) / 32;
     // Workgroups are dealt round-robin over the 8 XCDs: workgroup b takes unit
@@ -1518,14 +1523,27 @@ __global__ __launch_bounds__(256) void moe_router_mfma_kernel(MoeRouterArgs a, c
         s_sc[i / 32][el] = ok ? bf16_bits_to_f32(a.qs[(size_t)e * NG + g]) : 0.0f;
         s_bi[i / 32][el] = ok ? bf16_bits_to_f32(a.qb[(size_t)e * NG + g]) : 0.0f;
     }
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
+    for (uint32_t i = threadIdx.x; i < (g1 - g0) * 32 * 8; i += blockDim.x) {
+        // piece p (8 codes) of expert el in group g0 + gi
+        const uint32_t gi = i / 256, el = (i / 8) % 32, p = i % 8;
+        const uint32_t off = e0 + el < E ? (e0 + el) * H + (g0 + gi) * kQGroup + 8 * p : kOutOfRange;
+        const auto q2 = __builtin_amdgcn_raw_buffer_load_b64(rq, (int)off, 0, 0);
+        u32x4_t qb;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t word = q2[c / 2], sh = 16 * (c % 2);
+            const float lo = (float)((word >> sh) & 0xFFu), hi = (float)((word >> (sh + 8)) & 0xFFu);
+            qb[c] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+        }
+        s_codes[(gi * 32 + el) * kRow + p] = qb;
+    }
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t h = lane >> 5, r = lane & 31;
     const uint32_t token = t0 + 32 * wave + r;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(split, T * 2 * H * 2);
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
     const uint32_t arow = token < T ? token * 2 * H * 2 : kOutOfRange;
-    const uint32_t qrow = e0 + r < E ? (e0 + r) * H : kOutOfRange;
     f32x16_t tot;
 #pragma unroll
     for (int el = 0; el < 16; ++el)
@@ -1533,7 +1551,6 @@ __global__ __launch_bounds__(256) void moe_router_mfma_kernel(MoeRouterArgs a, c
     // One group's loads: per k-step the hi and lo pieces of x and 8 codes.
     struct GroupRegs {
         u32x4_t ahi[4], alo[4];
-        u32x2_t q[4];
     };
     auto load_group = [&](GroupRegs &G, uint32_t g) {
 #pragma unroll
@@ -1542,8 +1559,6 @@ __global__ __launch_bounds__(256) void moe_router_mfma_kernel(MoeRouterArgs a, c
             const bool ok = g < g1;
             G.ahi[ks] = load_b128(ra, arow == kOutOfRange || !ok ? kOutOfRange : arow + k * 2);
             G.alo[ks] = load_b128(ra, arow == kOutOfRange || !ok ? kOutOfRange : arow + (H + k) * 2);
-            G.q[ks] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-                rq, (int)(qrow == kOutOfRange || !ok ? kOutOfRange : qrow + k), 0, 0));
         }
     };
     auto compute_group = [&](const GroupRegs &G, uint32_t g) {
@@ -1554,14 +1569,9 @@ __global__ __launch_bounds__(256) void moe_router_mfma_kernel(MoeRouterArgs a, c
         float sx = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            u32x4_t qb;
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const uint32_t word = G.q[ks][p / 2], sh = 16 * (p % 2);
-                const float lo = (float)((word >> sh) & 0xFFu), hi = (float)((word >> (sh + 8)) & 0xFFu);
-                qb[p] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
-            }
-            const bf16x8_t qv = __builtin_bit_cast(bf16x8_t, qb);
+            // codes of expert r, columns 16 ks + 8 h .. +7 of the group
+            const bf16x8_t qv =
+                __builtin_bit_cast(bf16x8_t, s_codes[((g - g0) * 32 + r) * kRow + 2 * ks + h]);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qv, __builtin_bit_cast(bf16x8_t, G.ahi[ks]), acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qv, __builtin_bit_cast(bf16x8_t, G.alo[ks]), acc, 0, 0, 0);
 #pragma unroll
@@ -1612,11 +1622,16 @@ __global__ __launch_bounds__(256) void moe_router_partials_kernel(const float *p
 } // namespace
 
 // Splits so that the workgroups cover the CUs about twice, at least 4 groups each.
+// at most this many groups per split: their converted codes (4.6 KB each) stay in LDS
+constexpr uint32_t kRouterMfmaMaxSplitGroups = 24;
+
 uint32_t moe_router_mfma_splits(const MoeRouterArgs &a) {
     const uint32_t blocks = ((a.T + 127) / 128) * ((a.E + 31) / 32);
     const uint32_t ng = a.H / kQGroup;
     uint32_t s = (512 + blocks - 1) / blocks;
     s = s < ng / 4 ? s : ng / 4;
+    const uint32_t smin = (ng + kRouterMfmaMaxSplitGroups - 1) / kRouterMfmaMaxSplitGroups;
+    s = s > smin ? s : smin;
     return s >= 1 ? s : 1;
 }
 
@@ -1624,10 +1639,17 @@ hipError_t moe_router_mfma_launch(const MoeRouterArgs &a, const uint16_t *split,
                                   uint32_t splits, hipStream_t stream) {
     if (a.T == 0)
         return hipSuccess;
-    if (splits < 1 || splits > a.H / kQGroup || (uint64_t)a.T * a.H * 4 >= (1ull << 31))
+    if (splits < 1 || splits > a.H / kQGroup || (uint64_t)a.T * a.H * 4 >= (1ull << 31) ||
+        (a.H / kQGroup + splits - 1) / splits > kRouterMfmaMaxSplitGroups)
         return hipErrorInvalidValue;
     const uint32_t units = ((a.T + 127) / 128) * ((a.E + 31) / 32) * splits;
-    hipLaunchKernelGGL(moe_router_mfma_kernel, dim3(8 * ((units + 7) / 8)), dim3(256), 0, stream,
+    // converted codes: the largest split's groups x 32 experts x 72 bf16
+    const uint32_t ng = a.H / kQGroup, gmax = (ng + splits - 1) / splits;
+    const size_t lds = (size_t)gmax * 32 * 72 * 2;
+    static std::atomic<uint64_t> attr{0};
+    if (hipError_t e = set_lds(moe_router_mfma_kernel, lds, attr); e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(moe_router_mfma_kernel, dim3(8 * ((units + 7) / 8)), dim3(256), lds, stream,
                        a, split, part, splits);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
