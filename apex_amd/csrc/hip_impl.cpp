@@ -93,10 +93,11 @@ constexpr uint32_t kFileBuffers = 8;
 // Scratch of the dense GEMMs (slot 0: the fp32 split, slot 1: split-K partials), one
 // set per device, grown on demand and held until the process ends.  A call holds the
 // device's lease while it enqueues the kernels that use the scratch; at the end it
-// records an event on its stream, and a later call on another stream makes its stream
-// wait for that event first (on the GPU, no host synchronisation), so uses from any
-// streams and threads run one after another.  Growing waits for the last user's
-// stream, frees the old buffer and allocates the new one.  (Stream-ordered
+// records an event on its stream, and the next call makes its stream wait for that
+// event first (on the GPU, no host synchronisation), so uses from any streams and
+// threads run one after another.  Growing synchronises the calling stream (which
+// already waits for the last use), frees the old buffer and allocates the new one.
+// (Stream-ordered
 // hipMallocAsync / hipFreeAsync per call measured 40-330 us of host time per call
 // once two sizes alternate.)
 struct DeviceScratch {
@@ -104,7 +105,6 @@ struct DeviceScratch {
     void *p[2] = {nullptr, nullptr};
     size_t bytes[2] = {0, 0};
     hipEvent_t done = nullptr;        // recorded after the last use
-    hipStream_t last = nullptr;       // stream of the last use
     bool used = false;
 };
 
@@ -128,7 +128,9 @@ class ScratchLease {
         if (!d_->done)
             hip_check(hipEventCreateWithFlags(&d_->done, hipEventDisableTiming),
                       "GEMM scratch event");
-        if (d_->used && d_->last != s_)
+        // always, also when the last use was on this stream's handle: a destroyed
+        // stream's handle value can come back for a new stream
+        if (d_->used)
             hip_check(hipStreamWaitEvent(s_, d_->done, 0), "GEMM scratch: wait for last use");
     }
     void *get(int slot, size_t bytes) {
@@ -147,10 +149,8 @@ class ScratchLease {
         return d_->p[slot];
     }
     ~ScratchLease() {
-        if (taken_ && hipEventRecord(d_->done, s_) == hipSuccess) {
-            d_->last = s_;
+        if (taken_ && hipEventRecord(d_->done, s_) == hipSuccess)
             d_->used = true;
-        }
     }
 
   private:
