@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace apex_hip {
 
 // Arguments of one GEMV launch.  codes/scales/tensor_scale index 0 is the plain
@@ -23,11 +25,12 @@ struct GemvArgs {
 
 enum class GemvMode { PlainF32, PlainBF16, GegluBF16, GegluF32 };
 
-// Tuning knobs (set from the device properties at backend init, or by sweeps).
-extern int kTargetWavesPerCU;
-extern int kGemvMapping;
-extern int kGemvDepth;
-extern int kNumCUs;
+// Launch sizing, process-wide: target resident GEMV waves per CU
+// (apex_hip_set_gemv_waves_per_cu) and the device's CU count (read at first use).
+// Atomics: a setter may run while other threads dispatch.
+extern std::atomic<int> kTargetWavesPerCU;
+extern std::atomic<int> kNumCUs;
+inline int num_cus() { return kNumCUs.load(std::memory_order_relaxed); }
 
 hipError_t gemv_launch(const GemvArgs &a, GemvMode mode, bool x_is_bf16, hipStream_t stream);
 hipError_t geglu_f32_launch(const float *gate, const float *up, float *out, uint32_t count,

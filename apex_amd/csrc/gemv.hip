@@ -76,10 +76,8 @@ __global__ __launch_bounds__(kThreads) void read_probe_kernel(const void *p, uin
 
 } // namespace
 
-int kTargetWavesPerCU = 12;
-int kGemvMapping = 0;
-int kGemvDepth = 2;
-int kNumCUs = 256;
+std::atomic<int> kTargetWavesPerCU{12};
+std::atomic<int> kNumCUs{256};
 
 hipError_t gemv_launch(const GemvArgs &a, GemvMode mode, bool x_is_bf16, hipStream_t stream) {
     if (a.tokens == 0 || a.rows == 0)
@@ -112,7 +110,7 @@ hipError_t read_probe_launch(const void *p, size_t bytes, uint32_t *sink, hipStr
     const size_t pieces = bytes / 16;
     if (pieces == 0 || pieces >= (1ull << 27))
         return hipErrorInvalidValue;
-    const unsigned grid = (unsigned)kNumCUs * 8;
+    const unsigned grid = (unsigned)num_cus() * 8;
     hipLaunchKernelGGL(read_probe_kernel, dim3(grid), dim3(kThreads), 0, stream, p,
                        (uint32_t)pieces, sink);
     return hipGetLastError();

@@ -58,7 +58,7 @@ void init_device_tuning() {
     if (hipGetDevice(&dev) == hipSuccess &&
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
         cus > 0)
-        apex_hip::kNumCUs = cus;
+        apex_hip::kNumCUs.store(cus, std::memory_order_relaxed);
     done = true;
 }
 
@@ -81,8 +81,14 @@ void check_nvfp4_shape(uint32_t rows, uint32_t K) {
 
 // Tokens from which the dense products (matmul, GeGLU) run as MFMA GEMMs instead of
 // GEMVs, [bf16 activations, fp32 activations]; 0 = by size (use_dense_gemm).  Set by
-// apex_hip_set_gemm_min_tokens.
-uint32_t g_gemm_min_tokens[2] = {0, 0};
+// apex_hip_set_gemm_min_tokens; atomic because a setter may run while other threads
+// dispatch.
+std::atomic<uint32_t> g_gemm_min_tokens[2] = {0, 0};
+
+// Dense-product launches of this process by form (apex_hip_dense_dispatch_counts).
+enum DispatchKind { kDispGemv = 0, kDispGemm = 1, kDispSplitK = 2, kDispSplit = 3, kDispKinds };
+std::atomic<uint64_t> g_dispatch[kDispKinds] = {};
+void count_dispatch(DispatchKind k) { g_dispatch[k].fetch_add(1, std::memory_order_relaxed); }
 
 // Pinned staging for file -> device streaming: 8 buffers of 8 MiB, i.e. 4 reader threads
 // with a read and a copy in flight each (64 MiB pinned, kept between calls); measured
@@ -120,20 +126,12 @@ DeviceScratch &device_scratch(int dev) {
 
 class ScratchLease {
   public:
-    explicit ScratchLease(hipStream_t stream) : s_(stream) {
-        int dev = 0;
-        hip_check(hipGetDevice(&dev), "hipGetDevice");
-        d_ = &device_scratch(dev);
-        lock_ = std::unique_lock<std::mutex>(d_->mu);
-        if (!d_->done)
-            hip_check(hipEventCreateWithFlags(&d_->done, hipEventDisableTiming),
-                      "GEMM scratch event");
-        // always, also when the last use was on this stream's handle: a destroyed
-        // stream's handle value can come back for a new stream
-        if (d_->used)
-            hip_check(hipStreamWaitEvent(s_, d_->done, 0), "GEMM scratch: wait for last use");
-    }
+    // The device's scratch is locked, and the stream made to wait for its last use,
+    // only when a call takes scratch (the first get()): calls that need none, such as
+    // a bf16 GEMM without split-K, are not ordered behind other streams' GEMMs.
+    explicit ScratchLease(hipStream_t stream) : s_(stream) {}
     void *get(int slot, size_t bytes) {
+        acquire();
         if (d_->bytes[slot] < bytes) {
             if (d_->p[slot]) {
                 hip_check(hipStreamSynchronize(s_), "GEMM scratch resize: stream sync");
@@ -145,19 +143,33 @@ class ScratchLease {
             hip_check(hipMalloc(&d_->p[slot], want), "GEMM scratch allocation");
             d_->bytes[slot] = want;
         }
-        taken_ = true;
         return d_->p[slot];
     }
     ~ScratchLease() {
-        if (taken_ && hipEventRecord(d_->done, s_) == hipSuccess)
+        if (d_ && hipEventRecord(d_->done, s_) == hipSuccess)
             d_->used = true;
     }
 
   private:
+    void acquire() {
+        if (d_)
+            return;
+        int dev = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        DeviceScratch *d = &device_scratch(dev);
+        lock_ = std::unique_lock<std::mutex>(d->mu);
+        if (!d->done)
+            hip_check(hipEventCreateWithFlags(&d->done, hipEventDisableTiming),
+                      "GEMM scratch event");
+        // always, also when the last use was on this stream's handle: a destroyed
+        // stream's handle value can come back for a new stream
+        if (d->used)
+            hip_check(hipStreamWaitEvent(s_, d->done, 0), "GEMM scratch: wait for last use");
+        d_ = d;
+    }
     hipStream_t s_;
-    DeviceScratch *d_ = nullptr;
+    DeviceScratch *d_ = nullptr; // set once the lease holds the device's scratch
     std::unique_lock<std::mutex> lock_;
-    bool taken_ = false;
 };
 
 // The MFMA GEMM for matmul (geglu false: W = c0/s0) or GeGLU (gate c0/s0, up c1/s1):
@@ -192,6 +204,7 @@ void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, boo
         hip_check(apex_hip::gemm_split_launch(static_cast<const float *>(x), norm_w, eps, split,
                                               M, K, stream),
                   "fp32 GEMM split launch");
+        count_dispatch(kDispSplit);
         g.A = split;
         g.a_k = 2 * K;
     }
@@ -200,9 +213,11 @@ void dense_gemm(const void *x, bool bf16, const uint16_t *norm_w, float eps, boo
         auto *part = static_cast<float *>(scratch.get(1, apex_hip::gemm_splitk_bytes(g, splits)));
         hip_check(apex_hip::gemm_splitk_launch(g, splits, part, stream),
                   "gemm_nvfp4 split-K launch");
+        count_dispatch(kDispSplitK);
         return;
     }
     hip_check(apex_hip::gemm_launch(g, stream), "gemm_nvfp4 launch");
+    count_dispatch(kDispGemm);
 }
 
 void gemm_impl(const uint16_t *A, const uint32_t *codes, const uint8_t *scales, float ts,
@@ -227,7 +242,7 @@ void gemm_impl(const uint16_t *A, const uint32_t *codes, const uint8_t *scales, 
 bool use_dense_gemm(uint32_t tokens, uint32_t rows, uint32_t K, bool bf16, bool geglu) {
     if (!apex_hip::gemm_supported(tokens, rows, K, bf16 ? K : 2 * K, !bf16))
         return false;
-    if (const uint32_t fixed = g_gemm_min_tokens[bf16 ? 0 : 1])
+    if (const uint32_t fixed = g_gemm_min_tokens[bf16 ? 0 : 1].load(std::memory_order_relaxed))
         return tokens >= fixed;
     if (geglu)
         return tokens >= 16;
@@ -262,6 +277,7 @@ void matmul_impl(const void *x, bool bf16, const uint32_t *codes, const uint8_t 
                                             : apex_hip::GemvMode::PlainF32,
                                     bf16, stream),
               "matmul_nvfp4 launch");
+    count_dispatch(kDispGemv);
 }
 
 // norm_w (fp32 x only): RMS-normalise each x row first (x * inv * norm_w, eps norm_eps).
@@ -305,12 +321,14 @@ void geglu_impl(const void *x, bool bf16, const uint32_t *gc, const uint8_t *gs,
                                             : apex_hip::GemvMode::GegluF32,
                                     bf16, stream),
               "geglu_nvfp4 launch");
+    count_dispatch(kDispGemv);
 }
 
 bool moe_use_gemm(uint32_t T, uint32_t k, uint32_t H, uint32_t I) {
-    if (apex_hip::kMoePath == 1)
+    const int path = apex_hip::kMoePath.load(std::memory_order_relaxed);
+    if (path == 1)
         return false;
-    if (apex_hip::kMoePath == 2)
+    if (path == 2)
         return true;
     return !(T <= apex_hip::kMoeGemvMaxTokens && (uint64_t)T * k <= apex_hip::kMoeGemvMaxPairs &&
              H <= 3072 && I <= 1024);
@@ -388,7 +406,7 @@ void router_impl(const apex_hip::MoeRouterArgs &a, hipStream_t stream) {
     if (!apex_hip::moe_router_supported(a, &why))
         fail(APEX_HIP_E_INVALID, std::string("moe_router: ") + why);
     init_device_tuning();
-    if (a.T >= apex_hip::kRouterMfmaMinTokens) {
+    if (a.T >= apex_hip::kRouterMfmaMinTokens && apex_hip::moe_router_mfma_fits(a)) {
         // prefill: MFMA form on the normed rows split into bf16 hi + lo
         ScratchLease scratch(stream);
         auto *split =
@@ -481,7 +499,17 @@ void launch_matmul_nvfp4(const LaunchCtx &c) {
         need(c, 3, (uint64_t)(tokens - 1) * w_rows * 4 + (uint64_t)rows * 4, "matmul_nvfp4 output");
     if (tokens == 0 || rows == 0)
         return;
-    // Output rows are strided by w_rows even when the grid covers fewer rows.
+    if (rows == w_rows) {
+        // The launch of src/ops.h:36-45 (ceil(w_rows / 8) groups of 256 threads) covers
+        // every row, so the output is a contiguous [T, w_rows]: the product of
+        // apex_nvfp4_matmul_f32, an MFMA GEMM at prefill token counts (fp32 x through
+        // its bf16 hi + lo split) and a GEMV below them.
+        matmul_impl(c.ptr[0], false, (const uint32_t *)c.ptr[1], (const uint8_t *)c.ptr[2], 1.0f,
+                    c.ptr[3], tokens, rows, K, c.stream);
+        return;
+    }
+    // A grid covering fewer rows than w_rows: those rows only, output rows strided by
+    // w_rows (shaders/matmul.metal:14-18 writes output[token * w_rows + row]).
     init_device_tuning();
     apex_hip::GemvArgs a{};
     a.x = c.ptr[0];
@@ -495,6 +523,7 @@ void launch_matmul_nvfp4(const LaunchCtx &c) {
     a.out_stride = w_rows;
     hip_check(apex_hip::gemv_launch(a, apex_hip::GemvMode::PlainF32, false, c.stream),
               "matmul_nvfp4 launch");
+    count_dispatch(kDispGemv);
 }
 
 void rms_norm_impl(const float *x, const uint16_t *w, float *y, uint32_t rows, uint32_t n,
@@ -1194,19 +1223,27 @@ int apex_hip_read_probe(const void *ptr, size_t bytes, uint32_t *sink, void *str
     });
 }
 
-int apex_hip_read_probe_sink_words(void) { return 8 * apex_hip::kNumCUs; }
+int apex_hip_read_probe_sink_words(void) { return 8 * apex_hip::num_cus(); }
 
 int apex_hip_set_gemm_min_tokens(uint32_t bf16_tokens, uint32_t f32_tokens) {
     return guard([&] {
-        g_gemm_min_tokens[0] = bf16_tokens;
-        g_gemm_min_tokens[1] = f32_tokens;
+        g_gemm_min_tokens[0].store(bf16_tokens, std::memory_order_relaxed);
+        g_gemm_min_tokens[1].store(f32_tokens, std::memory_order_relaxed);
+    });
+}
+
+int apex_hip_dense_dispatch_counts(uint64_t counts[4]) {
+    return guard([&] {
+        require(counts != nullptr, "counts is null");
+        for (int i = 0; i < kDispKinds; ++i)
+            counts[i] = g_dispatch[i].load(std::memory_order_relaxed);
     });
 }
 
 int apex_hip_set_gemv_waves_per_cu(int waves) {
     return guard([&] {
         require(waves >= 1 && waves <= 32, "waves per CU must be in [1, 32]");
-        apex_hip::kTargetWavesPerCU = waves;
+        apex_hip::kTargetWavesPerCU.store(waves, std::memory_order_relaxed);
     });
 }
 
@@ -1302,7 +1339,7 @@ int apex_experts_to_device(const char *path, uint64_t stride, uint64_t slot_byte
 int apex_hip_set_moe_path(int path) {
     return guard([&] {
         require(path >= 0 && path <= 2, "moe path must be 0 (by size), 1 (grouped GEMV) or 2 (grouped GEMM)");
-        apex_hip::kMoePath = path;
+        apex_hip::kMoePath.store(path, std::memory_order_relaxed);
     });
 }
 

@@ -46,7 +46,7 @@
 
 namespace apex_hip {
 
-int kMoePath = 0;
+std::atomic<int> kMoePath{0};
 
 namespace {
 
@@ -67,7 +67,6 @@ __device__ __forceinline__ float uniform_f(float v) {
     return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v)));
 }
 
-size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct PlanView {
     int32_t *hdr, *cnt, *off, *act, *pos_of_pair, *pair_of_pos, *tiles, *groups;
@@ -597,7 +596,7 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first) {
 // 2. moe_plan_scan_kernel (one workgroup): per expert, the exclusive scan of hist over
 //    the workgroups (written back in place) and the total count; plan_scan.
 // 3. moe_plan_scatter_kernel: pos = off[e] + hist[block][e] + rank, one pair per thread.
-constexpr uint32_t kRouteBlockTokens = 16; // one token per wave of a 1024-thread workgroup
+// kRouteBlockTokens (moe.h) tokens per workgroup: one per wave of 1024 threads
 
 __global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
     __shared__ unsigned long long mask[kMoeMaxExperts];
@@ -1354,31 +1353,6 @@ uint32_t gemv_slots(uint32_t K, int G) { return (K / 32 + G - 1) / G; }
 
 } // namespace
 
-MoeWorkspace moe_workspace(uint32_t T, uint32_t E, uint32_t k, uint32_t H, uint32_t I, bool gemm) {
-    MoeWorkspace w{};
-    const size_t P = (size_t)T * k;
-    w.max_tiles = (uint32_t)(P / 256 + (P < E ? P : E) + 1);
-    size_t off = 0;
-    w.ids = off;
-    off = align256(off + P * 4);
-    w.w = off;
-    off = align256(off + P * 4);
-    w.plan = off;
-    off = align256(off + 4 * ((size_t)kMoePlanHeader + 3 * E + 1 + 4 * P + 4 * (size_t)w.max_tiles));
-    w.h = off;
-    off = align256(off + P * I * 2);
-    w.d = off;
-    off = align256(off + P * H * 2);
-    if (gemm) { // prefill grouping: per-workgroup expert counts and in-workgroup ranks
-        w.hist = off;
-        off = align256(off + 4 * (size_t)E * ((T + kRouteBlockTokens - 1) / kRouteBlockTokens));
-        w.rank = off;
-        off = align256(off + 4 * P);
-    }
-    w.total = off;
-    return w;
-}
-
 bool moe_supported(const MoeArgs &a, bool gemm, const char **why) {
     auto no = [&](const char *m) {
         *why = m;
@@ -1448,11 +1422,22 @@ bool moe_router_supported(const MoeRouterArgs &a, const char **why) {
     return true;
 }
 
+// The largest dynamic LDS an instantiation can be launched with (hidden <= 4096,
+// experts <= 256, and never above kMaxDynLds: larger shapes take another tile size).
+// The kernel's limit is raised to it once, whatever the first call's shape.
+template <int TT, int WAVES> constexpr size_t router_lds_max() {
+    const size_t m = 4 * ((size_t)TT * kRouterMaxHidden + (size_t)TT * (kRouterMaxHidden / kQGroup) +
+                          (size_t)WAVES * TT * kMoeMaxExperts);
+    return m < kMaxDynLds ? m : kMaxDynLds;
+}
+
 template <int TT, int EPL, int WAVES>
 hipError_t router_launch(const MoeRouterArgs &a, hipStream_t stream) {
     static std::atomic<uint64_t> set{0};
     const size_t lds = router_lds<TT, WAVES>(a);
-    hipError_t e = set_lds(moe_router_kernel<TT, EPL, WAVES>, lds, set);
+    if (lds > router_lds_max<TT, WAVES>())
+        return hipErrorInvalidValue;
+    hipError_t e = set_lds(moe_router_kernel<TT, EPL, WAVES>, router_lds_max<TT, WAVES>(), set);
     if (e != hipSuccess)
         return e;
     hipLaunchKernelGGL((moe_router_kernel<TT, EPL, WAVES>), dim3((a.T + TT - 1) / TT),
@@ -1635,6 +1620,13 @@ uint32_t moe_router_mfma_splits(const MoeRouterArgs &a) {
     return s >= 1 ? s : 1;
 }
 
+bool moe_router_mfma_fits(const MoeRouterArgs &a) {
+    const uint32_t splits = moe_router_mfma_splits(a);
+    return (uint64_t)a.T * a.H * 4 < (1ull << 31) &&
+           (uint64_t)splits * a.T * a.E * 4 < (1ull << 31) &&
+           (a.H / kQGroup + splits - 1) / splits <= kRouterMfmaMaxSplitGroups;
+}
+
 hipError_t moe_router_mfma_launch(const MoeRouterArgs &a, const uint16_t *split, float *part,
                                   uint32_t splits, hipStream_t stream) {
     if (a.T == 0)
@@ -1646,8 +1638,11 @@ hipError_t moe_router_mfma_launch(const MoeRouterArgs &a, const uint16_t *split,
     // converted codes: the largest split's groups x 32 experts x 72 bf16
     const uint32_t ng = a.H / kQGroup, gmax = (ng + splits - 1) / splits;
     const size_t lds = (size_t)gmax * 32 * 72 * 2;
+    // the limit is raised once, to what the largest split needs (any shape)
     static std::atomic<uint64_t> attr{0};
-    if (hipError_t e = set_lds(moe_router_mfma_kernel, lds, attr); e != hipSuccess)
+    if (hipError_t e = set_lds(moe_router_mfma_kernel, (size_t)kRouterMfmaMaxSplitGroups * 32 * 72 * 2,
+                               attr);
+        e != hipSuccess)
         return e;
     hipLaunchKernelGGL(moe_router_mfma_kernel, dim3(8 * ((units + 7) / 8)), dim3(256), lds, stream,
                        a, split, part, splits);
@@ -1685,13 +1680,13 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
         return hipSuccess;
     if (!gemm) {
         hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(1024), 0, stream, a);
-        const dim3 grid((uint32_t)kNumCUs * kGemvBlocksPerCU), block(256);
+        const dim3 grid((uint32_t)num_cus() * kGemvBlocksPerCU), block(256);
         // gate/up: 32 lanes per row; x staged in LDS when it fits (one workgroup per
         // CU), else read per token from global memory
         const uint32_t xbytes = a.T * (a.H / 32 + 1) * 64;
         if (xbytes <= kXLdsBytes) {
             static std::atomic<uint64_t> attr[3] = {};
-            const dim3 lgrid((uint32_t)kNumCUs), lblock(kXLdsThreads);
+            const dim3 lgrid((uint32_t)num_cus()), lblock(kXLdsThreads);
             hipError_t err = hipSuccess;
             switch (gemv_slots(a.H, 32)) {
             case 1:

@@ -99,6 +99,7 @@ _PROTOS = {
     "apex_hip_read_probe_sink_words": (_I, []),
     "apex_hip_set_gemv_waves_per_cu": (_I, [_I]),
     "apex_hip_set_gemm_min_tokens": (_I, [_U32, _U32]),
+    "apex_hip_dense_dispatch_counts": (_I, [_P]),
     "apex_moe_route_bf16": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
     "apex_moe_workspace_bytes": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
     "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
@@ -333,6 +334,13 @@ def set_gemv_waves_per_cu(waves: int) -> None:
 def set_gemm_min_tokens(bf16_tokens: int = 0, f32_tokens: int = 0) -> None:
     """Tokens from which the dense matmul / GeGLU run as MFMA GEMMs (0: by size)."""
     check(lib().apex_hip_set_gemm_min_tokens(bf16_tokens, f32_tokens))
+
+
+def dense_dispatch_counts() -> dict:
+    """Dense-product launches of this process so far, by form."""
+    c = (C.c_uint64 * 4)()
+    check(lib().apex_hip_dense_dispatch_counts(C.cast(c, C.c_void_p)))
+    return {"gemv": c[0], "gemm": c[1], "splitk_gemm": c[2], "f32_split": c[3]}
 
 
 # ---- MoE expert FFN --------------------------------------------------------------

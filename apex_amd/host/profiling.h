@@ -11,6 +11,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 namespace apex {
 
@@ -76,63 +77,83 @@ class MemoryTracker {
     uint64_t total_ = 0, peak_ = 0;
 };
 
-struct PhaseStats {
-    double total_ms = 0.0, max_ms = 0.0;
-    long calls = 0;
-};
-
-// Accumulated wall time per named phase.
+// Wall-clock accounting per named phase ("gpu_sync" around Backend::sync, "mmap",
+// ...).  Timer scopes report into the process-wide Profile; phases keep the order in
+// which they first appeared.  Durations are kept as integer nanoseconds, so sums do
+// not drift however many calls a phase collects.
 class Profile {
   public:
+    struct Phase {
+        uint64_t count = 0;
+        uint64_t total_ns = 0;
+        uint64_t shortest_ns = UINT64_MAX;
+        uint64_t longest_ns = 0;
+        double mean_ms() const { return count ? total_ns / 1e6 / count : 0.0; }
+    };
+
     static Profile &get() {
         static Profile p;
         return p;
     }
+    // One call of `phase` that took `ms` milliseconds.
     void add(const std::string &phase, double ms) {
+        const uint64_t ns = ms > 0.0 ? (uint64_t)(ms * 1e6 + 0.5) : 0;
         std::lock_guard<std::mutex> lock(mu_);
-        PhaseStats &s = stats_[phase];
-        s.total_ms += ms;
-        s.calls++;
-        if (ms > s.max_ms)
-            s.max_ms = ms;
+        Phase &p = slot(phase);
+        p.count += 1;
+        p.total_ns += ns;
+        p.shortest_ns = ns < p.shortest_ns ? ns : p.shortest_ns;
+        p.longest_ns = ns > p.longest_ns ? ns : p.longest_ns;
     }
-    PhaseStats stats(const std::string &phase) {
+    // A copy of one phase's record (all zero if it never ran).
+    Phase phase(const std::string &name) {
         std::lock_guard<std::mutex> lock(mu_);
-        return stats_[phase];
+        for (const auto &e : phases_)
+            if (e.first == name)
+                return e.second;
+        return Phase{};
     }
     void reset() {
         std::lock_guard<std::mutex> lock(mu_);
-        stats_.clear();
+        phases_.clear();
     }
+    // One line per phase: calls, total, mean, shortest and longest call.
     void print(FILE *out = stderr) {
         std::lock_guard<std::mutex> lock(mu_);
-        std::fprintf(out, "%-24s %10s %8s %10s %10s\n", "phase", "total ms", "calls", "avg ms",
-                     "max ms");
-        for (const auto &[name, s] : stats_)
-            std::fprintf(out, "%-24s %10.2f %8ld %10.3f %10.3f\n", name.c_str(), s.total_ms,
-                         s.calls, s.total_ms / s.calls, s.max_ms);
+        for (const auto &[name, p] : phases_)
+            std::fprintf(out, "[time] %s: %llu call%s, %.3f ms in all, %.3f ms each (%.3f .. %.3f)\n",
+                         name.c_str(), (unsigned long long)p.count, p.count == 1 ? "" : "s",
+                         p.total_ns / 1e6, p.mean_ms(), p.shortest_ns / 1e6, p.longest_ns / 1e6);
     }
 
   private:
+    Phase &slot(const std::string &name) {
+        for (auto &e : phases_)
+            if (e.first == name)
+                return e.second;
+        phases_.emplace_back(name, Phase{});
+        return phases_.back().second;
+    }
     std::mutex mu_;
-    std::map<std::string, PhaseStats> stats_;
+    std::vector<std::pair<std::string, Phase>> phases_;
 };
 
-// Scope timer: adds the elapsed time to Profile under its name when destroyed.
+// Times the enclosing scope: on destruction the elapsed steady-clock time is added
+// to Profile::get() under the timer's phase name.
 class Timer {
   public:
-    explicit Timer(std::string name)
-        : name_(std::move(name)), start_(std::chrono::steady_clock::now()) {}
+    explicit Timer(std::string phase) : phase_(std::move(phase)), t0_(Clock::now()) {}
     Timer(const Timer &) = delete;
     Timer &operator=(const Timer &) = delete;
-    ~Timer() {
-        const auto end = std::chrono::steady_clock::now();
-        Profile::get().add(name_, std::chrono::duration<double, std::milli>(end - start_).count());
+    ~Timer() { Profile::get().add(phase_, elapsed_ms()); }
+    double elapsed_ms() const {
+        return std::chrono::duration<double, std::milli>(Clock::now() - t0_).count();
     }
 
   private:
-    std::string name_;
-    std::chrono::steady_clock::time_point start_;
+    using Clock = std::chrono::steady_clock;
+    std::string phase_;
+    Clock::time_point t0_;
 };
 
 } // namespace apex

@@ -13,11 +13,14 @@ them from HBM.  Steps are timed with HIP events recorded on the launch stream.
 Prints one JSON line: value = algorithmic bytes per step / average step time (GB/s).
 The roofline object prices the same kernel against MI355X's 8 TB/s HBM peak; the
 cpu_baseline object times the reference's own CPU implementation of the op
-(src/tests/cpu_ref.h matvecNvfp4Cpu + geluTanh, compiled from its sources) on a
-bounded sample, single-threaded like the reference.
+(src/tests/cpu_ref.h matvecNvfp4Cpu + geluTanh, compiled from its sources), single-
+threaded like the reference: the headline workload, and under "configs" every
+workload of the path in its GPU record's unit (the two prefill workloads on stated
+slices, extrapolated).
 
 The "secondary" object carries the metric's second half and the other workloads of
-the path, each timed the same way (HIP events around back-to-back steps):
+the path, each timed the same way (HIP events around back-to-back steps; at least 10
+launches and 20 ms of GPU time per record, the count in its "steps"):
   moe_prefill   MoE layer prefill: 4096 tokens, hidden 2816, 128 experts, top-8,
                 intermediate 704, Zipf(1.1) routing -> TFLOP/s vs the 2.5 PFLOP/s
                 dense bf16 MFMA peak (flops of the routed pairs only);
@@ -102,55 +105,166 @@ def time_geglu(steps: int, warmup: int, rows=21504, K=5376):
     }
 
 
-def cpu_baseline_geglu(budget_s: float = 10.0, rows=21504, K=5376):
-    """The reference's CPU op on the same workload: gate and up matvecNvfp4Cpu
-    (fp64 accumulation, single thread) and geluTanh, over a row sample sized to the
-    time budget; throughput in the same unit (algorithmic GB/s)."""
+# ---- CPU baseline: the reference's own CPU code on every workload ------------------
+
+def _cpu_ops():
+    """(kind, matvec, geglu, moe_ffn): the reference's matvecNvfp4Cpu / geluTanh compiled
+    from its sources (src/tests/cpu_ref.h) where available ("reference"), else the
+    oracle's restatement of the same arithmetic ("port").  Single-threaded, as the
+    reference is (src/tests/cpu_ref.h:50-63)."""
     import oracle  # the oracle / reference CPU code is the checker and the baseline only
 
-    x, gate, up, algo_bytes, _ = geglu_workload(rows, K)
-    xf = synth.bf16_to_f32(x)
-    kind = "reference" if oracle.ref_available() else "port"
-    mv = oracle.ref_matvec if kind == "reference" else (lambda c, s, v: oracle.matvec(c, s, v))
-    gelu = oracle.ref().ref_gelu_tanh if kind == "reference" else oracle.gelu
-    # calibrate on 256 rows, then run a sample sized to the budget
-    t = time.perf_counter()
-    mv(gate.codes[:256], gate.scales[:256], xf)
-    per_row = (time.perf_counter() - t) / 256
-    n = int(min(rows, max(256, budget_s / (2 * per_row))))
-    reps = 0
-    t = time.perf_counter()
+    if oracle.ref_available():
+        return ("reference", oracle.ref_matvec,
+                lambda g, u, x: oracle.ref_geglu(g, u, x),
+                lambda slots, x, ids, w, E: oracle.ref_moe_ffn(slots, x, ids, w, E))
+    return ("port", lambda c, s, x: oracle.matvec(c, s, x),
+            lambda g, u, x: oracle.geglu(oracle.matvec(*g, x), oracle.matvec(*u, x)),
+            lambda slots, x, ids, w, E: oracle.moe_ffn(slots, x, ids, w))
+
+
+def _repeat(fn, budget_s):
+    """Run fn() until budget_s has elapsed (at least once): (seconds per call, calls)."""
+    n, t0 = 0, time.perf_counter()
     while True:
-        g = mv(gate.codes[:n], gate.scales[:n], xf)
-        u = mv(up.codes[:n], up.scales[:n], xf)
-        h = np.array([gelu(float(a)) for a in g.ravel()], np.float32) * u.ravel()
-        reps += 1
-        if time.perf_counter() - t >= budget_s:
-            break
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            return dt / n, n
+
+
+def cpu_baselines(budget_s: float = 4.0):
+    """The reference's CPU implementation timed on every workload of the path, on this
+    host, one core, in the unit of the workload's GPU record.  Configurations 0-2 run
+    whole; 3 (dense prefill GEMM) runs a slice of weight rows for all 2048 tokens and
+    4 (MoE prefill) two slices of tokens: both products are linear in those rows /
+    tokens, so the full-size time is extrapolated (for 4 along the line through the two
+    slices, which keeps the per-expert row decodes a slice pays once out of the slope)."""
+    import oracle
+    kind, mv, geglu, moe = _cpu_ops()
+    nproc = os.cpu_count()
+    out = {}
+
+    def rec(value, unit, sample):
+        return {"value": value, "unit": unit, "cores": 1, "kind": kind,
+                "sample": f"{sample}; single-threaded, host nproc={nproc}"}
+
+    # 0: GEMV 2048 x 2048, bf16 x (widened exactly), batch 1
+    x, w = synth.gemv_case(seed=0)
+    xf = synth.bf16_to_f32(x)
+    algo = w.codes.nbytes + w.scales.nbytes + x.nbytes + w.rows * 2
+    sec, n = _repeat(lambda: mv(w.codes, w.scales, xf), budget_s / 4)
+    out["gemv_2048"] = rec(round(algo / sec / 1e9, 4), "GB/s",
+                           f"config 0 whole: matvecNvfp4Cpu 2048x2048, batch 1, {n} calls, "
+                           f"{sec * 1e3:.2f} ms each")
+
+    # 1: decode fused GeGLU 2 x [21504 x 5376], batch 1 (the headline workload)
+    x, gate, up, algo, _ = geglu_workload()
+    xf = synth.bf16_to_f32(x)
+    sec, n = _repeat(lambda: geglu((gate.codes, gate.scales), (up.codes, up.scales), xf), budget_s)
+    out["geglu_decode"] = rec(round(algo / sec / 1e9, 4), "GB/s",
+                              f"config 1 whole: gate and up matvecNvfp4Cpu [21504x5376] + "
+                              f"geluTanh(gate) * up, batch 1, {n} calls, {sec:.2f} s each")
+
+    # 2: MoE decode, 16 tokens
+    x, logits, slots = _case("moe_decode")
+    T, H, E, I = x.shape[0], x.shape[1], logits.shape[1], slots.I
+    ids, wts = oracle.moe_route(synth.bf16_to_f32(logits), 8)
+    U = len(np.unique(ids))
+    algo = U * 3 * (I * H // 2 + I * H // 16) + x.nbytes + logits.nbytes + T * H * 2
+    xf = synth.bf16_to_f32(x)
+    sec, n = _repeat(lambda: moe(slots, xf, ids, wts, E), budget_s / 2)
+    out["moe_decode"] = rec(round(algo / sec / 1e9, 4), "GB/s",
+                            f"config 2 whole: 16 tokens x top-8 over {U} experts, per expert "
+                            f"gate/up/down matvecNvfp4Cpu + geluTanh, weighted sum; {n} calls, "
+                            f"{sec:.2f} s each")
+
+    # 3: prefill GEMM 2048 x 21504 x 5376 on a slice of W's rows
+    A, w = _case("gemm")
+    Af = synth.bf16_to_f32(A)
+    M, N, K = A.shape[0], w.rows, w.K
+    t = time.perf_counter()
+    mv(w.codes[:4], w.scales[:4], Af)
+    per_row = (time.perf_counter() - t) / 4
+    rows = int(min(N, max(8, budget_s / per_row)))
+    t = time.perf_counter()
+    mv(w.codes[:rows], w.scales[:rows], Af)
     dt = time.perf_counter() - t
-    bytes_per_row = (algo_bytes - xf.size * 2 - rows * 2) / rows
-    sample_bytes = reps * (n * bytes_per_row + x.nbytes + n * 2)
-    return {
-        "value": round(sample_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
-        "sample": f"decode GeGLU, gate+up rows 0..{n - 1} of {rows} (K={K}), batch 1, "
-                  f"{reps} pass(es) in {dt:.1f} s single-threaded, host nproc={os.cpu_count()}",
-        "_h": h,
-    }
+    full = dt * N / rows
+    out["gemm_prefill"] = rec(round(2.0 * M * N * K / full / 1e12, 6), "TFLOP/s",
+                              f"config 3 slice: rows 0..{rows - 1} of {N} x all {M} tokens "
+                              f"(K={K}) in {dt:.2f} s, extrapolated x{N / rows:.1f} to "
+                              f"{full:.0f} s for the whole GEMM")
+
+    # 4: MoE prefill, 4096 tokens, on two slices of tokens
+    x, logits, slots = _case("moe_prefill")
+    T, H, E, I = x.shape[0], x.shape[1], logits.shape[1], slots.I
+    ids, wts = oracle.moe_route(synth.bf16_to_f32(logits), 8)
+    xf = synth.bf16_to_f32(x)
+
+    def slice_time(nt):
+        t = time.perf_counter()
+        moe(slots, xf[:nt], ids[:nt], wts[:nt], E)
+        return time.perf_counter() - t
+
+    t4 = slice_time(4)
+    n1 = int(max(8, min(T // 4, budget_s / 4 / max(t4 / 4, 1e-6))))
+    n2 = 3 * n1
+    t1, t2 = slice_time(n1), slice_time(n2)
+    slope = (t2 - t1) / (n2 - n1)
+    full = t1 + slope * (T - n1)
+    flops = 2.0 * T * 8 * 3 * H * I
+    out["moe_prefill"] = rec(round(flops / full / 1e12, 6), "TFLOP/s",
+                             f"config 4 slices: tokens 0..{n1 - 1} in {t1:.2f} s and 0..{n2 - 1} "
+                             f"in {t2:.2f} s (experts grouped, gate/up/down matvecNvfp4Cpu + "
+                             f"geluTanh), the line through both extrapolated to all {T} tokens: "
+                             f"{full:.0f} s")
+    return out
 
 
-def time_steps(step, steps, warmup, stream):
-    """Average seconds per step of `step(i)` launched back to back on `stream`."""
-    for i in range(warmup):
-        step(i)
+# ---- GPU timing -----------------------------------------------------------------------
+
+# every secondary record times at least this many launches and this much GPU time
+MIN_TIMED_STEPS = 10
+MIN_TIMED_MS = 20.0
+
+
+def time_steps(step, steps, warmup, stream, min_steps=MIN_TIMED_STEPS, min_ms=MIN_TIMED_MS):
+    """Seconds per step of `step(i)` launched back to back on `stream`, and the number of
+    steps timed: `warmup` untimed steps, then max(steps, min_steps) timed steps, more if
+    needed to cover min_ms of GPU time (estimated from the warmup)."""
+    warmup = max(1, warmup)
     stream.synchronize()
-    hip.synchronize()
     e0, e1 = hip.Event(), hip.Event()
     e0.record(stream)
-    for i in range(steps):
+    for i in range(warmup):
         step(i)
     e1.record(stream)
     e1.synchronize()
-    return e0.elapsed_ms(e1) / 1e3 / steps
+    est_ms = e0.elapsed_ms(e1) / warmup
+    n = max(steps, min_steps)
+    if est_ms > 0:
+        n = max(n, int(np.ceil(min_ms / est_ms)))
+    hip.synchronize()
+    e0.record(stream)
+    for i in range(n):
+        step(i)
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / 1e3 / n, n
+
+
+_CASE_CACHE = {}
+
+
+def _case(name):
+    """Seeded synthetic workloads shared by the GPU records and the CPU baselines."""
+    if name not in _CASE_CACHE:
+        _CASE_CACHE[name] = {"moe_decode": lambda: synth.moe_decode_case(seed=0),
+                             "moe_prefill": lambda: synth.moe_prefill_case(seed=0),
+                             "gemm": lambda: synth.gemm_case(seed=0)}[name]()
+    return _CASE_CACHE[name]
 
 
 def moe_setup(case, copies):
@@ -171,7 +285,7 @@ def moe_setup(case, copies):
 
 
 def time_moe_decode(steps, warmup):
-    case = synth.moe_decode_case(seed=0)
+    case = _case("moe_decode")
     x, logits, slots = case
     T, H, E, I = x.shape[0], x.shape[1], logits.shape[1], slots.I
     # distinct experts the step streams: from the library's own router
@@ -189,10 +303,10 @@ def time_moe_decode(steps, warmup):
     def step(i):
         hip.moe_ffn_bf16(dx, dl, ms[i % copies], y, T, E, 8, H, I, ws, stream=stream)
 
-    sec = time_steps(step, steps, warmup, stream)
+    sec, nsteps = time_steps(step, steps, warmup, stream)
     stream.close()
     gbs = algo / sec / 1e9
-    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(sec * 1e3, 6),
+    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
             "roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(algo),
             "distinct_experts": int(U), "slot_copies_rotated": copies,
             "workload": "MoE decode: x bf16 [16,2816], logits bf16 [16,128], top-8, 128 "
@@ -202,7 +316,7 @@ def time_moe_decode(steps, warmup):
 
 
 def time_moe_prefill(steps, warmup):
-    case = synth.moe_prefill_case(seed=0)
+    case = _case("moe_prefill")
     x, logits, slots = case
     T, H, E, I = x.shape[0], x.shape[1], logits.shape[1], slots.I
     flops = 2.0 * T * 8 * 3 * H * I
@@ -212,19 +326,21 @@ def time_moe_prefill(steps, warmup):
     def step(i):
         hip.moe_ffn_bf16(dx, dl, ms[0], y, T, E, 8, H, I, ws, stream=stream)
 
-    sec = time_steps(step, steps, warmup, stream)
+    sec, nsteps = time_steps(step, steps, warmup, stream)
     stream.close()
     tf = flops / sec / 1e12
-    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
+    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
             "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(flops),
             "workload": "MoE prefill: x bf16 [4096,2816], Zipf(1.1) routing over 128 experts "
                         "(8 empty), top-8, NVFP4 gate/up [704x2816], down [2816x704], y bf16",
-            "path": "route, plan, grouped MFMA GEMM gate/up with GeGLU epilogue, grouped "
-                    "MFMA GEMM down, weighted combine (5 launches)"}
+            "path": "route + per-workgroup expert masks, plan scan, position scatter, "
+                    "grouped MFMA GEMM gate/up with GeGLU epilogue, grouped MFMA GEMM down, "
+                    "weighted combine (6 launches)"}
 
 
 def time_gemm_prefill(steps, warmup, M=2048, N=21504, K=5376):
-    A, w = synth.gemm_case(seed=0, M=M, N=N, K=K)
+    A, w = _case("gemm") if (M, N, K) == (2048, 21504, 5376) else \
+        synth.gemm_case(seed=0, M=M, N=N, K=K)
     dA = hip.DeviceArray.from_numpy(A)
     dc, ds = hip.DeviceArray.from_numpy(w.codes), hip.DeviceArray.from_numpy(w.scales)
     C = hip.DeviceArray((M, N), np.uint16)
@@ -233,15 +349,16 @@ def time_gemm_prefill(steps, warmup, M=2048, N=21504, K=5376):
     def step(i):
         hip.nvfp4_gemm_bf16(dA, dc, ds, C, M, N, K, stream=stream)
 
-    sec = time_steps(step, steps, warmup, stream)
+    sec, nsteps = time_steps(step, steps, warmup, stream)
     stream.close()
     for a in (dA, dc, ds, C):
         a.close()
     tf = 2.0 * M * N * K / sec / 1e12
-    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
+    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
             "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(2 * M * N * K),
             "workload": f"prefill GEMM: A bf16 [{M},{K}] x NVFP4 W [{N}x{K}]^T -> C bf16 [{M},{N}]",
-            "yardstick_vendor_bf16_gemm_tflops": vendor_bf16_gemm(M, N, K, steps, warmup)}
+            "yardstick_vendor_bf16_gemm_tflops": vendor_bf16_gemm(M, N, K, max(steps, 60),
+                                                                  max(warmup, 5))}
 
 
 def time_dense_prefill(steps, warmup, T=2048, N=21504, K=5376):
@@ -265,9 +382,9 @@ def time_dense_prefill(steps, warmup, T=2048, N=21504, K=5376):
          lambda i: hip.nvfp4_matmul_f32(xf, dw[0], dw[1], yf, T, N, K, stream=stream),
          f"prefill matmul, fp32 contract: x fp32 [{T},{K}] x NVFP4 [{N}x{K}]^T -> fp32 "
          f"[{T},{N}] (bf16 hi + lo split, 2x MFMA work)")]:
-        sec = time_steps(fn, steps, warmup, stream)
+        sec, nsteps = time_steps(fn, steps, warmup, stream)
         tf = flops / sec / 1e12
-        out[name] = {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
+        out[name] = {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
                      "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(flops),
                      "workload": text}
     stream.close()
@@ -292,13 +409,13 @@ def time_dense_mlp_prefill(steps, warmup, T=512, H=2816, I=2112):
         hip.nvfp4_geglu_rms_norm_f32(dh, dnw, 1e-6, gc, gs, uc, us, hh, T, I, H, stream=stream)
         hip.nvfp4_matmul_f32(hh, dc, ds, y, T, H, I, stream=stream)
 
-    sec = time_steps(step, steps, warmup, stream)
+    sec, nsteps = time_steps(step, steps, warmup, stream)
     stream.close()
     for a in arrs + [hh, y]:
         a.close()
     flops = 2.0 * T * (2 * I * H + H * I)
     tf = flops / sec / 1e12
-    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6),
+    return {"value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
             "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(flops),
             "workload": f"dense MLP prefill, fp32: {T} tokens, RMSNorm [{H}] fused into GeGLU "
                         f"NVFP4 [{I}x{H}] x2, down NVFP4 [{H}x{I}] (GEMMs: split pass, split-K)"}
@@ -316,11 +433,11 @@ def time_norms(steps, warmup, T=4096, H=2816, heads=16, D=256):
     dx, dw, dy = (hip.DeviceArray.from_numpy(x), hip.DeviceArray.from_numpy(w),
                   hip.DeviceArray((T, H), np.float32))
     stream = hip.Stream()
-    sec = time_steps(lambda i: hip.rms_norm_f32(dx, dw, dy, T, H, 1e-6, stream=stream), steps,
+    sec, nsteps = time_steps(lambda i: hip.rms_norm_f32(dx, dw, dy, T, H, 1e-6, stream=stream), steps,
                      warmup, stream)
     algo = 2 * x.nbytes + w.nbytes
     out["rms_norm"] = {"value": round(algo / sec / 1e9, 2), "unit": "GB/s",
-                       "ms_per_step": round(sec * 1e3, 6),
+                       "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
                        "roofline_frac": round(algo / sec / 1e9 / HBM_PEAK_GBS, 4),
                        "algorithmic_bytes": int(algo),
                        "workload": f"rms_norm_f32: x fp32 [{T},{H}], bf16 weights [{H}]"}
@@ -328,12 +445,12 @@ def time_norms(steps, warmup, T=4096, H=2816, heads=16, D=256):
     hw = synth.bf16_from_f32((1 + 0.1 * rng.standard_normal(D)).astype(np.float32))
     dq, dhw, do = (hip.DeviceArray.from_numpy(q), hip.DeviceArray.from_numpy(hw),
                    hip.DeviceArray(q.shape, np.float32))
-    sec = time_steps(lambda i: hip.head_norm_rope_f32(dq, dhw, do, T, heads, D, D // 2, 10000.0,
+    sec, nsteps = time_steps(lambda i: hip.head_norm_rope_f32(dq, dhw, do, T, heads, D, D // 2, 10000.0,
                                                       0, heads * D, D, 1e-6, stream=stream),
                      steps, warmup, stream)
     algo = 2 * q.nbytes + hw.nbytes
     out["head_norm_rope"] = {"value": round(algo / sec / 1e9, 2), "unit": "GB/s",
-                             "ms_per_step": round(sec * 1e3, 6),
+                             "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
                              "roofline_frac": round(algo / sec / 1e9 / HBM_PEAK_GBS, 4),
                              "algorithmic_bytes": int(algo),
                              "workload": f"head_norm_rope_f32: q fp32 [{T},{heads},{D}], "
@@ -371,7 +488,7 @@ def time_dense_mlp_decode(steps, warmup, H=2816, I=2112):
         hip.nvfp4_geglu_rms_norm_f32(dh, dnw, 1e-6, gc, gs, uc, us, hh, 1, I, H, stream=stream)
         hip.nvfp4_matmul_f32(hh, dc, ds, y, 1, H, I, stream=stream)
 
-    sec = time_steps(step, steps, warmup, stream)
+    sec, nsteps = time_steps(step, steps, warmup, stream)
     stream.close()
     for arrs in sets:
         for a in arrs:
@@ -379,7 +496,7 @@ def time_dense_mlp_decode(steps, warmup, H=2816, I=2112):
     for a in (dh, dnw, hh, y):
         a.close()
     gbs = algo / sec / 1e9
-    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(sec * 1e3, 6),
+    return {"value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
             "roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(algo),
             "weight_copies_rotated": copies,
             "workload": f"dense MLP decode, batch 1, fp32: RMSNorm [1,{H}] fused into GeGLU "
@@ -395,13 +512,13 @@ def time_router(steps, warmup, E=128, H=2816):
         arrs = [hip.DeviceArray.from_numpy(a) for a in (h, rw.norm_w, rw.qw, rw.qs, rw.qb)]
         lg = hip.DeviceArray((T, E), np.float32)
         stream = hip.Stream()
-        sec = time_steps(lambda i: hip.moe_router_logits_q8(*arrs, lg, T, E, H, 1e-6,
+        sec, nsteps = time_steps(lambda i: hip.moe_router_logits_q8(*arrs, lg, T, E, H, 1e-6,
                                                             stream=stream), steps, warmup, stream)
         stream.close()
         for a in arrs + [lg]:
             a.close()
         out[name] = {"value": round(2.0 * T * E * H / sec / 1e12, 3), "unit": "TFLOP/s",
-                     "ms_per_step": round(sec * 1e3, 6),
+                     "ms_per_step": round(sec * 1e3, 6), "steps": nsteps,
                      "workload": f"router logits: h fp32 [{T},{H}], affine q8 [{E}x{H}] "
                                  f"(group 64), fp32 out [{T},{E}]"}
     return out
@@ -491,7 +608,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-budget", type=float, default=4.0,
+                    help="seconds of CPU time per baseline configuration (about)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="time only the headline fused-GeGLU workload")
     ap.add_argument("--calibrate", action="store_true",
@@ -549,23 +667,23 @@ def main(argv=None):
         },
     }
     if not args.no_secondary:
-        sec_steps = max(1, args.steps // 100)
-        sec_warm = max(1, args.warmup // 100)
+        # each record: at least MIN_TIMED_STEPS launches and MIN_TIMED_MS of GPU time
+        sec_steps, sec_warm = max(1, args.steps // 100), max(2, args.warmup // 100)
+        dec_steps, dec_warm = max(1, args.steps // 10), max(2, args.warmup // 10)
         line["secondary"] = {
             "moe_prefill": time_moe_prefill(sec_steps, sec_warm),
             "gemm_prefill": time_gemm_prefill(sec_steps, sec_warm),
             **time_dense_prefill(sec_steps, sec_warm),
-            "moe_decode": time_moe_decode(max(1, args.steps // 10), max(1, args.warmup // 10)),
+            "moe_decode": time_moe_decode(dec_steps, dec_warm),
         }
-        line["secondary"].update(time_norms(max(1, args.steps // 10), max(1, args.warmup // 10)))
-        line["secondary"]["dense_mlp_decode"] = time_dense_mlp_decode(
-            max(1, args.steps // 10), max(1, args.warmup // 10))
-        line["secondary"].update(time_router(max(1, args.steps // 100), max(1, args.warmup // 100)))
+        line["secondary"].update(time_norms(dec_steps, dec_warm))
+        line["secondary"]["dense_mlp_decode"] = time_dense_mlp_decode(dec_steps, dec_warm)
+        line["secondary"].update(time_router(sec_steps, sec_warm))
         line["secondary"]["slot_streaming"] = time_slot_streaming()
     if not args.no_cpu:
-        cb = cpu_baseline_geglu(args.cpu_budget)
-        cb.pop("_h")
-        line["cpu_baseline"] = cb
+        cpu = cpu_baselines(args.cpu_budget)
+        # the headline workload's line first, then every configuration's
+        line["cpu_baseline"] = {**cpu["geglu_decode"], "configs": cpu}
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -105,10 +105,14 @@ int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
  * with positional arguments.  Returns at once; kernels run in queue order.
  * Kernels and argument lists (B = buffer, U = uint32 value, F = float value):
  *   matmul_nvfp4      B input f32 [T,K], B weights u32 [rows,K/8], B scales u8
- *                     [rows,K/16], B output f32 [T,rows], U hidden_dim K, U w_rows.
+ *                     [rows,K/16], B output f32 [T,w_rows], U hidden_dim K, U w_rows.
  *                     T = threadgroups.y and rows covered = min(w_rows,
  *                     threadgroups.x * threads/32), as the reference launch
- *                     (src/ops.h:34-46, shaders/matmul.metal:14-18) implies.
+ *                     (src/ops.h:34-46, shaders/matmul.metal:14-18) implies.  A grid
+ *                     covering every row (the reference's ceil(w_rows/8) x 256) runs
+ *                     apex_nvfp4_matmul_f32: an MFMA GEMM at prefill token counts, a
+ *                     GEMV below them; a grid covering fewer rows runs the GEMV on
+ *                     those rows (output rows strided by w_rows).
  *   geglu_f32         B gate, B up, B output, U count (in place allowed);
  *                     src/ops.h:48-55, shaders/geglu.metal:6-24.
  *   matmul_nvfp4_bf16 B input bf16 [T,K], B weights, B scales, B output bf16 [T,rows],
@@ -301,6 +305,12 @@ int apex_hip_set_gemv_waves_per_cu(int waves);
  * device, grown on demand (growing synchronises the calling stream) and held until the
  * process ends; uses from different streams are ordered on the GPU by an event. */
 int apex_hip_set_gemm_min_tokens(uint32_t bf16_tokens, uint32_t f32_tokens);
+
+/* Dense-product launches this process has made, by form, counted when the matmul and
+ * GeGLU entry points and registry kernels (matmul_nvfp4, geglu_nvfp4_*, ...) enqueue
+ * them: counts[0] GEMVs, [1] MFMA GEMMs, [2] split-K MFMA GEMMs, [3] fp32 hi + lo split
+ * passes.  Lets a host see which form a call took; no device needed. */
+int apex_hip_dense_dispatch_counts(uint64_t counts[4]);
 
 /* ---- MoE expert FFN (no reference kernel) ------------------------------------------
  * Semantics: tools/dump_reference.py:208-219 (router top-k, experts combined with the

@@ -250,6 +250,9 @@ def ref():
         R.ref_gelu_tanh.argtypes = [_F]
         R.ref_diff.argtypes = [_P, _P, _SZ, C.POINTER(C.c_double), C.POINTER(C.c_double)]
         R.ref_rms_norm.argtypes = [_P, _P, _P, _SZ, _F]
+        R.ref_geglu.argtypes = [_P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ]
+        R.ref_moe_ffn.argtypes = [_P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _SZ, _SZ,
+                                  _SZ, _SZ, _SZ]
         _ref = R
     return _ref
 
@@ -282,4 +285,34 @@ def ref_rms_norm(x, w_bf16, eps: float) -> np.ndarray:
     n = x.shape[1]
     for r in range(x.shape[0]):
         ref().ref_rms_norm(px + r * n * 4, pw, y[r].ctypes.data, n, eps)
+    return y
+
+
+def ref_geglu(gate, up, x) -> np.ndarray:
+    """gelu_tanh(Wg x) * (Wu x) with the reference's matvecNvfp4Cpu and geluTanh;
+    gate/up are (codes, scales) pairs, x fp32 [T, K] -> fp32 [T, rows]."""
+    gc, pgc = _c(gate[0], np.uint32)
+    gs, pgs = _c(gate[1], np.uint8)
+    uc, puc = _c(up[0], np.uint32)
+    us, pus = _c(up[1], np.uint8)
+    x, px = _c(np.atleast_2d(x), np.float32)
+    rows, K = gc.shape[0], gc.shape[1] * 8
+    out = np.empty((x.shape[0], rows), np.float32)
+    ref().ref_geglu(pgc, pgs, puc, pus, px, out.ctypes.data, x.shape[0], rows, K)
+    return out
+
+
+def ref_moe_ffn(slots, x, ids, weights, experts: int) -> np.ndarray:
+    """The MoE expert FFN with the reference's CPU functions (tokens grouped per expert);
+    slots: apex_amd.synth.ExpertSlots, x fp32 [T, H], ids / weights [T, k] -> fp32 [T, H]."""
+    data, pd = _c(slots.data, np.uint8)
+    x, px = _c(np.atleast_2d(x), np.float32)
+    ids, pi = _c(ids, np.int32)
+    w, pw = _c(weights, np.float32)
+    o = slots.offsets
+    T, k = ids.shape
+    y = np.empty((T, slots.H), np.float32)
+    ref().ref_moe_ffn(pd, slots.stride, o["gate_w"], o["gate_s"], o["up_w"], o["up_s"],
+                      o["down_w"], o["down_s"], px, pi, pw, y.ctypes.data, T, k, experts,
+                      slots.H, slots.I)
     return y

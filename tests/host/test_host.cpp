@@ -16,6 +16,7 @@
 #include <string>
 #include <vector>
 
+#include "apex_hip.h"
 #include "hip_backend.h"
 #include "model_info.h"
 #include "model_loader.h"
@@ -167,34 +168,55 @@ void test_dense_mlp(HipBackend &be) {
         be.release(b);
 }
 
-// The reference-named launches at a prefill token count, where matmul_nvfp4 and the
-// fused GeGLU run as MFMA GEMMs (fp32 x through its bf16 hi + lo split; split-K for
-// these few tiles): the same reference gate as the decode sizes.
+// MFMA GEMM launches (plain and split-K) made by the library so far.
+uint64_t gemm_launches() {
+    uint64_t c[4] = {};
+    if (apex_hip_dense_dispatch_counts(c) != APEX_HIP_OK)
+        return 0;
+    return c[1] + c[2];
+}
+
+// The reference-named launches at prefill token counts: denseMlp queues matmul_nvfp4
+// with the reference's grid (src/ops.h:34-46, 61-69), which covers every row, so each
+// of its three products runs as an MFMA GEMM (fp32 x through its bf16 hi + lo split;
+// split-K for these few tiles), checked by the library's launch counts, at the same
+// reference gate as the decode sizes.
 void test_dense_prefill(HipBackend &be) {
     Rng rng{11};
-    const uint32_t H = 1024, I = 512, T = 128;
+    const uint32_t H = 1024, I = 512;
     HostMatrix g = random_matrix(rng, I, H), u = random_matrix(rng, I, H), d = random_matrix(rng, H, I);
-    std::vector<float> x((size_t)T * H);
-    for (auto &v : x)
-        v = rng.normal();
-    std::vector<float> want((size_t)T * H);
-    orc_dense_mlp(g.codes.data(), g.scales.data(), u.codes.data(), u.scales.data(), d.codes.data(),
-                  d.scales.data(), x.data(), want.data(), T, H, I);
     DevMatrix dg = upload_matrix(be, g), du = upload_matrix(be, u), dd = upload_matrix(be, d);
-    Buffer *in = upload(be, x.data(), x.size() * 4, "activations");
-    Buffer *gate_tmp = be.allocate((size_t)T * I * 4, "scratch");
-    Buffer *up_tmp = be.allocate((size_t)T * I * 4, "scratch");
-    Buffer *out = be.allocate((size_t)T * H * 4, "scratch");
-    denseMlp(be, in, dg.m, du.m, dd.m, gate_tmp, up_tmp, out, T);
-    be.sync();
-    double r = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
-    report("denseMlp fp32 at 128 tokens (GEMMs) vs oracle", r < 1e-5, "rel_l2 " + std::to_string(r));
-    denseMlpFused(be, in, dg.m, du.m, dd.m, gate_tmp, out, T);
-    be.sync();
-    r = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
-    report("denseMlpFused fp32 at 128 tokens (GEMMs) vs oracle", r < 1e-5,
-           "rel_l2 " + std::to_string(r));
-    for (Buffer *b : {dg.buf, du.buf, dd.buf, in, gate_tmp, up_tmp, out})
+    for (uint32_t T : {128u, 512u}) {
+        std::vector<float> x((size_t)T * H);
+        for (auto &v : x)
+            v = rng.normal();
+        std::vector<float> want((size_t)T * H);
+        orc_dense_mlp(g.codes.data(), g.scales.data(), u.codes.data(), u.scales.data(),
+                      d.codes.data(), d.scales.data(), x.data(), want.data(), T, H, I);
+        Buffer *in = upload(be, x.data(), x.size() * 4, "activations");
+        Buffer *gate_tmp = be.allocate((size_t)T * I * 4, "scratch");
+        Buffer *up_tmp = be.allocate((size_t)T * I * 4, "scratch");
+        Buffer *out = be.allocate((size_t)T * H * 4, "scratch");
+        const std::string tag = " at " + std::to_string(T) + " tokens";
+        uint64_t n0 = gemm_launches();
+        denseMlp(be, in, dg.m, du.m, dd.m, gate_tmp, up_tmp, out, T);
+        be.sync();
+        double r = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
+        report("denseMlp fp32" + tag + " vs oracle", r < 1e-5, "rel_l2 " + std::to_string(r));
+        uint64_t n = gemm_launches() - n0;
+        report("denseMlp" + tag + ": matmul_nvfp4 ran 3 MFMA GEMMs", n == 3,
+               std::to_string(n) + " GEMM launches");
+        n0 = gemm_launches();
+        denseMlpFused(be, in, dg.m, du.m, dd.m, gate_tmp, out, T);
+        be.sync();
+        r = rel_l2(static_cast<float *>(be.contents(out)), want.data(), want.size());
+        report("denseMlpFused fp32" + tag + " vs oracle", r < 1e-5, "rel_l2 " + std::to_string(r));
+        n = gemm_launches() - n0;
+        report("denseMlpFused" + tag + ": 2 MFMA GEMMs", n == 2, std::to_string(n) + " GEMM launches");
+        for (Buffer *b : {in, gate_tmp, up_tmp, out})
+            be.release(b);
+    }
+    for (Buffer *b : {dg.buf, du.buf, dd.buf})
         be.release(b);
 }
 
@@ -509,6 +531,15 @@ int main(int argc, char **argv) {
         // Without a device, construction fails with the C ABI's message.
         report("HipBackend without a device throws",
                throws([] { HipBackend be(0); }, "HipBackend"));
+        Profile::get().add("phase_a", 1.5);
+        Profile::get().add("phase_a", 0.25);
+        { Timer t("phase_b"); }
+        const Profile::Phase a = Profile::get().phase("phase_a");
+        report("Profile: calls, total, shortest and longest per phase",
+               a.count == 2 && a.total_ns == 1750000 && a.shortest_ns == 250000 &&
+                   a.longest_ns == 1500000 && Profile::get().phase("phase_b").count == 1 &&
+                   Profile::get().phase("never").count == 0);
+        Profile::get().reset();
         return g_failures ? 1 : 0;
     }
     HipBackend be(0);
@@ -521,6 +552,9 @@ int main(int argc, char **argv) {
     if (!packed.empty())
         test_packed_moe(be, packed);
     test_errors(be);
+    const Profile::Phase ps = Profile::get().phase("gpu_sync");
+    report("Backend::sync timed under gpu_sync", ps.count > 0 && ps.longest_ns >= ps.shortest_ns,
+           std::to_string(ps.count) + " calls");
     Profile::get().print(stdout);
     std::printf("%s (%d failure%s)\n", g_failures ? "FAILED" : "OK", g_failures,
                 g_failures == 1 ? "" : "s");

@@ -43,6 +43,7 @@ def test_host_layer_without_device(packed_dir):
     r = run("--no-gpu", "--packed", packed_dir)
     assert r.returncode == 0, r.stdout
     assert "PASS HipBackend without a device throws" in r.stdout
+    assert "PASS Profile: calls, total, shortest and longest per phase" in r.stdout
     for name in ("config and quantization", "expert slot pieces", "layer files", "core tensors",
                  "unknown tensor throws"):
         assert f"PASS manifest: {name}" in r.stdout
@@ -54,7 +55,12 @@ def test_host_layer_on_gpu(packed_dir):
     assert r.returncode == 0, r.stdout
     assert "FAIL" not in r.stdout
     for name in ("denseMlp fp32 (4 launches) vs oracle", "denseMlpFused fp32 (2 launches) vs oracle",
+                 "denseMlp fp32 at 128 tokens vs oracle", "denseMlp fp32 at 512 tokens vs oracle",
+                 "denseMlp at 128 tokens: matmul_nvfp4 ran 3 MFMA GEMMs",
+                 "denseMlp at 512 tokens: matmul_nvfp4 ran 3 MFMA GEMMs",
+                 "denseMlpFused at 512 tokens: 2 MFMA GEMMs",
                  "matmulNvfp4Bf16 T=96", "moeFfn vs oracle", "rmsNorm vs oracle",
                  "headNormRope vs oracle", "unknown kernel throws", "manifest: layer files",
-                 "packed router logits vs oracle", "packed MoE block vs oracle"):
+                 "packed router logits vs oracle", "packed MoE block vs oracle",
+                 "Backend::sync timed under gpu_sync"):
         assert f"PASS {name}" in r.stdout

@@ -325,6 +325,25 @@ def test_moe_ffn_is_the_weighted_sum_of_dense_ffns():
     assert np.array_equal(y2, 2 * y)
 
 
+def test_reference_cpu_compositions_equal_the_oracle():
+    """The CPU baselines' reference compositions (ref_geglu, ref_moe_ffn: the
+    reference's matvecNvfp4Cpu and geluTanh, tokens grouped per expert) give the
+    oracle's results bit for bit: every (row, token) dot product is computed on its
+    own in fp64, so grouping tokens changes nothing."""
+    if not oracle.ref_available():
+        pytest.skip("reference CPU code not built (reference not mounted)")
+    rng = np.random.default_rng(23)
+    E, H, I, T, k = 7, 128, 64, 5, 3
+    slots = synth.expert_slots(rng, E, H, I)
+    x = synth.bf16_to_f32(synth.normal_bf16(rng, (T, H)))
+    ids, w = oracle.moe_route(synth.bf16_to_f32(synth.normal_bf16(rng, (T, E))), k)
+    assert np.array_equal(oracle.ref_moe_ffn(slots, x, ids, w, E), oracle.moe_ffn(slots, x, ids, w))
+    g = (slots.piece(0, "gate_w"), slots.piece(0, "gate_s"))
+    u = (slots.piece(0, "up_w"), slots.piece(0, "up_s"))
+    want = oracle.geglu(oracle.matvec(*g, x), oracle.matvec(*u, x))
+    assert np.array_equal(oracle.ref_geglu(g, u, x), want)
+
+
 def test_expert_slot_layout():
     offsets, stride, used = synth.slot_layout(2816, 704)
     assert used == 3_345_408 and stride == 3_358_720 and stride % 16384 == 0
