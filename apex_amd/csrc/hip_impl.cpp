@@ -335,7 +335,8 @@ bool moe_use_gemm(uint32_t T, uint32_t k, uint32_t H, uint32_t I) {
 }
 
 // Router logits arrive as bf16 (`logits`) or fp32 (`logits_f32`, with an optional
-// bf16 per-expert scale on the routing weights); exactly one is given.
+// bf16 per-expert scale on the routing weights); exactly one is given.  `ws` null: the
+// decode path on the library's fixed workspace (no allocation; decode shapes only).
 void moe_impl(const uint16_t *x, const uint16_t *logits, const float *logits_f32,
               const uint16_t *pes, const apex_moe_slots *slots, uint16_t *y, uint32_t T,
               uint32_t E, uint32_t k, uint32_t H, uint32_t I, void *ws, size_t ws_bytes,
@@ -343,9 +344,10 @@ void moe_impl(const uint16_t *x, const uint16_t *logits, const float *logits_f32
     require(slots != nullptr, "moe_ffn: slots is null");
     if (T == 0)
         return;
-    require(x && (logits || logits_f32) && slots->base && y && ws, "moe_ffn: null pointer");
+    const bool fixed_ws = ws == nullptr;
+    require(x && (logits || logits_f32) && slots->base && y, "moe_ffn: null pointer");
     init_device_tuning();
-    const bool gemm = moe_use_gemm(T, k, H, I);
+    const bool gemm = !fixed_ws && moe_use_gemm(T, k, H, I);
     apex_hip::MoeArgs a{};
     a.x = x;
     a.logits = logits;
@@ -357,8 +359,13 @@ void moe_impl(const uint16_t *x, const uint16_t *logits, const float *logits_f32
     a.T = T, a.E = E, a.k = k, a.H = H, a.I = I;
     const char *why = nullptr;
     if (!apex_hip::moe_supported(a, gemm, &why))
-        fail(APEX_HIP_E_INVALID, std::string("moe_ffn: ") + why);
+        fail(APEX_HIP_E_INVALID, std::string(fixed_ws ? "moe_ffn (no-allocation form): "
+                                                       : "moe_ffn: ") + why);
     const apex_hip::MoeWorkspace w = apex_hip::moe_workspace(T, E, k, H, I, gemm);
+    if (fixed_ws) {
+        hip_check(apex_hip::moe_static_workspace(&ws), "moe_ffn: fixed workspace address");
+        ws_bytes = apex_hip::kMoeStaticWorkspaceBytes;
+    }
     require((uintptr_t)ws % 256 == 0, "moe_ffn: workspace must be 256-byte aligned");
     if (ws_bytes < w.total)
         fail(APEX_HIP_E_INVALID, "moe_ffn: workspace too small (need " + std::to_string(w.total) +
@@ -1262,8 +1269,19 @@ int apex_moe_ffn_bf16(const uint16_t *x, const uint16_t *logits, const apex_moe_
                       uint32_t hidden, uint32_t inter, void *workspace, size_t workspace_bytes,
                       void *stream) {
     return guard([&] {
+        require(workspace != nullptr || tokens == 0, "moe_ffn: workspace is null");
         moe_impl(x, logits, nullptr, nullptr, slots, y, tokens, experts, top_k, hidden, inter,
                  workspace, workspace_bytes, as_stream(stream));
+    });
+}
+
+int apex_moe_ffn_bf16_noalloc(const uint16_t *x, const uint16_t *logits,
+                              const apex_moe_slots *slots, uint16_t *y, uint32_t tokens,
+                              uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
+                              void *stream) {
+    return guard([&] {
+        moe_impl(x, logits, nullptr, nullptr, slots, y, tokens, experts, top_k, hidden, inter,
+                 nullptr, 0, as_stream(stream));
     });
 }
 
@@ -1274,6 +1292,7 @@ int apex_moe_ffn_f32logits_bf16(const uint16_t *x, const float *logits,
                                 size_t workspace_bytes, void *stream) {
     return guard([&] {
         require(logits != nullptr || tokens == 0, "moe_ffn: null pointer");
+        require(workspace != nullptr || tokens == 0, "moe_ffn: workspace is null");
         moe_impl(x, nullptr, logits, per_expert_scale, slots, y, tokens, experts, top_k, hidden,
                  inter, workspace, workspace_bytes, as_stream(stream));
     });

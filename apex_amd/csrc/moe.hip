@@ -1675,6 +1675,31 @@ hipError_t moe_router_logits_launch(const MoeRouterArgs &a, hipStream_t stream) 
     return router_launch_epl<4, 8>(a, stream);
 }
 
+// The decode path's fixed workspace (moe_static_workspace).  Host code never names the
+// array in a launch or copy: its device address is looked up per device and passed on.
+static __device__ __align__(256) uint8_t scratch[kMoeStaticWorkspaceBytes];
+
+hipError_t moe_static_workspace(void **ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<void *> addr[kMaxDevices] = {};
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess)
+        return e;
+    if (dev < 0 || dev >= kMaxDevices)
+        return hipErrorInvalidDevice;
+    void *p = addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        // with the device current: each device holds its own copy of the array
+        if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess)
+            return e;
+        if (!p)
+            return hipErrorInvalidSymbol;
+        addr[dev].store(p, std::memory_order_release);
+    }
+    *ptr = p;
+    return hipSuccess;
+}
+
 hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     if (a.T == 0)
         return hipSuccess;

@@ -104,6 +104,7 @@ _PROTOS = {
     "apex_moe_workspace_bytes": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
     "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
     "apex_hip_set_moe_path": (_I, [_I]),
+    "apex_moe_ffn_bf16_noalloc": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P]),
     "apex_rms_norm_f32": (_I, [_P, _P, _P, _U32, _U32, _F, _P]),
     "apex_file_to_device": (_I, [C.c_char_p, _U64, _U64, _P, _U64, _U32, _P]),
     "apex_experts_to_device": (_I, [C.c_char_p, _U64, _U64, _P, _U32, _P, _U64, _U64, _U32, _P]),
@@ -393,6 +394,13 @@ def moe_ffn_bf16(x, logits, slots: MoeSlots, y, tokens, experts, top_k, hidden, 
     check(lib().apex_moe_ffn_bf16(x.ptr, logits.ptr, C.byref(slots), y.ptr, tokens, experts,
                                   top_k, hidden, inter, workspace.ptr, workspace.nbytes,
                                   _s(stream)))
+
+
+def moe_ffn_bf16_noalloc(x, logits, slots: MoeSlots, y, tokens, experts, top_k, hidden, inter,
+                         stream=None):
+    """apex_moe_ffn_bf16's decode path on the library's fixed workspace (no allocation)."""
+    check(lib().apex_moe_ffn_bf16_noalloc(x.ptr, logits.ptr, C.byref(slots), y.ptr, tokens, experts,
+                                          top_k, hidden, inter, _s(stream)))
 
 
 def set_moe_path(path: int) -> None:

@@ -385,6 +385,20 @@ int apex_moe_ffn_bf16(const uint16_t *x, const uint16_t *logits, const apex_moe_
                       uint32_t hidden, uint32_t inter, void *workspace, size_t workspace_bytes,
                       void *stream);
 
+/* No counterpart in the reference: apex_moe_ffn_bf16's decode path (grouped GEMVs) for
+ * callers that cannot allocate device memory -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  The workspace is a fixed device
+ * array of 2.25 MiB inside the library (each GPU the library runs on holds its own
+ * copy until the process ends); the call allocates nothing and takes no workspace
+ * argument.  Limits: tokens <= 32, tokens * top_k <= 256, experts <= 256, hidden <= 3072,
+ * inter <= 1024 (larger shapes return APEX_HIP_E_INVALID).  Results are identical to
+ * apex_moe_ffn_bf16 on the same shapes.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams or threads) race. */
+int apex_moe_ffn_bf16_noalloc(const uint16_t *x, const uint16_t *logits,
+                              const apex_moe_slots *slots, uint16_t *y, uint32_t tokens,
+                              uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
+                              void *stream);
+
 /* Path selection of apex_moe_ffn_bf16: 0 by size (default), 1 grouped GEMV, 2 grouped GEMM. */
 int apex_hip_set_moe_path(int path);
 
