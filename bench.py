@@ -20,7 +20,8 @@ slices, extrapolated).
 
 The "secondary" object carries the metric's second half and the other workloads of
 the path, each timed the same way (HIP events around back-to-back steps; at least 10
-launches and 20 ms of GPU time per record, the count in its "steps"):
+launches and 20 ms of GPU time per record, the count in its "steps", after at least
+60 ms of untimed warmup launches: the clocks ramp under sustained MFMA load):
   moe_prefill   MoE layer prefill: 4096 tokens, hidden 2816, 128 experts, top-8,
                 intermediate 704, Zipf(1.1) routing -> TFLOP/s vs the 2.5 PFLOP/s
                 dense bf16 MFMA peak (flops of the routed pairs only);
@@ -225,15 +226,21 @@ def cpu_baselines(budget_s: float = 4.0):
 
 # ---- GPU timing -----------------------------------------------------------------------
 
-# every secondary record times at least this many launches and this much GPU time
+# every secondary record times at least this many launches and this much GPU time, after
+# at least this much GPU time of untimed warmup launches of the same step: the clocks
+# ramp under sustained MFMA load (the dense prefill GEMM runs 476 -> 417 -> 400 -> 390 us
+# over its first 60 launches, ~27 ms, and holds there), so a record timed right after a
+# cold start would measure the ramp, not the kernel
 MIN_TIMED_STEPS = 10
 MIN_TIMED_MS = 20.0
+MIN_WARMUP_MS = 60.0
 
 
-def time_steps(step, steps, warmup, stream, min_steps=MIN_TIMED_STEPS, min_ms=MIN_TIMED_MS):
+def time_steps(step, steps, warmup, stream, min_steps=MIN_TIMED_STEPS, min_ms=MIN_TIMED_MS,
+               min_warmup_ms=MIN_WARMUP_MS):
     """Seconds per step of `step(i)` launched back to back on `stream`, and the number of
-    steps timed: `warmup` untimed steps, then max(steps, min_steps) timed steps, more if
-    needed to cover min_ms of GPU time (estimated from the warmup)."""
+    steps timed: max(warmup, 1) untimed steps -- more until min_warmup_ms of GPU time has
+    run -- then max(steps, min_steps) timed steps, more if needed to cover min_ms."""
     warmup = max(1, warmup)
     stream.synchronize()
     e0, e1 = hip.Event(), hip.Event()
@@ -242,7 +249,16 @@ def time_steps(step, steps, warmup, stream, min_steps=MIN_TIMED_STEPS, min_ms=MI
         step(i)
     e1.record(stream)
     e1.synchronize()
-    est_ms = e0.elapsed_ms(e1) / warmup
+    warm_ms = e0.elapsed_ms(e1)
+    est_ms = warm_ms / warmup
+    if est_ms > 0 and warm_ms < min_warmup_ms:
+        more = int(np.ceil((min_warmup_ms - warm_ms) / est_ms))
+        e0.record(stream)
+        for i in range(more):
+            step(warmup + i)
+        e1.record(stream)
+        e1.synchronize()
+        est_ms = e0.elapsed_ms(e1) / more
     n = max(steps, min_steps)
     if est_ms > 0:
         n = max(n, int(np.ceil(min_ms / est_ms)))
@@ -358,7 +374,7 @@ def time_gemm_prefill(steps, warmup, M=2048, N=21504, K=5376):
             "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(2 * M * N * K),
             "workload": f"prefill GEMM: A bf16 [{M},{K}] x NVFP4 W [{N}x{K}]^T -> C bf16 [{M},{N}]",
             "yardstick_vendor_bf16_gemm_tflops": vendor_bf16_gemm(M, N, K, max(steps, 60),
-                                                                  max(warmup, 5))}
+                                                                  max(warmup, 160))}
 
 
 def time_dense_prefill(steps, warmup, T=2048, N=21504, K=5376):
