@@ -367,6 +367,59 @@ __device__ __forceinline__ void store_tile_bf16(const Acc<MT, WC> &acc, uint16_t
             }
 }
 
+// The same output as store_tile_bf16 (wide form), for 1 x 4 tiles, staged through LDS: a
+// lane's 16-byte pieces land in a row-major copy of the tile (16-byte chunks XOR-swizzled
+// by row % 16, so neither the accumulator-order writes nor the row-order reads conflict),
+// then each store instruction writes whole rows (two 512-byte rows, 8 cache lines)
+// instead of 16 bytes in each of 32 rows.  Passes of at most 128 rows (64 KB of `lds`,
+// which the tile loop has drained).  Requires N and ldc multiples of 8, C 16-byte aligned.
+template <int MT>
+__device__ __forceinline__ void store_tile_bf16_lds(const Acc<MT, 4> &acc, uint8_t *lds, uint16_t *C,
+                                                    uint32_t ldc, uint32_t m0, uint32_t n0, uint32_t M,
+                                                    uint32_t N, float scale) {
+    constexpr int kRows = 32 * MT;
+    constexpr int kPassRows = kRows > 128 ? 128 : kRows;
+    constexpr int kRowBytes = BN * 2;
+    constexpr int kChunks = kRowBytes / 16; // 32
+    const int lane = threadIdx.x & 63;
+    const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)threadIdx.x >> 6);
+    const uint64_t bytes = (uint64_t)(M - m0) * ldc * 2;
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(C + (size_t)m0 * ldc + n0, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);
+#pragma unroll
+    for (int ps = 0; ps < kRows / kPassRows; ++ps) {
+        if (ps > 0)
+            __syncthreads(); // the previous pass's reads are done
+        // block (i, j), piece p -> row 32 i + lane % 32, chunk 8 wave + 4 j + 2 p + lane / 32
+#pragma unroll
+        for (int ii = 0; ii < kPassRows / 32; ++ii) {
+            const int i = ps * (kPassRows / 32) + ii;
+            const int r = 32 * ii + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                u32x4_t o[2];
+                pack_bf16_cols(acc[i][j] * scale, o);
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const int c = 8 * wave + 4 * j + 2 * p + (lane >> 5);
+                    *reinterpret_cast<u32x4_t *>(lds + r * kRowBytes + ((c ^ (r & 15)) * 16)) = o[p];
+                }
+            }
+        }
+        __syncthreads();
+        // thread t: chunk t % 32 of rows t / 32 + 8 s
+#pragma unroll
+        for (int sr = 0; sr < kPassRows / 8; ++sr) {
+            const int r = (int)(threadIdx.x / kChunks) + 8 * sr;
+            const int c = (int)(threadIdx.x % kChunks);
+            const u32x4_t v = *reinterpret_cast<const u32x4_t *>(lds + r * kRowBytes + ((c ^ (r & 15)) * 16));
+            const uint32_t col = 8 * c;
+            const uint32_t off = n0 + col < N ? ((ps * kPassRows + r) * ldc + col) * 2 : kOut;
+            __builtin_amdgcn_raw_buffer_store_b128(v, rc, (int)off, 0, 0);
+        }
+    }
+}
+
 // fp32 output of a tile (times `scale`), placed as store_tile_bf16 places it: a lane's
 // runs of 4 consecutive columns go out as 16-byte stores when `wide` (N and ldc
 // multiples of 4, C 16-byte aligned), otherwise one 4-byte store per element.

@@ -21,8 +21,9 @@
 //   gate/up  persistent waves over (active expert, 2 rows) units: the unit's gate and
 //            up rows stream once and serve every token routed to the expert; GeGLU in
 //            registers -> h[pos] (bf16).
-//   down     the same over (active expert, 16 rows) units of the down matrices, x =
-//            h[pos] -> d[pos] (bf16).
+//   down     persistent waves over (token group, 8 rows) units: a group is up to 4
+//            positions of one expert whose h rows sit in LDS; each unit's down rows are
+//            decoded once for the whole group -> d[pos] (bf16).
 //   combine  as in the prefill regime.
 // Prefill regime: MFMA grouped GEMMs on the gemm_core tile (bf16 MFMA on exactly
 // dequantised weights).
@@ -1007,6 +1008,44 @@ constexpr int kGemvBlocksPerCU = 4; // 256-thread workgroups per CU (global x)
 constexpr int kXLdsThreads = 1024;  // x in LDS: one workgroup of 16 waves per CU
 constexpr uint32_t kXLdsBytes = 120 * 1024;
 
+// Activation rows staged in LDS as [row][4 pieces][nchunks + 1] 16-byte entries: entry
+// (r, q, c) = bytes [64 c + 16 q, +16) of the row at byte offset row_off(r) of `rs`, and
+// chunk nchunks of every (r, q) plane is zero (its load lies past the descriptor), so
+// lanes past the end of a row read zeros without a branch.  Each thread issues all its
+// loads (up to kStagePerThread) before its first LDS write, so the copy costs one
+// memory round trip; a load-then-write loop waits for each load in turn (~1 us each
+// at kernel start, when every CU copies at once).
+constexpr int kStagePerThread = 8;
+static_assert(kStagePerThread * kXLdsThreads * 16 >= kXLdsBytes, "one round covers the LDS budget");
+
+template <typename RowOff>
+__device__ __forceinline__ void stage_rows(uint4 *xl, __amdgpu_buffer_rsrc_t rs, uint32_t n_rows,
+                                           int nchunks, RowOff row_off) {
+    const uint32_t nc = (uint32_t)nchunks + 1, n = n_rows * 4 * nc;
+    for (uint32_t base = 0; base < n; base += kStagePerThread * blockDim.x) {
+        u32x4_t v[kStagePerThread];
+        uint32_t dst[kStagePerThread];
+#pragma unroll
+        for (int k = 0; k < kStagePerThread; ++k) {
+            const uint32_t i = base + threadIdx.x + k * blockDim.x;
+            uint32_t off = kOutOfRange;
+            dst[k] = 0xFFFFFFFFu;
+            if (i < n) {
+                const uint32_t r = i / (4 * nc), rem = i % (4 * nc);
+                const uint32_t c = rem / 4, q = rem % 4;
+                if ((int)c < nchunks)
+                    off = row_off(r) + c * 64 + q * 16;
+                dst[k] = (r * 4 + q) * nc + c;
+            }
+            v[k] = load_b128(rs, off);
+        }
+#pragma unroll
+        for (int k = 0; k < kStagePerThread; ++k)
+            if (dst[k] != 0xFFFFFFFFu)
+                xl[dst[k]] = __builtin_bit_cast(uint4, v[k]);
+    }
+}
+
 template <bool GATE_UP, int G, int SLOTS, int NB, bool XLDS, int TG>
 __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 256 : 4) void moe_gemv_kernel(MoeArgs a) {
     static_assert(TG == 1 || (XLDS && TG == kTokenGroup), "token groups read x from LDS");
@@ -1048,19 +1087,8 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
             s_grp[i] = (uint32_t)v.groups[2 * i + 1];
         }
     }
-    if constexpr (XLDS) {
-        // entry (t, piece q, chunk c) = bytes [64 c + 16 q, +16) of row t; chunk nchunks
-        // of every (t, q) plane is zero (its load lies past the descriptor), so lanes past
-        // the end of a row read zeros without a branch
-        const uint32_t nc = nchunks + 1;
-        const uint32_t n = a.T * 4 * nc;
-        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-            const uint32_t t = i / (4 * nc), rem = i % (4 * nc);
-            const uint32_t c = rem / 4, q = rem % 4;
-            const uint32_t off = (int)c < nchunks ? t * K * 2 + c * 64 + q * 16 : kOutOfRange;
-            xl[(t * 4 + q) * nc + c] = __builtin_bit_cast(uint4, load_b128(rx, off));
-        }
-    }
+    if constexpr (XLDS)
+        stage_rows(xl, rx, a.T, nchunks, [&](uint32_t t) { return t * K * 2; });
     __syncthreads();
     const uint32_t wave = uniform(threadIdx.x >> 6);
     const uint32_t waves_per_block = blockDim.x / 64;
@@ -1181,6 +1209,172 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     }
 }
 
+// Decode down GEMV over token groups, h staged in LDS by segment.  At decode sizes the
+// down GEMV is bound by its weight decode and dots rather than by its bytes (one
+// position per item: 28 us for 8 distinct experts, 31 us for 128, at 128 positions),
+// so each item decodes its weight rows once for a whole group (up to kTokenGroup
+// positions of one expert, see plan_from_masks), and 8-lane row groups keep 22 of
+// every 24 chunk slots busy at I = 704 (32-lane groups: 22 of 32).  Measured against
+// the per-position kernel: 18 vs 28 us (8 experts), 26 vs 30 us (83 experts of 128
+// positions), 34 vs 31 us (128 experts, no group larger than 1: the 8-lane groups read
+// 4x the x bytes per weight byte from LDS).  The groups' h rows are read from LDS.  All P rows
+// need not fit: the groups are split over S segments, group g in segment g % S (so every
+// size class splits evenly), workgroup b serves segment b % S and stages only its
+// segment's rows -- per class at most one group more than an even share, so at most
+// ceil(P / S) + 10 rows, which the host sizes `cap` and S for.
+//   Items (row block rb of R * NB rows, group i of the segment) are dealt class by class
+// (groups of 4, 3, 2, 1 positions), rb-major, round-robin over the segment's workgroups
+// first, so every CU and SIMD gets an even share of each cost class.  The first item's
+// weight loads are issued before the h rows are staged.
+template <int G, int SLOTS, int NB>
+__global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_group_kernel(MoeArgs a, uint32_t S,
+                                                                                     uint32_t cap) {
+    constexpr int R = 64 / G;
+    constexpr int TG = kTokenGroup;
+    __shared__ int s_exp[kMoeGemvMaxPairs];      // expert of the segment's group i
+    __shared__ uint32_t s_grp[kMoeGemvMaxPairs]; // its first staged row | size << 16
+    __shared__ uint32_t s_pos[kMoeGemvMaxPairs]; // position of staged row j
+    __shared__ uint32_t s_nrows;
+    extern __shared__ uint4 xl[];                // [staged row][4 pieces][nchunks + 1]
+    const int lane = threadIdx.x & 63;
+    const int sub = lane / G, gl = lane % G;
+    const uint32_t P = a.T * a.k, H = a.H, I = a.I;
+    const int nchunks = (int)(I / 32);
+    const uint32_t nc = (uint32_t)nchunks + 1;
+    const PlanView v = plan_view(a.plan, a.E, P);
+    const uint32_t seg = blockIdx.x % S, wg = blockIdx.x / S;
+    const uint32_t nwg = (gridDim.x - seg + S - 1) / S;
+    const uint32_t wave = uniform(threadIdx.x >> 6);
+    // the segment's groups per size class: g in [lo, hi) with g % S == seg
+    auto below = [&](uint32_t x) { return (x + S - 1 - seg) / S; };
+    uint32_t ncls[TG], ngs = 0;
+    {
+        uint32_t lo = 0;
+#pragma unroll
+        for (int q = 0; q < TG; ++q) {
+            const uint32_t hi = lo + uniform(v.hdr[3 + q]);
+            ncls[q] = below(hi) - below(lo);
+            ngs += ncls[q];
+            lo = hi;
+        }
+    }
+    if (wave == 0) {
+        uint32_t base = 0;
+        for (uint32_t i0 = 0; i0 < ngs; i0 += 64) {
+            const uint32_t i = i0 + lane;
+            int e = 0;
+            uint32_t p0 = 0, n = 0;
+            if (i < ngs) {
+                const uint32_t g = seg + S * i;
+                e = v.groups[2 * g];
+                const uint32_t gp = (uint32_t)v.groups[2 * g + 1];
+                p0 = gp & 0xFFFFu;
+                n = gp >> 16;
+            }
+            int total;
+            const uint32_t off = base + (uint32_t)wave_excl_scan((int)n, lane, total);
+            if (i < ngs) {
+                s_exp[i] = e;
+                s_grp[i] = off | (n << 16);
+                for (uint32_t u = 0; u < n; ++u)
+                    s_pos[off + u] = p0 + u;
+            }
+            base += (uint32_t)total;
+        }
+        if (lane == 0)
+            s_nrows = base;
+    }
+    __syncthreads();
+
+    const uint32_t per_e = (H + R * NB - 1) / (R * NB);
+    const uint32_t items = per_e * ngs;
+    const uint32_t nw = nwg * (blockDim.x / 64);
+    const bool last_ok = gl + (SLOTS - 1) * G < nchunks;
+    const uint32_t last_c = last_ok ? (SLOTS - 1) * G * 16 : kOutOfRange;
+    const uint32_t last_s = last_ok ? (SLOTS - 1) * G * 2 : kOutOfRange;
+    const uint32_t wbytes = H * I / 2, sbytes = H * I / 16;
+    auto locate = [&](uint32_t it, uint32_t &rb, uint32_t &i) {
+        uint32_t g0 = 0;
+#pragma unroll
+        for (int q = 0; q < TG; ++q) {
+            const uint32_t nq = ncls[q];
+            if (it < per_e * nq) {
+                rb = it / nq;
+                i = g0 + (it - rb * nq);
+                return;
+            }
+            it -= per_e * nq;
+            g0 += nq;
+        }
+    };
+    auto issue = [&](RowRegs<SLOTS> (&w)[NB], uint32_t it) {
+        uint32_t rb, i;
+        locate(it, rb, i);
+        const uint8_t *slot = a.slots.base + (size_t)uniform(s_exp[i]) * a.slots.stride;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(slot + a.slots.down_w, wbytes);
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(slot + a.slots.down_s, sbytes);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const uint32_t row = rb * R * NB + b * R + sub;
+            load_row<SLOTS, G>(w[b], rc, rs, row < H ? row : H, gl, I, last_c, last_s);
+        }
+    };
+    // x chunk of slot s of staged row j (j < cap by the segment bound; the clamp only
+    // keeps the reads inside the staged rows)
+    auto lds_x = [&](uint32_t j, int s) {
+        const int c = min(gl + s * G, nchunks); // chunk nchunks is zero
+        const uint4 *plane = xl + min(j, cap - 1) * 4 * nc + c;
+        XChunk<uint16_t> xc;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            xc.p[q] = __builtin_bit_cast(u32x4_t, plane[q * nc]);
+        return xc;
+    };
+    auto compute = [&](const RowRegs<SLOTS> (&w)[NB], uint32_t it) {
+        uint32_t rb, i;
+        locate(it, rb, i);
+        const uint32_t gp = uniform(s_grp[i]);
+        const uint32_t j0 = gp & 0xFFFFu;
+        const int n = (int)(gp >> 16);
+        float dots[TG][NB];
+        rows_dot_group<G, SLOTS, NB, TG>(dots, w, n, [&](int t, int s) { return lds_x(j0 + t, s); });
+        if (gl == 0)
+#pragma unroll
+            for (int t = 0; t < TG; ++t) {
+                if (t >= n)
+                    break;
+                const uint32_t pos = uniform(s_pos[j0 + t]);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const uint32_t row = rb * R * NB + b * R + sub;
+                    if (row < H)
+                        a.d[(size_t)pos * H + row] = f32_to_bf16_bits(dots[t][b]);
+                }
+            }
+    };
+
+    const uint32_t first = wave * nwg + wg;
+    RowRegs<SLOTS> wa[NB], wb[NB];
+    if (first < items)
+        issue(wa, first);
+    // the segment's h rows: staged row j = h[s_pos[j]]
+    stage_rows(xl, make_rsrc(a.h, P * I * 2), min(s_nrows, cap), nchunks,
+               [&](uint32_t j) { return s_pos[j] * I * 2; });
+    __syncthreads();
+    // two register sets: the next item's weight loads are in flight during this item's
+    // decode and dots
+    for (uint32_t it = first; it < items; it += 2 * nw) {
+        if (it + nw < items)
+            issue(wb, it + nw);
+        compute(wa, it);
+        if (it + nw >= items)
+            break;
+        if (it + 2 * nw < items)
+            issue(wa, it + 2 * nw);
+        compute(wb, it + nw);
+    }
+}
+
 // ---------------------------------------------------------------------------------
 // Prefill: grouped GEMMs
 // ---------------------------------------------------------------------------------
@@ -1263,7 +1457,10 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
     const __amdgpu_buffer_rsrc_t rw2[2] = {rw, rw};
     Acc<MT, 4> acc;
     gemm_tile<MT, 4>(lds, ra, rw2, rw2, I, a_row, w_code, w_scale, acc);
-    store_tile_bf16<MT, 4>(acc, a.d + (size_t)row0 * H, H, 0, n0, nrows, H, 1.0f, true);
+    // Whole-row stores staged through the drained LDS ring: 3% faster than the direct
+    // 16-byte pieces on this short-K GEMM (the GeGLU gate/up epilogue was 5% slower
+    // staged, so it stores directly).
+    store_tile_bf16_lds<MT>(acc, lds, a.d + (size_t)row0 * H, H, 0, n0, nrows, H, 1.0f);
 }
 
 // The down GEMM's K (= I) is short, so a tile's prologue (plan lookups, first stages in
@@ -1350,6 +1547,53 @@ template <typename F> hipError_t set_lds(F *kernel, size_t bytes, std::atomic<ui
 }
 
 uint32_t gemv_slots(uint32_t K, int G) { return (K / 32 + G - 1) / G; }
+
+// Decode down GEMV by token groups (moe_down_group_kernel): 8-lane row groups, one row
+// set (8 rows) per item -- two row sets per item exceed the register budget of 16
+// waves per CU with the second in-flight set.  Segments: the fewest S with
+// ceil(P / S) + 10 staged rows within the LDS budget.  The decode path's limits
+// (I <= 1024, P <= kMoeGemvMaxPairs) always leave one: 4 slots at most, and 16
+// segments fit even the largest I.
+constexpr int kDownGroupLanes = 8;
+constexpr int kDownGroupNB = 1;
+constexpr uint32_t kDownGroupMaxSlots = 4;
+static_assert((1024 / 32 + kDownGroupLanes - 1) / kDownGroupLanes <= kDownGroupMaxSlots &&
+                  (kMoeGemvMaxPairs + 15) / 16 + 10 <= kXLdsBytes / ((1024 / 32 + 1) * 64),
+              "every decode shape (I <= 1024, P <= 256) has a segment count");
+
+uint32_t down_group_segments(uint32_t P, uint32_t I, uint32_t &rows) {
+    const uint32_t hrow = (I / 32 + 1) * 64;
+    const uint32_t cap = kXLdsBytes / hrow;
+    if (gemv_slots(I, kDownGroupLanes) > kDownGroupMaxSlots)
+        return 0;
+    for (uint32_t S = 1; S <= 16 && S <= (uint32_t)num_cus(); ++S)
+        if ((P + S - 1) / S + 10 <= cap) {
+            rows = (P + S - 1) / S + 10 < P ? (P + S - 1) / S + 10 : P;
+            return S;
+        }
+    return 0;
+}
+
+template <int SLOTS, int NB>
+hipError_t launch_down_group(const MoeArgs &a, uint32_t S, uint32_t rows, hipStream_t stream) {
+    static std::atomic<uint64_t> attr{0};
+    const hipError_t err = set_lds(moe_down_group_kernel<kDownGroupLanes, SLOTS, NB>, kXLdsBytes, attr);
+    if (err != hipSuccess)
+        return err;
+    const size_t bytes = (size_t)rows * (a.I / 32 + 1) * 64;
+    hipLaunchKernelGGL((moe_down_group_kernel<kDownGroupLanes, SLOTS, NB>), dim3((uint32_t)num_cus()),
+                       dim3(kXLdsThreads), bytes, stream, a, S, rows);
+    return hipSuccess;
+}
+
+hipError_t down_group_by_slots(const MoeArgs &a, uint32_t S, uint32_t rows, hipStream_t stream) {
+    switch (gemv_slots(a.I, kDownGroupLanes)) {
+    case 1: return launch_down_group<1, kDownGroupNB>(a, S, rows, stream);
+    case 2: return launch_down_group<2, kDownGroupNB>(a, S, rows, stream);
+    case 3: return launch_down_group<3, kDownGroupNB>(a, S, rows, stream);
+    default: return launch_down_group<4, kDownGroupNB>(a, S, rows, stream);
+    }
+}
 
 } // namespace
 
@@ -1736,10 +1980,13 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
             default: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, false, 1>), grid, block, 0, stream, a); break;
             }
         }
-        // down: 32 lanes per row (one slot for I <= 1024), 8 row sets (16 rows) per item;
-        // 8 or 16 lanes per row (fewer idle lanes at 22 chunks) re-read x per fewer rows
-        // and measured slower
-        hipLaunchKernelGGL((moe_gemv_kernel<false, 32, 1, 8, false, 1>), grid, block, 0, stream, a);
+        uint32_t rows = 0;
+        const uint32_t S = down_group_segments(a.T * a.k, a.I, rows);
+        if (S == 0)
+            return hipErrorInvalidValue; // excluded by moe_supported's limits
+        const hipError_t err = down_group_by_slots(a, S, rows, stream);
+        if (err != hipSuccess)
+            return err;
         hipLaunchKernelGGL(moe_combine_kernel, dim3(a.T, (a.H + kCombineCols - 1) / kCombineCols),
                            dim3(256), 0, stream, a);
         return hipGetLastError();

@@ -102,13 +102,15 @@ def test_moe_odd_shapes(path):
 
 
 def test_moe_decode_gemv_variants():
-    """The grouped-GEMV path's other kernel variants: down rows over 16 lanes (I of 30
-    and 32 chunks), gate/up with one and two slots, and x read from global memory
-    (32 tokens of hidden 3072 do not fit the LDS staging), with 256 (token, expert)
-    pairs, the most the path takes."""
+    """The grouped-GEMV path's other kernel variants.  Down by token groups with 1, 2
+    and 4 chunk slots per lane and 1, 2 and 6 LDS segments (256 (token, expert) pairs,
+    the most the path takes, at I = 256 and at I = 1024, the largest it takes); gate/up
+    with one and two slots, and x read from global memory (32 tokens of hidden 3072 do
+    not fit the LDS staging)."""
     rng = np.random.default_rng(11)
     for T, E, H, I, k in [(4, 12, 512, 1024, 2), (5, 9, 1536, 960, 3),
-                          (32, 64, 3072, 256, 8)]:
+                          (32, 64, 3072, 256, 8), (24, 40, 512, 448, 6),
+                          (32, 64, 256, 1024, 8)]:
         x = synth.normal_bf16(rng, (T, H))
         logits = synth.normal_bf16(rng, (T, E))
         slots = synth.expert_slots(rng, E, H, I)
@@ -126,6 +128,24 @@ def test_moe_decode_full_size_both_paths():
     assert rel_l2(got_gemm, want) < TOL_BF16
     # deterministic: a second run is bit-identical
     assert np.array_equal(run_moe(x, logits, slots, 8, 0), got_gemv)
+
+
+def test_moe_decode_hot_experts():
+    """Decode where tokens share experts: 16 or 13 tokens all prefer the same 8 of 128
+    experts (token groups of 4 only, then groups of 4 and 1), and 15 tokens spread over
+    5 hot experts plus one cold pick each (every group size 1..4 present)."""
+    rng = np.random.default_rng(12)
+    E, H, I, k = 128, 2816, 704, 8
+    slots = synth.expert_slots(rng, E, H, I)
+    hot = [3, 17, 18, 40, 77, 90, 101, 127]
+    for T, hot_e, kk in [(16, hot, 8), (13, hot, 8), (15, hot[:5], 6)]:
+        x = synth.normal_bf16(rng, (T, H))
+        lg = rng.standard_normal((T, E), dtype=np.float32)
+        lg[:, hot_e] += 20.0
+        logits = synth.bf16_from_f32(lg)
+        got = run_moe(x, logits, slots, kk, 1)
+        assert rel_l2(got, moe_ref(x, logits, slots, kk)) < TOL_BF16, (T, len(hot_e), kk)
+        assert np.array_equal(run_moe(x, logits, slots, kk, 1), got)
 
 
 def test_moe_hot_experts_span_many_tiles():
