@@ -745,10 +745,11 @@ __device__ __forceinline__ int wave_excl_scan(int x, int lane, int &total) {
 // experts ascending, each expert's tokens ascending), the active list and the token
 // groups (sizes 4, 3, 2, 1 in that order, see moe_gemv_kernel) -> plan; offsets also
 // -> s_off.
-__device__ void plan_from_masks(const MoeArgs &a, const uint32_t *mask, int32_t *s_off, int lane) {
+__device__ void plan_from_masks(const MoeArgs &a, int32_t *plan, const uint32_t *mask, int32_t *s_off,
+                                int lane) {
     static_assert(kTokenGroup == 4 && kMoeMaxExperts == 256, "4 experts per lane, group sizes 4..1");
     const uint32_t E = a.E, P = a.T * a.k;
-    const PlanView v = plan_view(a.plan, E, P);
+    const PlanView v = plan_view(plan, E, P);
     int c[4];
     int sum[6] = {}; // pairs, active experts, groups of 4, of 3, of 2, of 1
 #pragma unroll
@@ -808,40 +809,52 @@ __device__ void plan_from_masks(const MoeArgs &a, const uint32_t *mask, int32_t 
 // no atomics whose order matters: each routed pair sets its token's bit in its
 // expert's mask (LDS atomicOr), one wave turns the masks into the plan, and a pair's
 // position is its expert's offset plus the number of its expert's tokens below its
-// own (so positions do not depend on timing).
-__global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
-    __shared__ uint32_t s_mask[kMoeMaxExperts];
-    __shared__ int32_t s_off[kMoeMaxExperts];
-    __shared__ int32_t s_ids[kMoeGemvMaxPairs];
+// own (so positions do not depend on timing).  The plan goes to `plan` (global memory
+// or an LDS copy); ids and weights go to a.ids / a.w when `write_routes`.
+struct RoutePlanLds {
+    uint32_t mask[kMoeMaxExperts];
+    int32_t off[kMoeMaxExperts];
+    int32_t ids[kMoeGemvMaxPairs];
+};
+
+__device__ void route_plan_block(const MoeArgs &a, int32_t *plan, RoutePlanLds &s, bool write_routes) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const uint32_t k = a.k, P = a.T * k;
-    if (threadIdx.x < kMoeMaxExperts)
-        s_mask[threadIdx.x] = 0;
+    for (uint32_t e = threadIdx.x; e < kMoeMaxExperts; e += blockDim.x)
+        s.mask[e] = 0;
     __syncthreads();
     for (uint32_t t = wave; t < a.T; t += blockDim.x / 64) {
         int32_t id;
         float wt;
         route_token_args(a, t, lane, id, wt);
         if ((uint32_t)lane < k) {
-            a.ids[t * k + lane] = id;
-            a.w[t * k + lane] = wt;
-            s_ids[t * k + lane] = id;
-            atomicOr(&s_mask[id], 1u << t);
+            if (write_routes) {
+                a.ids[t * k + lane] = id;
+                a.w[t * k + lane] = wt;
+            }
+            s.ids[t * k + lane] = id;
+            atomicOr(&s.mask[id], 1u << t);
         }
     }
     __syncthreads();
     if (wave == 0)
-        plan_from_masks(a, s_mask, s_off, lane);
+        plan_from_masks(a, plan, s.mask, s.off, lane);
     __syncthreads();
-    const PlanView v = plan_view(a.plan, a.E, P);
+    const PlanView v = plan_view(plan, a.E, P);
     for (uint32_t p = threadIdx.x; p < P; p += blockDim.x) {
         const uint32_t t = p / k;
-        const int e = s_ids[p];
-        const int pos = s_off[e] + __popc(s_mask[e] & ((1u << t) - 1u));
+        const int e = s.ids[p];
+        const int pos = s.off[e] + __popc(s.mask[e] & ((1u << t) - 1u));
         v.pos_of_pair[p] = pos;
         v.pair_of_pos[pos] = (int32_t)p;
     }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
+    __shared__ RoutePlanLds s;
+    route_plan_block(a, a.plan, s, true);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1018,37 +1031,60 @@ constexpr uint32_t kXLdsBytes = 120 * 1024;
 constexpr int kStagePerThread = 8;
 static_assert(kStagePerThread * kXLdsThreads * 16 >= kXLdsBytes, "one round covers the LDS budget");
 
+// One round of the copy: entries threadIdx.x + k * blockDim.x (k < kStagePerThread)
+// loaded into registers by stage_issue, written to LDS by stage_commit, so independent
+// work can run while the loads are in flight.
+struct StageRegs {
+    u32x4_t v[kStagePerThread];
+    uint32_t dst[kStagePerThread];
+};
+
 template <typename RowOff>
-__device__ __forceinline__ void stage_rows(uint4 *xl, __amdgpu_buffer_rsrc_t rs, uint32_t n_rows,
-                                           int nchunks, RowOff row_off) {
+__device__ __forceinline__ void stage_issue(StageRegs &st, __amdgpu_buffer_rsrc_t rs, uint32_t n_rows,
+                                            int nchunks, uint32_t base, RowOff row_off) {
     const uint32_t nc = (uint32_t)nchunks + 1, n = n_rows * 4 * nc;
-    for (uint32_t base = 0; base < n; base += kStagePerThread * blockDim.x) {
-        u32x4_t v[kStagePerThread];
-        uint32_t dst[kStagePerThread];
 #pragma unroll
-        for (int k = 0; k < kStagePerThread; ++k) {
-            const uint32_t i = base + threadIdx.x + k * blockDim.x;
-            uint32_t off = kOutOfRange;
-            dst[k] = 0xFFFFFFFFu;
-            if (i < n) {
-                const uint32_t r = i / (4 * nc), rem = i % (4 * nc);
-                const uint32_t c = rem / 4, q = rem % 4;
-                if ((int)c < nchunks)
-                    off = row_off(r) + c * 64 + q * 16;
-                dst[k] = (r * 4 + q) * nc + c;
-            }
-            v[k] = load_b128(rs, off);
+    for (int k = 0; k < kStagePerThread; ++k) {
+        const uint32_t i = base + threadIdx.x + k * blockDim.x;
+        uint32_t off = kOutOfRange;
+        st.dst[k] = 0xFFFFFFFFu;
+        if (i < n) {
+            const uint32_t r = i / (4 * nc), rem = i % (4 * nc);
+            const uint32_t c = rem / 4, q = rem % 4;
+            if ((int)c < nchunks)
+                off = row_off(r) + c * 64 + q * 16;
+            st.dst[k] = (r * 4 + q) * nc + c;
         }
-#pragma unroll
-        for (int k = 0; k < kStagePerThread; ++k)
-            if (dst[k] != 0xFFFFFFFFu)
-                xl[dst[k]] = __builtin_bit_cast(uint4, v[k]);
+        st.v[k] = load_b128(rs, off);
     }
 }
 
-template <bool GATE_UP, int G, int SLOTS, int NB, bool XLDS, int TG>
+__device__ __forceinline__ void stage_commit(const StageRegs &st, uint4 *xl) {
+#pragma unroll
+    for (int k = 0; k < kStagePerThread; ++k)
+        if (st.dst[k] != 0xFFFFFFFFu)
+            xl[st.dst[k]] = __builtin_bit_cast(uint4, st.v[k]);
+}
+
+template <typename RowOff>
+__device__ __forceinline__ void stage_rows(uint4 *xl, __amdgpu_buffer_rsrc_t rs, uint32_t n_rows,
+                                           int nchunks, RowOff row_off) {
+    const uint32_t n = n_rows * 4 * ((uint32_t)nchunks + 1);
+    for (uint32_t base = 0; base < n; base += kStagePerThread * blockDim.x) {
+        StageRegs st;
+        stage_issue(st, rs, n_rows, nchunks, base, row_off);
+        stage_commit(st, xl);
+    }
+}
+
+// Plan words of the decode regime (header, counts, offsets, active list, both position
+// maps and the token groups; no m-tiles) at the largest E and T * k.
+constexpr uint32_t kDecodePlanWords = kMoePlanHeader + 3 * kMoeMaxExperts + 1 + 4 * kMoeGemvMaxPairs;
+
+template <bool GATE_UP, int G, int SLOTS, int NB, bool XLDS, int TG, bool ROUTE = false>
 __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 256 : 4) void moe_gemv_kernel(MoeArgs a) {
     static_assert(TG == 1 || (XLDS && TG == kTokenGroup), "token groups read x from LDS");
+    static_assert(!ROUTE || (GATE_UP && XLDS), "routing runs in the gate/up kernel with x in LDS");
     constexpr int R = 64 / G;          // rows per row set
     constexpr int NM = GATE_UP ? 2 : 1;
     constexpr int NR = NM * NB;
@@ -1065,13 +1101,35 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     const uint32_t P = a.T * a.k, H = a.H, I = a.I;
     const uint32_t K = GATE_UP ? H : I, rows = GATE_UP ? I : H;
     const int nchunks = (int)(K / 32);
-    const PlanView v = plan_view(a.plan, a.E, P);
+    // ROUTE: every workgroup routes the T tokens and plans into LDS itself (the same
+    // deterministic plan everywhere, no launch of its own); workgroup 0 also writes the
+    // routes and the plan to global memory for the down and combine kernels.
+    int32_t *plan = a.plan;
+    const int32_t *ids = a.ids;
     const __amdgpu_buffer_rsrc_t rx =
         GATE_UP ? make_rsrc(a.x, a.T * H * 2) : make_rsrc(a.h, P * I * 2);
+    auto x_row = [&](uint32_t t) { return t * K * 2; };
+    if constexpr (ROUTE) {
+        __shared__ int32_t s_plan[kDecodePlanWords];
+        __shared__ RoutePlanLds s_rp;
+        // x's loads fly while the tokens are routed (the host keeps x within one round)
+        StageRegs st;
+        stage_issue(st, rx, a.T, nchunks, 0, x_row);
+        route_plan_block(a, s_plan, s_rp, blockIdx.x == 0);
+        stage_commit(st, xl);
+        if (blockIdx.x == 0) {
+            const uint32_t words = kMoePlanHeader + 3 * a.E + 1 + 4 * P;
+            for (uint32_t i = threadIdx.x; i < words; i += blockDim.x)
+                a.plan[i] = s_plan[i];
+        }
+        plan = s_plan;
+        ids = s_rp.ids;
+    }
+    const PlanView v = plan_view(plan, a.E, P);
     for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
         const uint32_t pair = (uint32_t)v.pair_of_pos[i];
         if constexpr (TG == 1)
-            s_exp[i] = a.ids[pair];
+            s_exp[i] = ids[pair];
         s_xrow[i] = GATE_UP ? pair / a.k : i;
     }
     uint32_t ncls[kTokenGroup] = {}; // TG > 1: groups of size 4, 3, 2, 1
@@ -1087,8 +1145,8 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
             s_grp[i] = (uint32_t)v.groups[2 * i + 1];
         }
     }
-    if constexpr (XLDS)
-        stage_rows(xl, rx, a.T, nchunks, [&](uint32_t t) { return t * K * 2; });
+    if constexpr (XLDS && !ROUTE)
+        stage_rows(xl, rx, a.T, nchunks, x_row);
     __syncthreads();
     const uint32_t wave = uniform(threadIdx.x >> 6);
     const uint32_t waves_per_block = blockDim.x / 64;
@@ -1948,10 +2006,10 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     if (a.T == 0)
         return hipSuccess;
     if (!gemm) {
-        hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(1024), 0, stream, a);
         const dim3 grid((uint32_t)num_cus() * kGemvBlocksPerCU), block(256);
         // gate/up: 32 lanes per row; x staged in LDS when it fits (one workgroup per
-        // CU), else read per token from global memory
+        // CU, which also routes and plans), else route+plan by its own launch and x
+        // read per token from global memory
         const uint32_t xbytes = a.T * (a.H / 32 + 1) * 64;
         if (xbytes <= kXLdsBytes) {
             static std::atomic<uint64_t> attr[3] = {};
@@ -1959,21 +2017,25 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
             hipError_t err = hipSuccess;
             switch (gemv_slots(a.H, 32)) {
             case 1:
-                err = set_lds(moe_gemv_kernel<true, 32, 1, 2, true, 1>, kXLdsBytes, attr[0]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, true, 1>), lgrid, lblock, xbytes, stream, a);
+                err = set_lds(moe_gemv_kernel<true, 32, 1, 2, true, 1, true>, kXLdsBytes, attr[0]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, true, 1, true>), lgrid, lblock, xbytes,
+                                   stream, a);
                 break;
             case 2:
-                err = set_lds(moe_gemv_kernel<true, 32, 2, 1, true, kTokenGroup>, kXLdsBytes, attr[1]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 1, true, kTokenGroup>), lgrid, lblock, xbytes, stream, a);
+                err = set_lds(moe_gemv_kernel<true, 32, 2, 1, true, kTokenGroup, true>, kXLdsBytes, attr[1]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 1, true, kTokenGroup, true>), lgrid, lblock,
+                                   xbytes, stream, a);
                 break;
             default:
-                err = set_lds(moe_gemv_kernel<true, 32, 3, 1, true, kTokenGroup>, kXLdsBytes, attr[2]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, true, kTokenGroup>), lgrid, lblock, xbytes, stream, a);
+                err = set_lds(moe_gemv_kernel<true, 32, 3, 1, true, kTokenGroup, true>, kXLdsBytes, attr[2]);
+                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, true, kTokenGroup, true>), lgrid, lblock,
+                                   xbytes, stream, a);
                 break;
             }
             if (err != hipSuccess)
                 return err;
         } else {
+            hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(1024), 0, stream, a);
             switch (gemv_slots(a.H, 32)) {
             case 1: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, false, 1>), grid, block, 0, stream, a); break;
             case 2: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 2, false, 1>), grid, block, 0, stream, a); break;
