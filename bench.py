@@ -327,8 +327,8 @@ def time_moe_decode(steps, warmup):
             "distinct_experts": int(U), "slot_copies_rotated": copies,
             "workload": "MoE decode: x bf16 [16,2816], logits bf16 [16,128], top-8, 128 "
                         "experts NVFP4 gate/up [704x2816], down [2816x704], y bf16 [16,2816]",
-            "path": "route+plan, grouped GEMV gate/up with GeGLU, grouped GEMV down by token "
-                    "groups, fixed-order combine (4 launches)"}
+            "path": "grouped GEMV gate/up with routing and planning in every workgroup and "
+                    "GeGLU, grouped GEMV down by token groups, fixed-order combine (3 launches)"}
 
 
 def time_moe_prefill(steps, warmup):
