@@ -35,8 +35,10 @@ inline int num_cus() { return kNumCUs.load(std::memory_order_relaxed); }
 hipError_t gemv_launch(const GemvArgs &a, GemvMode mode, bool x_is_bf16, hipStream_t stream);
 hipError_t geglu_f32_launch(const float *gate, const float *up, float *out, uint32_t count,
                             hipStream_t stream);
-// Streaming-read probe over [p, p+bytes) (bytes < 2 GiB); sink needs 8 * CUs words.
+// Streaming-read probe over [p, p+bytes) (bytes < 2 GiB); sink needs read_probe_blocks()
+// words, one per workgroup of the probe's grid.
 hipError_t read_probe_launch(const void *p, size_t bytes, uint32_t *sink, hipStream_t stream);
+uint32_t read_probe_blocks();
 hipError_t dequant_launch(const uint32_t *codes, const uint8_t *scales, void *out, uint32_t rows,
                           uint32_t K, float tensor_scale, bool bf16, hipStream_t stream);
 

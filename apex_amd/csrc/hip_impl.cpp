@@ -1230,7 +1230,7 @@ int apex_hip_read_probe(const void *ptr, size_t bytes, uint32_t *sink, void *str
     });
 }
 
-int apex_hip_read_probe_sink_words(void) { return 8 * apex_hip::num_cus(); }
+int apex_hip_read_probe_sink_words(void) { return (int)apex_hip::read_probe_blocks(); }
 
 int apex_hip_set_gemm_min_tokens(uint32_t bf16_tokens, uint32_t f32_tokens) {
     return guard([&] {

@@ -11,7 +11,9 @@ The weights are rotated over several copies (> 256 MB MALL) so every step stream
 them from HBM.  Steps are timed with HIP events recorded on the launch stream.
 
 Prints one JSON line: value = algorithmic bytes per step / average step time (GB/s).
-The roofline object prices the same kernel against MI355X's 8 TB/s HBM peak; the
+The roofline object prices the same kernel against MI355X's 8 TB/s HBM peak, and its
+"read_ceiling" times the fastest plain streaming read of the same bytes (rotated the
+same way) for the rate any kernel moving them reaches on this GPU; the
 cpu_baseline object times the reference's own CPU implementation of the op
 (src/tests/cpu_ref.h matvecNvfp4Cpu + geluTanh, compiled from its sources), single-
 threaded like the reference: the headline workload, and under "configs" every
@@ -104,6 +106,27 @@ def time_geglu(steps: int, warmup: int, rows=21504, K=5376):
         "algo_bytes": algo_bytes, "flops": flops, "per_step_s": per_step_s, "wall_s": wall,
         "copies": copies, "rows": rows, "K": K,
     }
+
+
+def time_read_ceiling(nbytes: int, copies: int, steps: int, warmup: int):
+    """The fastest plain streaming read of `nbytes` (the library's read probe, rotated
+    over `copies` buffers like the headline's weights, so the MALL serves none of it):
+    the rate a kernel moving these bytes can reach on this GPU, beside the spec peak."""
+    bufs = [hip.DeviceArray((nbytes,), np.uint8) for _ in range(copies)]
+    for b in bufs:
+        b.fill_bytes(1)
+    sink = hip.DeviceArray((hip.read_probe_sink_words(),), np.uint32)
+    stream = hip.Stream()
+
+    def step(i):
+        hip.read_probe(bufs[i % copies], sink, stream=stream)
+
+    sec, n = time_steps(step, steps, warmup, stream)
+    stream.close()
+    for b in bufs + [sink]:
+        b.close()
+    return {"value": round(nbytes / sec / 1e9, 2), "unit": "GB/s", "us_per_read": round(sec * 1e6, 3),
+            "steps": n, "bytes": int(nbytes), "copies_rotated": copies}
 
 
 # ---- CPU baseline: the reference's own CPU code on every workload ------------------
@@ -682,6 +705,10 @@ def main(argv=None):
             "traffic": load_traffic("geglu_decode"),
         },
     }
+    # the fastest plain read of the same bytes: how far the kernel is from what any
+    # kernel streaming them reaches here
+    ceil = time_read_ceiling(r["algo_bytes"], r["copies"], args.steps, args.warmup)
+    line["roofline"]["read_ceiling"] = {**ceil, "frac_of_ceiling": round(gbs / ceil["value"], 4)}
     if not args.no_secondary:
         # each record: at least MIN_TIMED_STEPS launches and MIN_TIMED_MS of GPU time
         sec_steps, sec_warm = max(1, args.steps // 100), max(2, args.warmup // 100)
