@@ -64,9 +64,12 @@ constexpr uint32_t kOut = 0x80000000u;     // an offset no descriptor covers
 // GEMV re-fetched the lines: 3.8x the L2 misses on the MoE gate/up GEMM).
 constexpr int kWCpol = 0;
 
-template <int MT, int WC = 4> struct Layout {
+// NT (32-row W blocks per wave) defaults to the full 256-row W tile; with WC = 2 and
+// NT = 2 only W rows 0..127 are used (the half-width tile: 2 x 2 waves, both wave rows
+// on the same 128 W rows), the stage layout staying that of 256 rows.
+template <int MT, int WC = 4, int NT = 8 / WC> struct Layout {
     static constexpr int kWR = 4 / WC;
-    static constexpr int kNT = 8 / WC;
+    static constexpr int kNT = NT;
     static constexpr int kBM = 32 * MT * kWR;
     static constexpr int kAStage = kBM * kARow;
     static constexpr int kStage = kAStage + kWCode + kWScale;
@@ -88,7 +91,7 @@ __device__ __forceinline__ uint32_t pack_bf16_hi(float lo, float hi) {
 // `lane` sits at tile row 32 MT (wave / WC) + 32 i + lane % 32 and tile column
 // 32 NT (wave % WC) + 32 j + 8 (e / 4) + 4 (lane / 32) + e % 4 -- a lane holds runs of
 // 4 consecutive columns of one row, which the epilogues pack into 16-byte stores.
-template <int MT, int WC = 4> using Acc = f32x16_t[MT][8 / WC];
+template <int MT, int WC = 4, int NT = 8 / WC> using Acc = f32x16_t[MT][NT];
 
 // bf16 output of one accumulator block: `v` (the lane's 16 values, already through any
 // elementwise epilogue) -> two 16-byte pieces, piece p = columns 16 p + 8 (lane / 32)
@@ -122,20 +125,20 @@ __device__ __forceinline__ void pack_bf16_cols(const f32x16_t &v, u32x4_t (&out)
 template <int MT, int WC> __device__ __forceinline__ int wave_row0() {
     return 32 * MT * ((threadIdx.x >> 6) / WC);
 }
-template <int WC> __device__ __forceinline__ int wave_col0() {
-    return 32 * (8 / WC) * ((threadIdx.x >> 6) % WC);
+template <int WC, int NT = 8 / WC> __device__ __forceinline__ int wave_col0() {
+    return 32 * NT * ((threadIdx.x >> 6) % WC);
 }
 
-template <int MT, int WC, typename ARow, typename WCode, typename WScale>
+template <int MT, int WC, int NT = 8 / WC, typename ARow, typename WCode, typename WScale>
 __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t ra,
                                           const __amdgpu_buffer_rsrc_t (&rc)[2],
                                           const __amdgpu_buffer_rsrc_t (&rs)[2], uint32_t K,
                                           ARow a_row, WCode w_code, WScale w_scale,
-                                          Acc<MT, WC> &acc, uint32_t kw_wrap = 0xFFFFFFFFu) {
-    constexpr int NT = 8 / WC;
+                                          Acc<MT, WC, NT> &acc, uint32_t kw_wrap = 0xFFFFFFFFu) {
+    static_assert(WC * NT * 32 <= BN, "the waves' W blocks lie in the staged W tile");
     constexpr int WR = 4 / WC;
-    constexpr int kAStage = Layout<MT, WC>::kAStage;
-    constexpr int kStage = Layout<MT, WC>::kStage;
+    constexpr int kAStage = Layout<MT, WC, NT>::kAStage;
+    constexpr int kStage = Layout<MT, WC, NT>::kStage;
     constexpr int kARows = 8 * MT * WR;       // A rows each wave copies per stage
     constexpr int kALoads = MT * WR;          // DMA loads of 8 A rows per wave per stage
     constexpr int kLoadsPerStage = kALoads + 2 + 1;
@@ -144,7 +147,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     const int lane = tid & 63;
     // uniform: LDS destinations (M0) and their arithmetic stay in scalar registers
     const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)tid >> 6);
-    const int wn = wave_col0<WC>();      // wave's column offset in the tile
+    const int wn = wave_col0<WC, NT>();  // wave's column offset in the tile
     const int wm = wave_row0<MT, WC>();  // wave's row offset in the tile
     const int frow = lane & 31;     // fragment row (A) / column (B) within a 32-wide tile
     const int h = lane >> 5;        // lane half: k pieces 4h .. 4h+3 of each stage
@@ -461,22 +464,25 @@ __device__ __forceinline__ void store_tile_f32(const Acc<MT, WC> &acc, float *C,
             }
 }
 
-// GeGLU epilogue of a 1 x 4 tile whose W rows interleave two matrices by 32 (tile row r:
-// gate if (r / 32) % 2 == 0, else up; h column c0 + 32 (r / 64) + r % 32), so acc[i][0]
-// and acc[i][1] of a wave hold gate and up of the same h columns c0 + 32 wave +
-// 8 (e / 4) + 4 (lane / 32) + e % 4, token row 32 i + lane % 32:
+// GeGLU epilogue of a tile whose W rows interleave two matrices by 32 (tile row r:
+// gate if (r / 32) % 2 == 0, else up; h column c0 + 32 (r / 64) + r % 32) and whose
+// waves hold two 32-row W blocks each -- the 1 x 4 tile (WC = 4) or the half-width 2 x 2
+// tile (WC = 2, W rows 0..127) -- so acc[i][0] and acc[i][1] of a wave hold gate and up
+// of the same h columns c0 + 32 (wave % WC) + 8 (e / 4) + 4 (lane / 32) + e % 4, token
+// row 32 MT (wave / WC) + 32 i + lane % 32:
 //   out[r][c] = gelu_tanh(gate_scale * gate) * (up_scale * up), r < nrows, c < ncols,
 // `out` at the tile's first token row, row stride ldc (shaders/geglu.metal:15-23).
 // OutT uint16_t (bf16 bits, round to nearest even) or float.  `wide`: 16-byte stores
 // (bf16: ncols and ldc multiples of 8; fp32: of 4; out 16-byte aligned), else one
 // store per element.
-template <int MT, typename OutT>
-__device__ __forceinline__ void store_tile_geglu(const Acc<MT, 4> &acc, OutT *out, uint32_t ldc,
+template <int MT, typename OutT, int WC = 4>
+__device__ __forceinline__ void store_tile_geglu(const Acc<MT, WC, 2> &acc, OutT *out, uint32_t ldc,
                                                  uint32_t nrows, uint32_t c0, uint32_t ncols,
                                                  float gate_scale, float up_scale, bool wide) {
     const int lane = threadIdx.x & 63;
-    const uint32_t wcol = c0 + 32 * (threadIdx.x >> 6);  // the wave's first h column
-    const uint32_t row = lane & 31;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t wcol = c0 + 32 * (wave % WC);                  // the wave's first h column
+    const uint32_t row = 32 * MT * (wave / WC) + (lane & 31);     // and its first row
     const uint64_t bytes = (uint64_t)nrows * ldc * sizeof(OutT);
     const __amdgpu_buffer_rsrc_t rh =
         make_rsrc(out, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);

@@ -1440,7 +1440,10 @@ __global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_gro
 using namespace gemm_core;
 constexpr int kGateUpCols = BN / 2; // h columns per gate/up tile
 
-template <int MT>
+// HALF: the tile's h columns past c0 + 64 do not exist (the last n-tile when I % 128 ==
+// 64), so it runs as the half-width tile -- 2 x 2 waves on W rows 0..127, each wave row
+// on half the token rows -- instead of leaving two of the four waves on zero W rows.
+template <int MT, bool HALF>
 __device__ __forceinline__ void gateup_tile(const MoeArgs &a, uint8_t *lds, const int32_t *pair_of_pos,
                                             int e, uint32_t row0, uint32_t nrows, uint32_t c0) {
     const uint32_t H = a.H, I = a.I, k = a.k;
@@ -1462,11 +1465,13 @@ __device__ __forceinline__ void gateup_tile(const MoeArgs &a, uint8_t *lds, cons
         return col < I ? ((r & 32) ? us : gs) + col * (H / 16) : kOut;
     };
     const __amdgpu_buffer_rsrc_t rw2[2] = {rw, rw};
-    Acc<MT, 4> acc;
-    gemm_tile<MT, 4>(lds, ra, rw2, rw2, H, a_row, w_code, w_scale, acc);
     // h[row0 + r][col] = gelu(gate) * up, 16-byte stores (I is a multiple of 64, so
     // 8-column pieces never straddle it); the store descriptor ends at row nrows.
-    store_tile_geglu<MT, uint16_t>(acc, a.h + (size_t)row0 * I, I, nrows, c0, I, 1.0f, 1.0f, true);
+    constexpr int MTW = HALF ? MT / 2 : MT; // 32-row A blocks per wave
+    constexpr int WC = HALF ? 2 : 4;
+    Acc<MTW, WC, 2> acc;
+    gemm_tile<MTW, WC, 2>(lds, ra, rw2, rw2, H, a_row, w_code, w_scale, acc);
+    store_tile_geglu<MTW, uint16_t, WC>(acc, a.h + (size_t)row0 * I, I, nrows, c0, I, 1.0f, 1.0f, true);
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup b on XCD b % 8).
@@ -1493,12 +1498,19 @@ __global__ __launch_bounds__(kThreads) void moe_gateup_gemm_kernel(MoeArgs a) {
     const int32_t *t = v.tiles + 4 * mt;
     const int e = uniform(t[0]), cls = uniform(t[3]);
     const uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]), c0 = nt * kGateUpCols;
-    if (cls == 0)
-        gateup_tile<8>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
+    if (c0 + kGateUpCols / 2 >= a.I) { // 64 h columns left
+        if (cls == 0)
+            gateup_tile<8, true>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
+        else if (cls == 1)
+            gateup_tile<4, true>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
+        else
+            gateup_tile<2, true>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
+    } else if (cls == 0)
+        gateup_tile<8, false>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
     else if (cls == 1)
-        gateup_tile<4>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
+        gateup_tile<4, false>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
     else
-        gateup_tile<2>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
+        gateup_tile<2, false>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
 }
 
 template <int MT>
