@@ -997,9 +997,10 @@ __device__ __forceinline__ void rows_dot_group(float (&out)[TG][NR], const RowRe
         pass(std::true_type{});
 }
 
-// Grouped GEMV over the routed (token, expert) pairs, in items of equal cost per
+// Decode gate/up GEMV over the routed (token, expert) pairs, in items of equal cost per
 // class that persistent waves walk round-robin, so they get equal shares however
-// unevenly the tokens spread over experts.
+// unevenly the tokens spread over experts.  K = H, gate and up rows side by side, GeGLU
+// in registers -> h[pos][row] (bf16).
 //   TG == 1: item (rb, pos) = row block rb (NB row sets of 64/G rows) of pos's expert
 //     dotted with pos's activation row; item i = (i / P, i % P), so the n positions
 //     of one expert are consecutive and the n items streaming the same weight rows
@@ -1009,14 +1010,13 @@ __device__ __forceinline__ void rows_dot_group(float (&out)[TG][NR], const RowRe
 //     Items are dealt class by class (groups of 4 tokens first, then 3, 2, 1), each
 //     class rb-major, round-robin over workgroups first, so every CU and SIMD gets an
 //     equal share of every cost class.
-//   GATE_UP: K = H, gate and up rows side by side, GeGLU -> h[pos][row] (bf16).
-//   else:    K = I, down rows, x = h[pos] -> d[pos][row] (bf16).
 // XLDS: all T activation rows are staged in LDS once per workgroup (piece-major, so
 // a wave's 16-byte reads of one piece of consecutive chunks are conflict-free) and
 // read from there; otherwise each item's row is loaded from global memory (L2).
 // Double-buffering the weights (next item's loads during this item's arithmetic)
 // measured slower at every shape: four waves per SIMD already cover the latency and
-// the second register set costs occupancy or spills.
+// the second register set costs occupancy or spills.  (The down GEMV is
+// moe_down_group_kernel.)
 constexpr int kGemvBlocksPerCU = 4; // 256-thread workgroups per CU (global x)
 constexpr int kXLdsThreads = 1024;  // x in LDS: one workgroup of 16 waves per CU
 constexpr uint32_t kXLdsBytes = 120 * 1024;
@@ -1081,12 +1081,12 @@ __device__ __forceinline__ void stage_rows(uint4 *xl, __amdgpu_buffer_rsrc_t rs,
 // maps and the token groups; no m-tiles) at the largest E and T * k.
 constexpr uint32_t kDecodePlanWords = kMoePlanHeader + 3 * kMoeMaxExperts + 1 + 4 * kMoeGemvMaxPairs;
 
-template <bool GATE_UP, int G, int SLOTS, int NB, bool XLDS, int TG, bool ROUTE = false>
+template <int G, int SLOTS, int NB, bool XLDS, int TG, bool ROUTE = false>
 __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 256 : 4) void moe_gemv_kernel(MoeArgs a) {
     static_assert(TG == 1 || (XLDS && TG == kTokenGroup), "token groups read x from LDS");
-    static_assert(!ROUTE || (GATE_UP && XLDS), "routing runs in the gate/up kernel with x in LDS");
+    static_assert(!ROUTE || XLDS, "routing runs in the workgroups that stage x in LDS");
     constexpr int R = 64 / G;          // rows per row set
-    constexpr int NM = GATE_UP ? 2 : 1;
+    constexpr int NM = 2; // gate, up
     constexpr int NR = NM * NB;
     // TG == 1: s_exp[pos] = expert of grouped position pos.  TG > 1: s_exp[g] = expert
     // of group g, s_grp[g] = its first position | size << 16.  s_xrow[pos] = activation
@@ -1099,15 +1099,14 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     const int lane = threadIdx.x & 63;
     const int sub = lane / G, gl = lane % G;
     const uint32_t P = a.T * a.k, H = a.H, I = a.I;
-    const uint32_t K = GATE_UP ? H : I, rows = GATE_UP ? I : H;
+    const uint32_t K = H, rows = I;
     const int nchunks = (int)(K / 32);
     // ROUTE: every workgroup routes the T tokens and plans into LDS itself (the same
     // deterministic plan everywhere, no launch of its own); workgroup 0 also writes the
     // routes and the plan to global memory for the down and combine kernels.
     int32_t *plan = a.plan;
     const int32_t *ids = a.ids;
-    const __amdgpu_buffer_rsrc_t rx =
-        GATE_UP ? make_rsrc(a.x, a.T * H * 2) : make_rsrc(a.h, P * I * 2);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.T * H * 2);
     auto x_row = [&](uint32_t t) { return t * K * 2; };
     if constexpr (ROUTE) {
         __shared__ int32_t s_plan[kDecodePlanWords];
@@ -1130,7 +1129,7 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
         const uint32_t pair = (uint32_t)v.pair_of_pos[i];
         if constexpr (TG == 1)
             s_exp[i] = ids[pair];
-        s_xrow[i] = GATE_UP ? pair / a.k : i;
+        s_xrow[i] = pair / a.k;
     }
     uint32_t ncls[kTokenGroup] = {}; // TG > 1: groups of size 4, 3, 2, 1
     uint32_t ng = 0;
@@ -1155,8 +1154,8 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     const bool last_ok = gl + (SLOTS - 1) * G < nchunks;
     const uint32_t last_c = last_ok ? (SLOTS - 1) * G * 16 : kOutOfRange;
     const uint32_t last_s = last_ok ? (SLOTS - 1) * G * 2 : kOutOfRange;
-    const uint64_t off_w[2] = {GATE_UP ? a.slots.gate_w : a.slots.down_w, a.slots.up_w};
-    const uint64_t off_s[2] = {GATE_UP ? a.slots.gate_s : a.slots.down_s, a.slots.up_s};
+    const uint64_t off_w[2] = {a.slots.gate_w, a.slots.up_w};
+    const uint64_t off_s[2] = {a.slots.gate_s, a.slots.up_s};
     const uint32_t wbytes = rows * K / 2, sbytes = rows * K / 16;
     const uint32_t nw = gridDim.x * waves_per_block;
 
@@ -1215,10 +1214,7 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
             const uint32_t row = r0 + b * R + sub;
             if (row >= rows)
                 continue;
-            if constexpr (GATE_UP)
-                a.h[(size_t)pos * I + row] = f32_to_bf16_bits(gelu_tanh_fast(dots[b]) * dots[NB + b]);
-            else
-                a.d[(size_t)pos * H + row] = f32_to_bf16_bits(dots[b]);
+            a.h[(size_t)pos * I + row] = f32_to_bf16_bits(gelu_tanh_fast(dots[b]) * dots[NB + b]);
         }
     };
     // Item it's rows (loaded into `w`) against its activation rows.
@@ -2029,18 +2025,18 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
             hipError_t err = hipSuccess;
             switch (gemv_slots(a.H, 32)) {
             case 1:
-                err = set_lds(moe_gemv_kernel<true, 32, 1, 2, true, 1, true>, kXLdsBytes, attr[0]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, true, 1, true>), lgrid, lblock, xbytes,
+                err = set_lds(moe_gemv_kernel<32, 1, 2, true, 1, true>, kXLdsBytes, attr[0]);
+                hipLaunchKernelGGL((moe_gemv_kernel<32, 1, 2, true, 1, true>), lgrid, lblock, xbytes,
                                    stream, a);
                 break;
             case 2:
-                err = set_lds(moe_gemv_kernel<true, 32, 2, 1, true, kTokenGroup, true>, kXLdsBytes, attr[1]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 1, true, kTokenGroup, true>), lgrid, lblock,
+                err = set_lds(moe_gemv_kernel<32, 2, 1, true, kTokenGroup, true>, kXLdsBytes, attr[1]);
+                hipLaunchKernelGGL((moe_gemv_kernel<32, 2, 1, true, kTokenGroup, true>), lgrid, lblock,
                                    xbytes, stream, a);
                 break;
             default:
-                err = set_lds(moe_gemv_kernel<true, 32, 3, 1, true, kTokenGroup, true>, kXLdsBytes, attr[2]);
-                hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, true, kTokenGroup, true>), lgrid, lblock,
+                err = set_lds(moe_gemv_kernel<32, 3, 1, true, kTokenGroup, true>, kXLdsBytes, attr[2]);
+                hipLaunchKernelGGL((moe_gemv_kernel<32, 3, 1, true, kTokenGroup, true>), lgrid, lblock,
                                    xbytes, stream, a);
                 break;
             }
@@ -2049,9 +2045,9 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
         } else {
             hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(1024), 0, stream, a);
             switch (gemv_slots(a.H, 32)) {
-            case 1: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 1, 2, false, 1>), grid, block, 0, stream, a); break;
-            case 2: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 2, 2, false, 1>), grid, block, 0, stream, a); break;
-            default: hipLaunchKernelGGL((moe_gemv_kernel<true, 32, 3, 1, false, 1>), grid, block, 0, stream, a); break;
+            case 1: hipLaunchKernelGGL((moe_gemv_kernel<32, 1, 2, false, 1>), grid, block, 0, stream, a); break;
+            case 2: hipLaunchKernelGGL((moe_gemv_kernel<32, 2, 2, false, 1>), grid, block, 0, stream, a); break;
+            default: hipLaunchKernelGGL((moe_gemv_kernel<32, 3, 1, false, 1>), grid, block, 0, stream, a); break;
             }
         }
         uint32_t rows = 0;

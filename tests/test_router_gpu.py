@@ -29,6 +29,24 @@ def router_logits(h, rw):
     return out.numpy()
 
 
+def test_router_small_shape_then_larger_shape():
+    """Each router kernel first runs a small shape, then a larger one with more dynamic
+    LDS: the LDS limit is raised once, to the kernel's largest possible size, so the
+    second call must launch.  Placed first in the file so these are the process's first
+    router launches.  VALU form (more than 256 tokens: 8-token tiles): 257 tokens at
+    H 64, E 8, then 300 at H 2816, E 64.  MFMA form (from 512 tokens): 512 tokens at
+    H 1024, E 8, then 8192 at H 2816, E 128, checked on a 64-token sample."""
+    rng = np.random.default_rng(21)
+    for T, E, H, sample in [(257, 8, 64, None), (300, 64, 2816, None),
+                            (512, 8, 1024, None), (8192, 128, 2816, 64)]:
+        h, rw = synth.router_case(seed=T + E, tokens=T, E=E, H=H)
+        print(f"router logits T={T} E={E} H={H}", flush=True)
+        got = router_logits(h, rw)
+        rows = np.arange(T) if sample is None else np.sort(rng.choice(T, sample, replace=False))
+        want = oracle.moe_router_logits(h[rows], rw.norm_w, rw.qw, rw.qs, rw.qb, EPS)
+        assert rel_l2(got[rows], want) < 1e-5, (T, E, H)
+
+
 @pytest.mark.parametrize("T,E,H", [(1, 128, 2816), (16, 128, 2816), (300, 128, 2816),
                                    (33, 64, 256), (9, 200, 4096), (257, 8, 64),
                                    (600, 128, 2816), (515, 200, 1024), (512, 8, 4096)])
