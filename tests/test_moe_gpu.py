@@ -106,11 +106,11 @@ def test_moe_decode_gemv_variants():
     and 4 chunk slots per lane and 1, 2 and 6 LDS segments (256 (token, expert) pairs,
     the most the path takes, at I = 256 and at I = 1024, the largest it takes); gate/up
     with one and two slots, and x read from global memory (32 tokens of hidden 3072 do
-    not fit the LDS staging)."""
+    not fit the LDS staging); 256 experts with top-16 at 16 tokens and at 1 token."""
     rng = np.random.default_rng(11)
     for T, E, H, I, k in [(4, 12, 512, 1024, 2), (5, 9, 1536, 960, 3),
                           (32, 64, 3072, 256, 8), (24, 40, 512, 448, 6),
-                          (32, 64, 256, 1024, 8)]:
+                          (32, 64, 256, 1024, 8), (16, 256, 512, 256, 16), (1, 256, 512, 704, 16)]:
         x = synth.normal_bf16(rng, (T, H))
         logits = synth.normal_bf16(rng, (T, E))
         slots = synth.expert_slots(rng, E, H, I)
