@@ -1270,12 +1270,13 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
 // positions of one expert, see plan_from_masks), and 8-lane row groups keep 22 of
 // every 24 chunk slots busy at I = 704 (32-lane groups: 22 of 32).  Measured against
 // the per-position kernel: 18 vs 28 us (8 experts), 26 vs 30 us (83 experts of 128
-// positions), 34 vs 31 us (128 experts, no group larger than 1: the 8-lane groups read
-// 4x the x bytes per weight byte from LDS).  The groups' h rows are read from LDS.  All P rows
-// need not fit: the groups are split over S segments, group g in segment g % S (so every
-// size class splits evenly), workgroup b serves segment b % S and stages only its
-// segment's rows -- per class at most one group more than an even share, so at most
-// ceil(P / S) + 10 rows, which the host sizes `cap` and S for.
+// positions), 34 vs 31 us (128 experts, no group larger than 1: the 8-lane groups
+// read 4x the x bytes per weight byte from LDS).
+//   The groups' h rows are read from LDS, and all P rows need not fit: the groups are
+// split over S segments, group g in segment g % S (so every size class splits
+// evenly), workgroup b serves segment b % S and stages only its segment's rows -- per
+// class at most one group more than an even share, so at most ceil(P / S) + 10 rows,
+// which the host sizes `cap` and S for.
 //   Items (row block rb of R * NB rows, group i of the segment) are dealt class by class
 // (groups of 4, 3, 2, 1 positions), rb-major, round-robin over the segment's workgroups
 // first, so every CU and SIMD gets an even share of each cost class.  The first item's
