@@ -184,3 +184,50 @@ def test_fused_geglu_every_scale_code():
     want = geglu_oracle(bf16(x), gate, up)
     got = run_geglu(bf16(x), gate, up, False)
     assert rel_l2(got, want) < TOL_REF_GATE
+
+
+def test_gemv_embedding_rows():
+    """The largest GEMV a matmulNvfp4 caller has: the embedding table used as a linear
+    layer, 262,144 rows x K 2816 (embed_tokens.weight [262144, 352] u32 in the model
+    listing), batch 1, fp32 and bf16 activations; the oracle checks 2048 sampled rows."""
+    rng = np.random.default_rng(31)
+    rows, K = 262144, 2816
+    w = synth.nvfp4_weights(rng, rows, K)
+    sample = np.sort(rng.choice(rows, 2048, replace=False))
+    for bf16_io in (False, True):
+        x = synth.normal_bf16(rng, (1, K)) if bf16_io else rng.standard_normal((1, K), dtype=np.float32)
+        got = run_matmul(x, w, bf16_io)
+        got = bf16(got) if bf16_io else got
+        want = oracle.matvec(w.codes[sample], w.scales[sample], bf16(x) if bf16_io else x)
+        assert rel_l2(got[:, sample], want) < (TOL_BF16 if bf16_io else TOL_REF_GATE), bf16_io
+
+
+def test_zero_tokens_write_nothing():
+    """tokens = 0 is a valid call: the matmul (fp32 and bf16 activations), the fused GeGLU
+    and the MoE FFN return success and leave their outputs as they were."""
+    rng = np.random.default_rng(32)
+    rows, K = 64, 256
+    w = synth.nvfp4_weights(rng, rows, K)
+    dw = (dev(w.codes), dev(w.scales))
+    for f, xt, ot in [(hip.nvfp4_matmul_f32, np.float32, np.float32),
+                      (hip.nvfp4_matmul_bf16, np.uint16, np.uint16)]:
+        out = hip.DeviceArray((1, rows), ot)
+        out.fill_bytes(0x5A)
+        f(dev(np.zeros((1, K), xt)), *dw, out, 0, rows, K)
+        hip.synchronize()
+        assert np.all(out.numpy().view(np.uint8) == 0x5A)
+    out = hip.DeviceArray((1, rows), np.uint16)
+    out.fill_bytes(0x5A)
+    hip.nvfp4_geglu_bf16(dev(np.zeros((1, K), np.uint16)), *dw, *dw, out, 0, rows, K)
+    hip.synchronize()
+    assert np.all(out.numpy().view(np.uint8) == 0x5A)
+    E, H, I = 8, 256, 128
+    slots = synth.expert_slots(rng, E, H, I)
+    ds = dev(slots.data)
+    y = hip.DeviceArray((1, H), np.uint16)
+    y.fill_bytes(0x5A)
+    ws = hip.DeviceArray((hip.moe_workspace_bytes(1, E, 2, H, I),), np.uint8)
+    hip.moe_ffn_bf16(dev(np.zeros((1, H), np.uint16)), dev(np.zeros((1, E), np.uint16)),
+                     hip.moe_slots(ds, slots.stride, slots.offsets), y, 0, E, 2, H, I, ws)
+    hip.synchronize()
+    assert np.all(y.numpy().view(np.uint8) == 0x5A)
