@@ -199,3 +199,38 @@ def test_moe_rejects_bad_layout():
     slots = synth.expert_slots(rng, E, H, I)
     with pytest.raises(hip.ApexHipError, match="multiples of 64"):
         hip.moe_forward(x, logits, slots, top_k=2)
+
+
+def _random_moe_shapes(seed, n):
+    """n seeded (T, E, k, H, I) shapes within the grouped-GEMV path's limits (T <= 32,
+    T * k <= 256, H <= 3072, I <= 1024, multiples of 64), E capped so the expert slots
+    stay small; I % 128 == 64 half the time (the half-width last gate/up tile)."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    while len(shapes) < n:
+        T = int(rng.integers(1, 33))
+        H = 64 * int(rng.integers(1, 49))
+        I = 64 * int(rng.integers(1, 17))
+        E = int(rng.integers(1, 257))
+        E = max(1, min(E, int(96e6 // (H * I))))
+        k = int(rng.integers(1, min(16, E) + 1))
+        if T * k <= 256:
+            shapes.append((T, E, k, H, I))
+    return shapes
+
+
+@pytest.mark.parametrize("path", [1, 2])
+def test_moe_random_shapes(path):
+    """12 seeded random shapes per path (grouped GEMV decode, grouped MFMA GEMM prefill),
+    normal or hot-expert routing, against the oracle."""
+    rng = np.random.default_rng(40 + path)
+    for T, E, k, H, I in _random_moe_shapes(50 + path, 12):
+        x = synth.normal_bf16(rng, (T, H))
+        lg = rng.standard_normal((T, E), dtype=np.float32)
+        if rng.random() < 0.5:
+            lg[:, rng.choice(E, min(E, k), replace=False)] += 8.0  # tokens share experts
+        logits = synth.bf16_from_f32(lg)
+        slots = synth.expert_slots(rng, E, H, I)
+        print(f"moe path {path} T={T} E={E} k={k} H={H} I={I}", flush=True)
+        got = run_moe(x, logits, slots, k, path)
+        assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16, (T, E, k, H, I)
