@@ -304,3 +304,25 @@ def test_dense_dispatch_boundaries_by_size(T):
     hip.nvfp4_matmul_bf16(dev(xb), dev(g.codes), dev(g.scales), out, T, N, K)
     hip.synchronize()
     assert rel_l2(bf16(out.numpy()), oracle.matvec(g.codes, g.scales, xf)) < TOL_BF16
+
+
+def test_dense_random_shapes(gemm_threshold):
+    """Seeded random shapes through the MFMA GEMM paths (every token count takes the
+    GEMM here): bf16 matmul, fp32 matmul (hi + lo split, split-K when the tiles are few)
+    and fused GeGLU (bf16 and fp32), M 1..300, N 1..800, K a multiple of 64 up to 2048,
+    against the oracle."""
+    rng = np.random.default_rng(60)
+    for _ in range(8):
+        M, N, K = int(rng.integers(1, 301)), int(rng.integers(1, 801)), 64 * int(rng.integers(1, 33))
+        print(f"dense GEMM M={M} N={N} K={K}", flush=True)
+        w = synth.nvfp4_weights(rng, N, K)
+        A = synth.normal_bf16(rng, (M, K))
+        want = oracle.matvec(w.codes, w.scales, bf16(A))
+        assert rel_l2(bf16(gemm(A, w)), want) < TOL_BF16, (M, N, K)
+        X = rng.standard_normal((M, K), dtype=np.float32)
+        assert rel_l2(run_matmul_f32(X, w), oracle.matvec(w.codes, w.scales, X)) < TOL_REF_GATE, (M, N, K)
+        u = synth.nvfp4_weights(rng, N, K)
+        gx = oracle.geglu(oracle.matvec(w.codes, w.scales, bf16(A)), oracle.matvec(u.codes, u.scales, bf16(A)))
+        assert rel_l2(run_geglu(A, w, u, False), gx) < TOL_BF16, (M, N, K)
+        gx = oracle.geglu(oracle.matvec(w.codes, w.scales, X), oracle.matvec(u.codes, u.scales, X))
+        assert rel_l2(run_geglu(X, w, u, True), gx) < TOL_REF_GATE, (M, N, K)
