@@ -28,6 +28,14 @@ bool gemm_supported(uint32_t M, uint32_t N, uint32_t K, uint32_t a_k, bool out_f
 
 hipError_t gemm_launch(const GemmArgs &a, hipStream_t stream);
 
+// How gemm_launch covers C on ncu CUs: whole tiles (256 x 256; GeGLU 256 rows x 128 h
+// columns) for the first nf n-tiles, narrow tiles of nt (1 or 2) 32-row W blocks for
+// the columns past them; nt = 0: whole tiles only (nf = all n-tiles).
+struct GemmTailPlan {
+    uint32_t nf, nt;
+};
+GemmTailPlan gemm_tail_plan(uint32_t M, uint32_t N, bool geglu, uint32_t ncu);
+
 // Split-K form for grids of few tiles: S workgroups per tile each run a contiguous
 // range of K stages (for a_k = 2K none crosses from the hi half to the lo half) and
 // store fp32 partials, part[S][M][N] (GeGLU: gate and up, part[S][2][M][N]); a second

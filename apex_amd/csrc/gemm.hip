@@ -24,6 +24,7 @@
 // buffer descriptors: rows past M or N read zeros; stores are guarded.
 #include "gemm.h"
 #include "gemm_core.h"
+#include "gemv.h"
 #include "lds_attr.h"
 
 #include <algorithm>
@@ -43,21 +44,15 @@ template <bool GEGLU, bool F32> __device__ __forceinline__ bool uniform_wide(con
     return a.N % q == 0 && a.ldc % q == 0 && ((uintptr_t)a.C & 15) == 0;
 }
 
-template <bool GEGLU, bool F32>
-__global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr uint32_t TN = GEGLU ? kGegluCols : BN;
-
-    const uint32_t tiles_m = (a.M + BM - 1) / BM;
-    const uint32_t tiles_n = (a.N + TN - 1) / TN;
-    const uint32_t tiles = tiles_m * tiles_n;
-    const uint32_t per_xcd = (tiles + 7) / 8;
-    const uint32_t t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (t >= tiles)
-        return;
-    const uint32_t m0 = (t % tiles_m) * BM;
-    const uint32_t n0 = (t / tiles_m) * TN;
-
+// One tile of C: rows [m0, m0 + 256), W tile rows n0 + w_row(r) for r < 32 NTW WCW
+// (plain: output columns n0 .. n0 + 32 NTW WCW - 1; GeGLU: h columns n0 .. n0 + 16 NTW
+// WCW - 1).  The
+// 256 x 256 tile is the 1 x 4 layout (MT 8, NTW 8); a narrow tile is the 4 x 1 layout,
+// each wave on 64 rows and all NTW W blocks (MT 2): the same 256 A rows per stage, the
+// decode of each W element 4 times (once per wave) but the tile as short as its width.
+template <bool GEGLU, bool F32, int MTW, int WCW, int NTW, int VPM>
+__device__ __forceinline__ void gemm_one_tile(const GemmArgs &a, uint8_t *lds, uint32_t m0,
+                                              uint32_t n0) {
     const uint32_t K = a.K, ak = a.a_k;
     const uint32_t M = a.M, N = a.N;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.A, M * ak * 2);
@@ -67,37 +62,117 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a) {
                                           make_rsrc(a.scales[GEGLU ? 1 : 0], N * (K / 16))};
     auto a_row = [=](int r) { return m0 + r < M ? (m0 + r) * ak * 2 : kOut; };
     // W tile row r -> row of its matrix: plain n0 + r; GeGLU n0 + 32 (r / 64) + r % 32
-    // (the matrix, (r / 32) % 2, is the descriptor's)
+    // (the matrix, (r / 32) % 2, is the descriptor's); rows past the tile's width read
+    // nothing
     auto w_row = [=](int r) { return GEGLU ? n0 + 32 * (r / 64) + r % 32 : n0 + r; };
-    auto w_code = [=](int r) { return w_row(r) < N ? w_row(r) * (K / 2) : kOut; };
-    auto w_scale = [=](int r) { return w_row(r) < N ? w_row(r) * (K / 16) : kOut; };
+    auto w_ok = [=](int r) { return r < 32 * NTW * WCW && w_row(r) < N; };
+    auto w_code = [=](int r) { return w_ok(r) ? w_row(r) * (K / 2) : kOut; };
+    auto w_scale = [=](int r) { return w_ok(r) ? w_row(r) * (K / 16) : kOut; };
 
-    Acc<MT, WC> acc;
-    gemm_tile<MT, WC>(lds, ra, rc, rs, ak, a_row, w_code, w_scale, acc, K);
+    Acc<MTW, WCW, NTW> acc;
+    gemm_tile<MTW, WCW, NTW, VPM>(lds, ra, rc, rs, ak, a_row, w_code, w_scale, acc, K);
 
     const bool wide = uniform_wide<GEGLU, F32>(a);
     if constexpr (GEGLU) {
         using OutT = std::conditional_t<F32, float, uint16_t>;
-        store_tile_geglu<MT, OutT>(acc, static_cast<OutT *>(a.C) + (size_t)m0 * a.ldc, a.ldc,
-                                   M - m0, n0, N, a.tensor_scale[0], a.tensor_scale[1], wide);
+        store_tile_geglu<MTW, OutT, WCW, NTW>(acc, static_cast<OutT *>(a.C) + (size_t)m0 * a.ldc,
+                                              a.ldc, M - m0, n0, N, a.tensor_scale[0],
+                                              a.tensor_scale[1], wide);
     } else if constexpr (F32) {
-        store_tile_f32<MT, WC>(acc, static_cast<float *>(a.C), a.ldc, m0, n0, M, N,
-                               a.tensor_scale[0], wide);
+        store_tile_f32<MTW, WCW, NTW>(acc, static_cast<float *>(a.C), a.ldc, m0, n0, M, N,
+                                      a.tensor_scale[0], wide);
     } else {
-        store_tile_bf16<MT, WC>(acc, static_cast<uint16_t *>(a.C), a.ldc, m0, n0, M, N,
-                                a.tensor_scale[0], wide);
+        store_tile_bf16<MTW, WCW, NTW>(acc, static_cast<uint16_t *>(a.C), a.ldc, m0, n0, M, N,
+                                       a.tensor_scale[0], wide);
     }
 }
 
-template <bool GEGLU, bool F32> hipError_t launch_kernel(const GemmArgs &a, hipStream_t stream) {
+// A narrow tile's 2 NT MFMAs per step share NT fragments' decode: up to 8 VALU ops after
+// each (3 and 5 measured the same).
+constexpr int kNarrowVpm = 8;
+constexpr uint32_t kNarrowMaxBlocks = 2; // widest narrow tile (32-row W blocks)
+
+// Workgroups [0, G_full): the 256 x 256 tiles of n-tiles [0, nf), XCD-aware (workgroup g
+// on tile (g % 8) * per_xcd + g / 8, tiles M-fastest: the tiles resident on one XCD
+// share A row blocks and W column blocks in its L2).  Workgroups past G_full: the
+// narrow tiles (nt = 1 or 2 W blocks each; GeGLU 2: one gate and one up block) of the
+// columns past nf n-tiles, dealt the same way; they fill the CUs of the last round,
+// which whole tiles would leave partly empty.
+template <bool GEGLU, bool F32>
+__global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a, uint32_t nf, uint32_t nt) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr uint32_t TN = GEGLU ? kGegluCols : BN;
-    const uint32_t tiles = ((a.M + BM - 1) / BM) * ((a.N + TN - 1) / TN);
-    const uint32_t grid = 8 * ((tiles + 7) / 8);
+    const uint32_t tiles_m = (a.M + BM - 1) / BM;
+    const uint32_t full = tiles_m * nf;
+    const uint32_t g_full = 8 * ((full + 7) / 8);
+    if (blockIdx.x < g_full) {
+        const uint32_t per_xcd = g_full / 8;
+        const uint32_t t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+        if (t >= full)
+            return;
+        gemm_one_tile<GEGLU, F32, MT, WC, 8 / WC, 3>(a, lds, (t % tiles_m) * BM, (t / tiles_m) * TN);
+        return;
+    }
+    const uint32_t tc = GEGLU ? 16 * nt : 32 * nt; // output columns of a narrow tile
+    const uint32_t c_tail = nf * TN;
+    const uint32_t tiles = tiles_m * ((a.N - c_tail + tc - 1) / tc);
+    const uint32_t per_xcd = (tiles + 7) / 8;
+    const uint32_t u = blockIdx.x - g_full;
+    const uint32_t t = (u % 8) * per_xcd + u / 8;
+    if (t >= tiles)
+        return;
+    const uint32_t m0 = (t % tiles_m) * BM, n0 = c_tail + (t / tiles_m) * tc;
+    if (GEGLU || nt == 2)
+        gemm_one_tile<GEGLU, F32, 2, 1, 2, kNarrowVpm>(a, lds, m0, n0);
+    else
+        gemm_one_tile<false, F32, 2, 1, 1, kNarrowVpm>(a, lds, m0, n0);
+}
+
+// The last round of whole tiles: with tiles = R * ncu + rem (0 < rem, R >= 1), whole
+// tiles cover the first nf = R * ncu / tiles_m n-tiles and narrow tiles of nt W blocks
+// the remaining columns, nt the smallest width whose tiles fit in the CUs left after
+// the whole tiles' R rounds plus one more round -- if that width is at most 2 blocks
+// (GeGLU: 2).  The narrow tiles are decode-bound (each wave decodes every W element of
+// the tile for its 64 rows): measured at 2048 x 21504 x 5376, a round of 2-block tiles
+// took 0.73 of a whole-tile round (the GeGLU GEMM 835 -> 795 us), a round of 5-block
+// tiles 1.16 (404 -> 426 us), so wider narrow tiles are not used.  nt = 0: whole
+// tiles only.
+GemmTailPlan plan_tail(uint32_t M, uint32_t N, bool geglu, uint32_t ncu) {
+    const uint32_t tn = geglu ? kGegluCols : BN;
+    const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + tn - 1) / tn;
+    const uint64_t tiles = (uint64_t)tiles_m * tiles_n;
+    GemmTailPlan p{tiles_n, 0};
+    if (ncu == 0 || tiles <= ncu || tiles % ncu == 0)
+        return p;
+    const uint64_t R = tiles / ncu;
+    const uint32_t nf = (uint32_t)(R * ncu / tiles_m);
+    if (nf == 0 || nf >= tiles_n)
+        return p;
+    const uint64_t cols = N - (uint64_t)nf * tn;
+    const uint64_t slots = (R + 1) * ncu - (uint64_t)tiles_m * nf;
+    for (uint32_t nt = geglu ? 2 : 1; nt <= kNarrowMaxBlocks; ++nt) {
+        const uint64_t tc = geglu ? 16 * nt : 32 * nt;
+        if (tiles_m * ((cols + tc - 1) / tc) <= slots)
+            return GemmTailPlan{nf, nt};
+    }
+    return p;
+}
+
+template <bool GEGLU, bool F32> hipError_t launch_kernel(const GemmArgs &a, hipStream_t stream) {
+    const GemmTailPlan p = plan_tail(a.M, a.N, GEGLU, (uint32_t)num_cus());
+    const uint32_t tiles_m = (a.M + BM - 1) / BM;
+    uint32_t grid = 8 * ((tiles_m * p.nf + 7) / 8);
+    if (p.nt) {
+        const uint32_t tc = GEGLU ? 16 * p.nt : 32 * p.nt;
+        const uint32_t c_tail = p.nf * (GEGLU ? kGegluCols : BN);
+        grid += 8 * ((tiles_m * ((a.N - c_tail + tc - 1) / tc) + 7) / 8);
+    }
     constexpr size_t lds = Layout<MT, WC>::kLds;
     static std::atomic<uint64_t> attr_set{0};
     if (hipError_t e = allow_dynamic_lds(nvfp4_gemm_kernel<GEGLU, F32>, lds, attr_set); e != hipSuccess)
         return e;
-    hipLaunchKernelGGL((nvfp4_gemm_kernel<GEGLU, F32>), dim3(grid), dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL((nvfp4_gemm_kernel<GEGLU, F32>), dim3(grid), dim3(kThreads), lds, stream, a,
+                       p.nf, p.nt);
     return hipGetLastError();
 }
 
@@ -345,6 +420,10 @@ bool gemm_supported(uint32_t M, uint32_t N, uint32_t K, uint32_t a_k, bool out_f
     return K % BK == 0 && K > 0 && M > 0 && N > 0 && (a_k == K || a_k == 2 * K) &&
            (uint64_t)M * a_k * 2 < (1ull << 31) && (uint64_t)N * (K / 2) < (1ull << 31) &&
            (uint64_t)BM * N * esz < (1ull << 31);
+}
+
+GemmTailPlan gemm_tail_plan(uint32_t M, uint32_t N, bool geglu, uint32_t ncu) {
+    return plan_tail(M, N, geglu, ncu);
 }
 
 hipError_t gemm_launch(const GemmArgs &a, hipStream_t stream) {

@@ -129,7 +129,10 @@ template <int WC, int NT = 8 / WC> __device__ __forceinline__ int wave_col0() {
     return 32 * NT * ((threadIdx.x >> 6) % WC);
 }
 
-template <int MT, int WC, int NT = 8 / WC, typename ARow, typename WCode, typename WScale>
+// VPM: VALU slots after each MFMA in the interleaved schedule (the decode work per MFMA
+// grows as MT shrinks: 2 fragments of 16 ops per 2 MT MFMAs).
+template <int MT, int WC, int NT = 8 / WC, int VPM = 3, typename ARow, typename WCode,
+          typename WScale>
 __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t ra,
                                           const __amdgpu_buffer_rsrc_t (&rc)[2],
                                           const __amdgpu_buffer_rsrc_t (&rs)[2], uint32_t K,
@@ -259,15 +262,15 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
             for (int i = 0; i < MT; ++i)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(B[j], A[i], acc[i][j], 0, 0, 0);
     };
-    // One MFMA, then up to three VALU ops and one LDS read, for the MT*NT MFMAs of a
-    // step.  Three slots leave room for the dequantisation of the smaller tiles (MT 4
-    // and 2 dequantise 2x and 4x as much per MFMA): 1.4 % faster MoE prefill than two,
-    // the same dense GEMM; four was slower.
+    // One MFMA, then up to VPM VALU ops and one LDS read, for the MT*NT MFMAs of a
+    // step.  Three slots (the default) leave room for the dequantisation of the MoE's
+    // smaller tiles (MT 4 and 2 dequantise 2x and 4x as much per MFMA): 1.4 % faster MoE
+    // prefill than two, the same dense GEMM; four was slower.
     auto interleave = [&]() {
 #pragma unroll
         for (int m = 0; m < MT * NT; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0); // VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0); // VALU
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
         }
         // Close the region: the next step's MFMAs must not be pulled into this one's
@@ -326,15 +329,14 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
 // M (the hardware drops stores past it) and columns past N get an out-of-range offset.
 // `wide` (N and ldc multiples of 8, C 16-byte aligned): 16-byte stores of 8 columns;
 // otherwise one 2-byte store per element.
-template <int MT, int WC>
-__device__ __forceinline__ void store_tile_bf16(const Acc<MT, WC> &acc, uint16_t *C, uint32_t ldc,
+template <int MT, int WC, int NT = 8 / WC>
+__device__ __forceinline__ void store_tile_bf16(const Acc<MT, WC, NT> &acc, uint16_t *C, uint32_t ldc,
                                                 uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
                                                 float scale, bool wide) {
-    constexpr int NT = 8 / WC;
     const int lane = threadIdx.x & 63;
     const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)threadIdx.x >> 6);
-    const uint32_t cm = 32 * MT * (wave / WC) + (lane & 31);             // row within the tile
-    const uint32_t cn = 32 * (8 / WC) * (wave % WC) + 8 * (lane >> 5);   // column within the tile
+    const uint32_t cm = 32 * MT * (wave / WC) + (lane & 31);         // row within the tile
+    const uint32_t cn = 32 * NT * (wave % WC) + 8 * (lane >> 5);     // column within the tile
     const uint64_t rows = M - m0;
     const uint64_t bytes = rows * ldc * 2;
     const __amdgpu_buffer_rsrc_t rc =
@@ -356,7 +358,7 @@ __device__ __forceinline__ void store_tile_bf16(const Acc<MT, WC> &acc, uint16_t
             }
         return;
     }
-    const uint32_t cq = 32 * (8 / WC) * (wave % WC) + 4 * (lane >> 5);
+    const uint32_t cq = 32 * NT * (wave % WC) + 4 * (lane >> 5);
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -426,11 +428,10 @@ __device__ __forceinline__ void store_tile_bf16_lds(const Acc<MT, 4> &acc, uint8
 // fp32 output of a tile (times `scale`), placed as store_tile_bf16 places it: a lane's
 // runs of 4 consecutive columns go out as 16-byte stores when `wide` (N and ldc
 // multiples of 4, C 16-byte aligned), otherwise one 4-byte store per element.
-template <int MT, int WC>
-__device__ __forceinline__ void store_tile_f32(const Acc<MT, WC> &acc, float *C, uint32_t ldc,
+template <int MT, int WC, int NT = 8 / WC>
+__device__ __forceinline__ void store_tile_f32(const Acc<MT, WC, NT> &acc, float *C, uint32_t ldc,
                                                uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
                                                float scale, bool wide) {
-    constexpr int NT = 8 / WC;
     const int lane = threadIdx.x & 63;
     const int wave = (int)__builtin_amdgcn_readfirstlane((uint32_t)threadIdx.x >> 6);
     const uint32_t cm = 32 * MT * (wave / WC) + (lane & 31);
@@ -466,32 +467,36 @@ __device__ __forceinline__ void store_tile_f32(const Acc<MT, WC> &acc, float *C,
 
 // GeGLU epilogue of a tile whose W rows interleave two matrices by 32 (tile row r:
 // gate if (r / 32) % 2 == 0, else up; h column c0 + 32 (r / 64) + r % 32) and whose
-// waves hold two 32-row W blocks each -- the 1 x 4 tile (WC = 4) or the half-width 2 x 2
-// tile (WC = 2, W rows 0..127) -- so acc[i][0] and acc[i][1] of a wave hold gate and up
-// of the same h columns c0 + 32 (wave % WC) + 8 (e / 4) + 4 (lane / 32) + e % 4, token
-// row 32 MT (wave / WC) + 32 i + lane % 32:
+// waves hold NT (even) 32-row W blocks each -- the 1 x 4 tile (WC = 4, NT = 2), the
+// half-width 2 x 2 tile (WC = 2, NT = 2, W rows 0..127) or a narrow 4 x 1 tile (WC = 1,
+// W rows 0 .. 32 NT - 1) -- so acc[i][2p] and acc[i][2p+1] of a wave hold gate and up of
+// the same h columns c0 + 16 NT (wave % WC) + 32 p + 8 (e / 4) + 4 (lane / 32) + e % 4,
+// token row 32 MT (wave / WC) + 32 i + lane % 32:
 //   out[r][c] = gelu_tanh(gate_scale * gate) * (up_scale * up), r < nrows, c < ncols,
 // `out` at the tile's first token row, row stride ldc (shaders/geglu.metal:15-23).
 // OutT uint16_t (bf16 bits, round to nearest even) or float.  `wide`: 16-byte stores
 // (bf16: ncols and ldc multiples of 8; fp32: of 4; out 16-byte aligned), else one
 // store per element.
-template <int MT, typename OutT, int WC = 4>
-__device__ __forceinline__ void store_tile_geglu(const Acc<MT, WC, 2> &acc, OutT *out, uint32_t ldc,
+template <int MT, typename OutT, int WC = 4, int NT = 2>
+__device__ __forceinline__ void store_tile_geglu(const Acc<MT, WC, NT> &acc, OutT *out, uint32_t ldc,
                                                  uint32_t nrows, uint32_t c0, uint32_t ncols,
                                                  float gate_scale, float up_scale, bool wide) {
+    static_assert(NT % 2 == 0, "gate and up blocks in pairs");
     const int lane = threadIdx.x & 63;
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t wcol = c0 + 32 * (wave % WC);                  // the wave's first h column
-    const uint32_t row = 32 * MT * (wave / WC) + (lane & 31);     // and its first row
+    const uint32_t row = 32 * MT * (wave / WC) + (lane & 31);     // the wave's first row
     const uint64_t bytes = (uint64_t)nrows * ldc * sizeof(OutT);
     const __amdgpu_buffer_rsrc_t rh =
         make_rsrc(out, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);
 #pragma unroll
+    for (int pr = 0; pr < NT / 2; ++pr)
+#pragma unroll
     for (int i = 0; i < MT; ++i) {
+        const uint32_t wcol = c0 + 16 * NT * (wave % WC) + 32 * pr; // the pair's first h column
         f32x16_t v;
 #pragma unroll
         for (int q = 0; q < 16; ++q)
-            v[q] = gelu_tanh_fast(acc[i][0][q] * gate_scale) * (acc[i][1][q] * up_scale);
+            v[q] = gelu_tanh_fast(acc[i][2 * pr][q] * gate_scale) * (acc[i][2 * pr + 1][q] * up_scale);
         const uint32_t ro = (row + 32 * i) * ldc;
         if (wide && sizeof(OutT) == 2) {
             u32x4_t o[2];

@@ -1247,6 +1247,20 @@ int apex_hip_dense_dispatch_counts(uint64_t counts[4]) {
     });
 }
 
+int apex_hip_gemm_tail_plan(uint32_t m, uint32_t n, int geglu, uint32_t ncu, uint32_t out[2]) {
+    return guard([&] {
+        require(out != nullptr, "out is null");
+        require(m > 0 && n > 0, "empty product");
+        if (ncu == 0) {
+            init_device_tuning();
+            ncu = (uint32_t)apex_hip::num_cus();
+        }
+        const apex_hip::GemmTailPlan p = apex_hip::gemm_tail_plan(m, n, geglu != 0, ncu);
+        out[0] = p.nf;
+        out[1] = p.nt;
+    });
+}
+
 int apex_hip_set_gemv_waves_per_cu(int waves) {
     return guard([&] {
         require(waves >= 1 && waves <= 32, "waves per CU must be in [1, 32]");

@@ -100,6 +100,7 @@ _PROTOS = {
     "apex_hip_set_gemv_waves_per_cu": (_I, [_I]),
     "apex_hip_set_gemm_min_tokens": (_I, [_U32, _U32]),
     "apex_hip_dense_dispatch_counts": (_I, [_P]),
+    "apex_hip_gemm_tail_plan": (_I, [_U32, _U32, _I, _U32, _P]),
     "apex_moe_route_bf16": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
     "apex_moe_workspace_bytes": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
     "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
@@ -342,6 +343,14 @@ def dense_dispatch_counts() -> dict:
     c = (C.c_uint64 * 4)()
     check(lib().apex_hip_dense_dispatch_counts(C.cast(c, C.c_void_p)))
     return {"gemv": c[0], "gemm": c[1], "splitk_gemm": c[2], "f32_split": c[3]}
+
+
+def gemm_tail_plan(m: int, n: int, geglu: bool = False, ncu: int = 0) -> tuple:
+    """(whole n-tiles, narrow-tile W blocks) of the MFMA GEMM's cover of an m x n
+    output on ncu CUs (0: the current device's); narrow 0: whole tiles only."""
+    out = (C.c_uint32 * 2)()
+    check(lib().apex_hip_gemm_tail_plan(m, n, int(geglu), ncu, C.cast(out, C.c_void_p)))
+    return out[0], out[1]
 
 
 # ---- MoE expert FFN --------------------------------------------------------------

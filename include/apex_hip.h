@@ -312,6 +312,12 @@ int apex_hip_set_gemm_min_tokens(uint32_t bf16_tokens, uint32_t f32_tokens);
  * passes.  Lets a host see which form a call took; no device needed. */
 int apex_hip_dense_dispatch_counts(uint64_t counts[4]);
 
+/* How the MFMA GEMM covers an M x N output (N: output columns; GeGLU: h columns) on
+ * `ncu` CUs (0: the current device's): out[0] = n-tiles of whole tiles (256 x 256, GeGLU
+ * 256 x 128 h columns), out[1] = W blocks (32 rows) of the narrow tiles that cover the
+ * columns past them and fill the last round's CUs (0: whole tiles only).  No launch. */
+int apex_hip_gemm_tail_plan(uint32_t m, uint32_t n, int geglu, uint32_t ncu, uint32_t out[2]);
+
 /* ---- MoE expert FFN (no reference kernel) ------------------------------------------
  * Semantics: tools/dump_reference.py:208-219 (router top-k, experts combined with the
  * router weights) with each expert the dense GeGLU FFN of src/ops.h:57-69

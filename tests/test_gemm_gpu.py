@@ -97,6 +97,58 @@ def test_gemm_many_tiles_exact():
     assert rel_l2(bf16(C)[:, ni], want) < TOL_BF16
 
 
+# (M, N, narrow W blocks on 256 CUs): whole 256 x 256 tiles for R rounds, narrow tiles
+# (4 waves x 64 rows, nt 32-row W blocks) for the columns past them (N - 65536 columns
+# for M = 256); ragged M and N
+NARROW_PLAIN = [(256, 70536, 1), (256, 76800, 2), (300, 38440, 2), (520, 25677, 2)]
+
+
+@pytest.mark.parametrize("M,N,nt", NARROW_PLAIN)
+def test_gemm_narrow_tail_tiles_exact(M, N, nt):
+    """Columns past the whole tiles' rounds run as narrow tiles (widths 1 and 2, ragged
+    M and N): one-hot rows make every output one weight, bit-exact; then random rows
+    against the oracle on the narrow columns and a sample of the rest, and the fp32
+    matmul (hi + lo split A, 2K columns, fp32 out) the same way."""
+    assert hip.gemm_tail_plan(M, N, False, 256)[1] == nt
+    assert hip.gemm_tail_plan(M, N, False)[1] > 0  # this device takes narrow tiles too
+    rng = np.random.default_rng(N + nt)
+    K = 128
+    w = synth.nvfp4_weights(rng, N, K)
+    perm = rng.integers(0, K, size=M)
+    A = np.zeros((M, K), np.float32)
+    A[np.arange(M), perm] = 1.0
+    got = bf16(gemm(synth.bf16_from_f32(A), w))
+    want = oracle.decode(w.codes, w.scales)[:, perm].T + np.float32(0.0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    A = synth.normal_bf16(rng, (M, K))
+    C = bf16(gemm(A, w))
+    nf = hip.gemm_tail_plan(M, N, False)[0]
+    ni = np.concatenate([np.sort(rng.choice(nf * 256, 512, replace=False)), np.arange(nf * 256, N)])
+    want = oracle.matvec_rows(w.codes, w.scales, bf16(A), ni)
+    assert rel_l2(C[:, ni], want) < TOL_BF16
+    if nt == 2 or M != 256:
+        X = rng.standard_normal((M, K), dtype=np.float32)
+        got = run_matmul_f32(X, w)
+        assert rel_l2(got[:, ni], oracle.matvec_rows(w.codes, w.scales, X, ni)) < TOL_REF_GATE
+
+
+@pytest.mark.parametrize("T,N,nt", [(256, 38400, 2), (300, 20000, 2), (520, 13000, 2)])
+def test_geglu_narrow_tail_tiles(T, N, nt, gemm_threshold):
+    """GeGLU GEMMs (bf16 and fp32 out) whose last h columns run as narrow tiles of one
+    gate and one up block (32 h columns), ragged T and N, against the oracle."""
+    assert hip.gemm_tail_plan(T, N, True, 256)[1] == nt
+    rng = np.random.default_rng(T + N)
+    K = 64
+    g, u = synth.nvfp4_weights(rng, N, K), synth.nvfp4_weights(rng, N, K)
+    x = synth.normal_bf16(rng, (T, K))
+    xf = bf16(x)
+    want = oracle.geglu(oracle.matvec(g.codes, g.scales, xf), oracle.matvec(u.codes, u.scales, xf))
+    assert rel_l2(run_geglu(x, g, u, False), want) < TOL_BF16
+    assert rel_l2(run_geglu(xf, g, u, True, 0.5, 2.0),
+                  oracle.geglu(oracle.matvec(g.codes, g.scales, xf, 0.5),
+                               oracle.matvec(u.codes, u.scales, xf, 2.0))) < TOL_REF_GATE
+
+
 def test_gemm_tensor_scale_and_matmul_dispatch(gemm_threshold):
     """apex_nvfp4_matmul_bf16 switches to the GEMM (here from 64 tokens); results agree
     with the GEMM entry point, and a power-of-two tensor scale scales the output
