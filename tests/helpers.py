@@ -40,3 +40,54 @@ def all_codes_weights(rows_per_code: int = 1):
         codes[r, :] = word
     scales = np.tile(np.arange(256, dtype=np.uint8), (rows, 1))
     return synth.Nvfp4Weights(codes, scales)
+
+
+def count_outside(got, want, rel: float, abs_frac: float) -> int:
+    """Elements of `got` farther from `want` than rel * |want| + abs_frac * rms(want): a
+    wrong, missing or misplaced tile, row or column shows up however few elements it
+    touches, which a norm over the whole output can hide."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape and np.all(np.isfinite(got))
+    rms = np.sqrt(np.mean(want * want))
+    return int(np.count_nonzero(np.abs(got - want) > rel * np.abs(want) + abs_frac * rms))
+
+
+def dequant_f64(codes, scales) -> np.ndarray:
+    """The oracle's exact dequantisation (fp32, every value exact), as fp64 for a numpy
+    contraction."""
+    import oracle
+    return oracle.decode(codes, scales).astype(np.float64)
+
+
+def moe_ffn_full(slots, x, ids, weights, bf16_intermediates: bool = False, with_abs: bool = False):
+    """The MoE FFN of every token, grouped by expert: per expert the oracle's exact
+    dequantisation of gate, up and down, fp64 numpy products, the oracle's GeGLU on the
+    fp32-rounded projections; y[t] = sum_j w[t,j] * down(h[t, expert j]).  The same
+    composition as oracle.moe_ffn (pinned against it in the oracle tests), fast enough for
+    4096 tokens.  bf16_intermediates: h and each pair's down projection d rounded to
+    bf16 (nearest even), as the grouped-GEMM path stores them between its kernels.
+    with_abs: also return sum_j |w[t,j] * d[t,j]| per element (the scale of one bf16
+    rounding step of the terms)."""
+    import oracle
+    x = np.asarray(x, np.float64)
+    T, k = ids.shape
+    y = np.zeros((T, slots.H), np.float64)
+    yabs = np.zeros((T, slots.H), np.float64) if with_abs else None
+    for e in np.unique(ids):
+        t_idx, j_idx = np.nonzero(ids == e)
+        g = dequant_f64(slots.piece(e, "gate_w"), slots.piece(e, "gate_s"))
+        u = dequant_f64(slots.piece(e, "up_w"), slots.piece(e, "up_s"))
+        d = dequant_f64(slots.piece(e, "down_w"), slots.piece(e, "down_s"))
+        xe = x[t_idx]
+        h = oracle.geglu((xe @ g.T).astype(np.float32), (xe @ u.T).astype(np.float32))
+        if bf16_intermediates:
+            h = synth.bf16_to_f32(synth.bf16_from_f32(h))
+        de = h.astype(np.float64) @ d.T
+        if bf16_intermediates:
+            de = synth.bf16_to_f32(synth.bf16_from_f32(de.astype(np.float32))).astype(np.float64)
+        term = weights[t_idx, j_idx][:, None].astype(np.float64) * de
+        y[t_idx] += term
+        if with_abs:
+            yabs[t_idx] += np.abs(term)
+    return (y, yabs) if with_abs else y

@@ -5,7 +5,7 @@ import pytest
 
 import oracle
 from apex_amd import hip, synth
-from tests.helpers import TOL_BF16, TOL_REF_GATE, bf16, rel_l2
+from tests.helpers import TOL_BF16, TOL_REF_GATE, bf16, count_outside, dequant_f64, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -50,28 +50,44 @@ def test_gemm_random(M, N, K):
     assert rel_l2(got, want) < TOL_BF16
 
 
-def test_gemm_prefill_full_size_sampled():
-    """Prefill dense GEMM: A [2048,5376] x W [21504x5376], seed 0.  The oracle checks
-    48 sampled rows of A against 1024 sampled weight rows; every row of the output is
-    checked against its own fp32 sum-of-row invariant."""
+def test_gemm_prefill_full_size():
+    """Prefill dense GEMM: A [2048,5376] x W [21504x5376], seed 0 (256 x 256 tiles over
+    2.625 rounds of the CUs).  Every element against an fp64 contraction of the oracle's
+    exact dequantisation: within 2^-8 of its value (bf16 output rounding) plus 2e-3 of the
+    output rms (fp32 accumulation); and 48 sampled rows x 1024 sampled columns against the
+    oracle's own fp64 matvec."""
     A, w = synth.gemm_case(seed=0)
     M, K = A.shape
     C = bf16(gemm(A, w))
+    Af = bf16(A)
+    want = Af.astype(np.float64) @ dequant_f64(w.codes, w.scales).T
+    assert count_outside(C, want, 2.0 ** -8, 2e-3) == 0
+    assert rel_l2(C, want) < TOL_BF16
     rng = np.random.default_rng(1)
     mi = np.sort(rng.choice(M, 48, replace=False))
     ni = np.sort(rng.choice(w.rows, 1024, replace=False))
-    want = oracle.matvec_rows(w.codes, w.scales, bf16(A[mi]), ni)
-    assert rel_l2(C[np.ix_(mi, ni)], want) < TOL_BF16
-    # all rows/cols at once: C . 1 = A . (W^T 1); W^T 1 is the column sum of the
-    # dequantised weights, exact in fp64
-    wsum = np.zeros(K, np.float64)
-    for r0 in range(0, w.rows, 2048):
-        wsum += synth.Nvfp4Weights(w.codes[r0:r0 + 2048], w.scales[r0:r0 + 2048]).dequant().sum(0, dtype=np.float64)
-    lhs = C.astype(np.float64).sum(1)
-    rhs = bf16(A).astype(np.float64) @ wsum
-    # each output carries its bf16 rounding (~2^-9 / sqrt(3) relative, random sign), so
-    # the row sums agree to ~1e-3; a wrong index or dropped term would be O(1)
-    assert rel_l2(lhs, rhs) < TOL_BF16
+    assert rel_l2(C[np.ix_(mi, ni)], oracle.matvec_rows(w.codes, w.scales, Af[mi], ni)) < TOL_BF16
+
+
+def test_geglu_prefill_full_size():
+    """Prefill fused GeGLU through the MFMA GEMM: x [2048,5376], gate and up [21504x5376]
+    (1344 tiles of 256 tokens x 128 h columns: five whole rounds, the last 1024 h columns
+    as narrow tiles).  Every element against gelu_tanh(gate) * up from fp64 contractions
+    of the oracle's dequantisation, the oracle's GeGLU."""
+    x, g, u = synth.geglu_case(seed=3, tokens=2048)
+    xf = bf16(x).astype(np.float64)
+    out = hip.DeviceArray((2048, g.rows), np.uint16)
+    hip.nvfp4_geglu_bf16(dev(x), dev(g.codes), dev(g.scales), dev(u.codes), dev(u.scales), out, 2048,
+                         g.rows, x.shape[1])
+    hip.synchronize()
+    got = bf16(out.numpy())
+    gate = (xf @ dequant_f64(g.codes, g.scales).T).astype(np.float32)
+    up = (xf @ dequant_f64(u.codes, u.scales).T).astype(np.float32)
+    want = oracle.geglu(gate, up)
+    assert count_outside(got, want, 2.0 ** -7, 2e-3) == 0
+    assert rel_l2(got, want) < TOL_BF16
+    nf, nt = hip.gemm_tail_plan(2048, g.rows, True)
+    assert nt == 0 or rel_l2(got[:, nf * 128:], want[:, nf * 128:]) < TOL_BF16
 
 
 def test_gemm_many_tiles_exact():
