@@ -1095,6 +1095,7 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     __shared__ int s_exp[kMoeGemvMaxPairs];
     __shared__ uint32_t s_grp[TG > 1 ? kMoeGemvMaxPairs : 1];
     __shared__ uint32_t s_xrow[kMoeGemvMaxPairs];
+    __shared__ uint32_t s_next; // TG > 1: the workgroup's next unclaimed item index
     extern __shared__ uint4 xl[];                 // XLDS: [T][4 pieces][nchunks + 1]
     const int lane = threadIdx.x & 63;
     const int sub = lane / G, gl = lane % G;
@@ -1146,6 +1147,8 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     }
     if constexpr (XLDS && !ROUTE)
         stage_rows(xl, rx, a.T, nchunks, x_row);
+    if (threadIdx.x == 0)
+        s_next = blockDim.x / 64;
     __syncthreads();
     const uint32_t wave = uniform(threadIdx.x >> 6);
     const uint32_t waves_per_block = blockDim.x / 64;
@@ -1252,14 +1255,32 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     };
 
     // TG == 1: consecutive items (which share weight rows) on the waves of one
-    // workgroup.  TG > 1: consecutive items on consecutive workgroups, so every CU (and
-    // every SIMD) gets an even share of each cost class.
-    const uint32_t first = TG == 1 ? blockIdx.x * waves_per_block + wave
-                                   : wave * gridDim.x + blockIdx.x;
-    for (uint32_t it = first; it < items; it += nw) {
-        RowRegs<SLOTS> w[NR];
-        issue(w, it);
-        compute(w, it);
+    // workgroup.  TG > 1: consecutive items on consecutive workgroups, so every CU gets
+    // an even share of each cost class -- workgroup b takes items b + gridDim.x j,
+    // j = 0, 1, ..., its waves claiming the next j from an LDS counter as they finish
+    // (each wave starts at j = its index): with static dealing (wave w on j = w mod 16)
+    // a workgroup's waves finished up to 11 us apart (items differ in group size, and
+    // 7-8 items per wave leave a whole item of imbalance), the kernel waiting for the
+    // last; claimed, a workgroup's waves end within about an item.
+    if constexpr (TG == 1) {
+        for (uint32_t it = blockIdx.x * waves_per_block + wave; it < items; it += nw) {
+            RowRegs<SLOTS> w[NR];
+            issue(w, it);
+            compute(w, it);
+        }
+    } else {
+        for (uint32_t j = wave;;) {
+            const uint32_t it = blockIdx.x + gridDim.x * j;
+            if (it >= items)
+                break;
+            RowRegs<SLOTS> w[NR];
+            issue(w, it);
+            uint32_t next = 0;
+            if (lane == 0)
+                next = atomicAdd(&s_next, 1u);
+            j = uniform(next);
+            compute(w, it);
+        }
     }
 }
 
@@ -1278,9 +1299,10 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
 // class at most one group more than an even share, so at most ceil(P / S) + 10 rows,
 // which the host sizes `cap` and S for.
 //   Items (row block rb of R * NB rows, group i of the segment) are dealt class by class
-// (groups of 4, 3, 2, 1 positions), rb-major, round-robin over the segment's workgroups
-// first, so every CU and SIMD gets an even share of each cost class.  The first item's
-// weight loads are issued before the h rows are staged.
+// (groups of 4, 3, 2, 1 positions), rb-major, round-robin over the segment's workgroups,
+// so every CU gets an even share of each cost class; a workgroup's waves claim its
+// items in that order from an LDS counter.  The first item's weight loads are issued
+// before the h rows are staged.
 template <int G, int SLOTS, int NB>
 __global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_group_kernel(MoeArgs a, uint32_t S,
                                                                                      uint32_t cap) {
@@ -1290,6 +1312,7 @@ __global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_gro
     __shared__ uint32_t s_grp[kMoeGemvMaxPairs]; // its first staged row | size << 16
     __shared__ uint32_t s_pos[kMoeGemvMaxPairs]; // position of staged row j
     __shared__ uint32_t s_nrows;
+    __shared__ uint32_t s_next;                  // the workgroup's next unclaimed item index
     extern __shared__ uint4 xl[];                // [staged row][4 pieces][nchunks + 1]
     const int lane = threadIdx.x & 63;
     const int sub = lane / G, gl = lane % G;
@@ -1339,11 +1362,12 @@ __global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_gro
         if (lane == 0)
             s_nrows = base;
     }
+    if (threadIdx.x == 0)
+        s_next = blockDim.x / 64;
     __syncthreads();
 
     const uint32_t per_e = (H + R * NB - 1) / (R * NB);
     const uint32_t items = per_e * ngs;
-    const uint32_t nw = nwg * (blockDim.x / 64);
     const bool last_ok = gl + (SLOTS - 1) * G < nchunks;
     const uint32_t last_c = last_ok ? (SLOTS - 1) * G * 16 : kOutOfRange;
     const uint32_t last_s = last_ok ? (SLOTS - 1) * G * 2 : kOutOfRange;
@@ -1408,7 +1432,17 @@ __global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_gro
             }
     };
 
-    const uint32_t first = wave * nwg + wg;
+    // workgroup wg takes items wg + nwg j, j = 0, 1, ...: each wave starts at j = its
+    // index and claims the next j from an LDS counter (static dealing, wave w on
+    // j = w mod 16, left a workgroup's waves finishing up to 6 us apart)
+    auto item = [&](uint32_t j) { return wg + nwg * j; };
+    auto claim = [&]() {
+        uint32_t next = 0;
+        if (lane == 0)
+            next = atomicAdd(&s_next, 1u);
+        return item(uniform(next));
+    };
+    const uint32_t first = item(wave);
     RowRegs<SLOTS> wa[NB], wb[NB];
     if (first < items)
         issue(wa, first);
@@ -1418,15 +1452,17 @@ __global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_gro
     __syncthreads();
     // two register sets: the next item's weight loads are in flight during this item's
     // decode and dots
-    for (uint32_t it = first; it < items; it += 2 * nw) {
-        if (it + nw < items)
-            issue(wb, it + nw);
+    for (uint32_t it = first; it < items;) {
+        const uint32_t it2 = claim();
+        if (it2 < items)
+            issue(wb, it2);
         compute(wa, it);
-        if (it + nw >= items)
+        if (it2 >= items)
             break;
-        if (it + 2 * nw < items)
-            issue(wa, it + 2 * nw);
-        compute(wb, it + nw);
+        it = claim();
+        if (it < items)
+            issue(wa, it);
+        compute(wb, it2);
     }
 }
 
