@@ -134,14 +134,17 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // route_token_by for bf16 logits, whose key fits 32 bits: the order-preserving image
 // of the 16 logit bits above 0xFFFF - e (larger logit first, then lower expert id,
 // as route_token_by orders), so each of the k rounds is one 32-bit wave maximum.
-__device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, uint32_t k,
-                                            int lane, int32_t &my_id, float &my_w) {
+// bits(e, q) returns expert e's logit bits (e = lane + 64 q).
+template <typename Bits>
+__device__ __forceinline__ void route_token_bits(Bits bits, uint32_t E, uint32_t k, int lane,
+                                                 int32_t &my_id, float &my_w) {
     uint32_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t e = lane + 64 * q;
         if (e < E) {
-            const uint32_t u = logits[e] == 0x8000u ? 0u : logits[e]; // -0 ties +0
+            const uint32_t b = bits(e, q);
+            const uint32_t u = b == 0x8000u ? 0u : b; // -0 ties +0
             const uint32_t ord = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
             key[q] = (ord << 16) | (0xFFFFu - e);
         } else {
@@ -173,7 +176,13 @@ __device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, 
     my_w = p / group_sum<64>(p);
 }
 
-// Top-k of one token's E logits (E <= 256; logit(e) returns expert e's as fp32) by wave
+__device__ __forceinline__ void route_token(const uint16_t *logits, uint32_t E, uint32_t k,
+                                            int lane, int32_t &my_id, float &my_w) {
+    route_token_bits([&](uint32_t e, int) { return (uint32_t)logits[e]; }, E, k, lane, my_id, my_w);
+}
+
+// Top-k of one token's E logits (E <= 256; logit(e, q) returns expert e = lane + 64 q's
+// as fp32) by wave
 // lanes 0..63, then softmax over the k; lane j < k returns slot j's expert id and
 // weight.  Keys order by logit, then by lower expert id (the reference tie-break), and
 // are unique per expert.
@@ -185,7 +194,7 @@ __device__ __forceinline__ void route_token_by(Logit logit, uint32_t E, uint32_t
     for (int q = 0; q < 4; ++q) {
         const uint32_t e = lane + 64 * q;
         if (e < E) {
-            const uint32_t f = __float_as_uint(logit(e));
+            const uint32_t f = __float_as_uint(logit(e, q));
             const uint32_t u = f == 0x80000000u ? 0u : f; // -0 ties +0
             const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
             key[q] = ((uint64_t)ord << 32) | (0xFFFFFFFFu - e);
@@ -223,10 +232,38 @@ __device__ __forceinline__ void route_token_args(const MoeArgs &a, uint32_t t, i
                                                  int32_t &id, float &wt) {
     if (a.logits_f32) {
         const float *l = a.logits_f32 + (size_t)t * a.E;
-        route_token_by([&](uint32_t e) { return l[e]; }, a.E, a.k, lane, id, wt);
+        route_token_by([&](uint32_t e, int) { return l[e]; }, a.E, a.k, lane, id, wt);
     } else {
         route_token(a.logits + (size_t)t * a.E, a.E, a.k, lane, id, wt);
     }
+    if (a.pes && (uint32_t)lane < a.k)
+        wt *= bf16_bits_to_f32(a.pes[id]);
+}
+
+// Token t's logits for lane `lane` (experts lane + 64 q; fp32 or bf16 bits), loaded
+// ahead of the routing so their latency overlaps other work.
+struct TokenLogits {
+    uint32_t v[4];
+};
+__device__ __forceinline__ TokenLogits load_token_logits(const MoeArgs &a, uint32_t t, int lane) {
+    TokenLogits r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t e = lane + 64 * q;
+        r.v[q] = e >= a.E ? 0u
+                 : a.logits_f32 ? __float_as_uint(a.logits_f32[(size_t)t * a.E + e])
+                                : (uint32_t)a.logits[(size_t)t * a.E + e];
+    }
+    return r;
+}
+
+// route_token_args on logits already loaded.
+__device__ __forceinline__ void route_token_loaded(const MoeArgs &a, const TokenLogits &r, int lane,
+                                                   int32_t &id, float &wt) {
+    if (a.logits_f32)
+        route_token_by([&](uint32_t, int q) { return __uint_as_float(r.v[q]); }, a.E, a.k, lane, id, wt);
+    else
+        route_token_bits([&](uint32_t, int q) { return r.v[q]; }, a.E, a.k, lane, id, wt);
     if (a.pes && (uint32_t)lane < a.k)
         wt *= bf16_bits_to_f32(a.pes[id]);
 }
@@ -242,7 +279,7 @@ __global__ __launch_bounds__(256) void moe_route_f32_kernel(const float *logits,
     int32_t id;
     float wt;
     const float *l = logits + (size_t)t * E;
-    route_token_by([&](uint32_t e) { return l[e]; }, E, k, lane, id, wt);
+    route_token_by([&](uint32_t e, int) { return l[e]; }, E, k, lane, id, wt);
     if ((uint32_t)lane < k) {
         ids[(size_t)t * k + lane] = id;
         w[(size_t)t * k + lane] = pes ? wt * bf16_bits_to_f32(pes[id]) : wt;
@@ -820,14 +857,17 @@ struct RoutePlanLds {
 __device__ void route_plan_block(const MoeArgs &a, int32_t *plan, RoutePlanLds &s, bool write_routes) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const uint32_t k = a.k, P = a.T * k;
+    const uint32_t k = a.k, P = a.T * k, nwaves = blockDim.x / 64;
+    // the wave's first two tokens' logits load while the masks are cleared
+    TokenLogits pre[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (wave + i * nwaves < a.T)
+            pre[i] = load_token_logits(a, wave + i * nwaves, lane);
     for (uint32_t e = threadIdx.x; e < kMoeMaxExperts; e += blockDim.x)
         s.mask[e] = 0;
     __syncthreads();
-    for (uint32_t t = wave; t < a.T; t += blockDim.x / 64) {
-        int32_t id;
-        float wt;
-        route_token_args(a, t, lane, id, wt);
+    auto record = [&](uint32_t t, int32_t id, float wt) {
         if ((uint32_t)lane < k) {
             if (write_routes) {
                 a.ids[t * k + lane] = id;
@@ -836,6 +876,22 @@ __device__ void route_plan_block(const MoeArgs &a, int32_t *plan, RoutePlanLds &
             s.ids[t * k + lane] = id;
             atomicOr(&s.mask[id], 1u << t);
         }
+    };
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t t = wave + i * nwaves;
+        if (t < a.T) {
+            int32_t id;
+            float wt;
+            route_token_loaded(a, pre[i], lane, id, wt);
+            record(t, id, wt);
+        }
+    }
+    for (uint32_t t = wave + 2 * nwaves; t < a.T; t += nwaves) {
+        int32_t id;
+        float wt;
+        route_token_args(a, t, lane, id, wt);
+        record(t, id, wt);
     }
     __syncthreads();
     if (wave == 0)
@@ -1042,20 +1098,30 @@ struct StageRegs {
 template <typename RowOff>
 __device__ __forceinline__ void stage_issue(StageRegs &st, __amdgpu_buffer_rsrc_t rs, uint32_t n_rows,
                                             int nchunks, uint32_t base, RowOff row_off) {
-    const uint32_t nc = (uint32_t)nchunks + 1, n = n_rows * 4 * nc;
+    const uint32_t nc = (uint32_t)nchunks + 1, per_row = 4 * nc, n = n_rows * per_row;
+    // (row, piece) of element i = base + tid + k * blockDim.x, stepped without a
+    // division per element (the per-element divisions cost ~1 us of issue per call)
+    const uint32_t i0 = base + threadIdx.x;
+    uint32_t r = i0 / per_row, rem = i0 - r * per_row;
+    const uint32_t step_r = blockDim.x / per_row, step_rem = blockDim.x - step_r * per_row;
 #pragma unroll
     for (int k = 0; k < kStagePerThread; ++k) {
-        const uint32_t i = base + threadIdx.x + k * blockDim.x;
+        const uint32_t i = i0 + k * blockDim.x;
         uint32_t off = kOutOfRange;
         st.dst[k] = 0xFFFFFFFFu;
         if (i < n) {
-            const uint32_t r = i / (4 * nc), rem = i % (4 * nc);
             const uint32_t c = rem / 4, q = rem % 4;
             if ((int)c < nchunks)
                 off = row_off(r) + c * 64 + q * 16;
             st.dst[k] = (r * 4 + q) * nc + c;
         }
         st.v[k] = load_b128(rs, off);
+        rem += step_rem;
+        r += step_r;
+        if (rem >= per_row) {
+            rem -= per_row;
+            ++r;
+        }
     }
 }
 
