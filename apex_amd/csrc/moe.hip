@@ -854,7 +854,11 @@ struct RoutePlanLds {
     int32_t ids[kMoeGemvMaxPairs];
 };
 
-__device__ void route_plan_block(const MoeArgs &a, int32_t *plan, RoutePlanLds &s, bool write_routes) {
+// `meanwhile` runs in every thread between the routing and the plan's barrier -- in
+// waves 1.. while wave 0 builds the plan -- for independent setup work.
+template <typename Meanwhile>
+__device__ void route_plan_block(const MoeArgs &a, int32_t *plan, RoutePlanLds &s, bool write_routes,
+                                 Meanwhile meanwhile) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const uint32_t k = a.k, P = a.T * k, nwaves = blockDim.x / 64;
@@ -896,6 +900,7 @@ __device__ void route_plan_block(const MoeArgs &a, int32_t *plan, RoutePlanLds &
     __syncthreads();
     if (wave == 0)
         plan_from_masks(a, plan, s.mask, s.off, lane);
+    meanwhile();
     __syncthreads();
     const PlanView v = plan_view(plan, a.E, P);
     for (uint32_t p = threadIdx.x; p < P; p += blockDim.x) {
@@ -910,7 +915,7 @@ __device__ void route_plan_block(const MoeArgs &a, int32_t *plan, RoutePlanLds &
 
 __global__ __launch_bounds__(1024) void moe_route_plan_kernel(MoeArgs a) {
     __shared__ RoutePlanLds s;
-    route_plan_block(a, a.plan, s, true);
+    route_plan_block(a, a.plan, s, true, [] {});
 }
 
 // ---------------------------------------------------------------------------------
@@ -1181,8 +1186,7 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
         // x's loads fly while the tokens are routed (the host keeps x within one round)
         StageRegs st;
         stage_issue(st, rx, a.T, nchunks, 0, x_row);
-        route_plan_block(a, s_plan, s_rp, blockIdx.x == 0);
-        stage_commit(st, xl);
+        route_plan_block(a, s_plan, s_rp, blockIdx.x == 0, [&] { stage_commit(st, xl); });
         if (blockIdx.x == 0) {
             const uint32_t words = kMoePlanHeader + 3 * a.E + 1 + 4 * P;
             for (uint32_t i = threadIdx.x; i < words; i += blockDim.x)
@@ -1192,12 +1196,6 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
         ids = s_rp.ids;
     }
     const PlanView v = plan_view(plan, a.E, P);
-    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
-        const uint32_t pair = (uint32_t)v.pair_of_pos[i];
-        if constexpr (TG == 1)
-            s_exp[i] = ids[pair];
-        s_xrow[i] = pair / a.k;
-    }
     uint32_t ncls[kTokenGroup] = {}; // TG > 1: groups of size 4, 3, 2, 1
     uint32_t ng = 0;
     if constexpr (TG > 1) {
@@ -1206,16 +1204,7 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
             ncls[q] = uniform(v.hdr[3 + q]);
             ng += ncls[q];
         }
-        for (uint32_t i = threadIdx.x; i < ng; i += blockDim.x) {
-            s_exp[i] = v.groups[2 * i];
-            s_grp[i] = (uint32_t)v.groups[2 * i + 1];
-        }
     }
-    if constexpr (XLDS && !ROUTE)
-        stage_rows(xl, rx, a.T, nchunks, x_row);
-    if (threadIdx.x == 0)
-        s_next = blockDim.x / 64;
-    __syncthreads();
     const uint32_t wave = uniform(threadIdx.x >> 6);
     const uint32_t waves_per_block = blockDim.x / 64;
     const uint32_t per_e = (rows + R * NB - 1) / (R * NB);
@@ -1227,6 +1216,12 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
     const uint64_t off_s[2] = {a.slots.gate_s, a.slots.up_s};
     const uint32_t wbytes = rows * K / 2, sbytes = rows * K / 16;
     const uint32_t nw = gridDim.x * waves_per_block;
+    // TG > 1: group g's expert and (first position | size << 16) -- straight from the
+    // plan when it is in LDS (ROUTE), else from the LDS copies made below
+    auto group_expert = [&](uint32_t g) { return ROUTE ? v.groups[2 * g] : s_exp[g]; };
+    auto group_info = [&](uint32_t g) {
+        return ROUTE ? (uint32_t)v.groups[2 * g + 1] : s_grp[g];
+    };
 
     // item it -> (row block, position or group)
     auto locate = [&](uint32_t it, uint32_t &rb, uint32_t &j) {
@@ -1255,7 +1250,8 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
         uint32_t rb, j;
         locate(it, rb, j);
         const uint32_t r0 = rb * R * NB;
-        const uint8_t *slot = a.slots.base + (size_t)uniform(s_exp[j]) * a.slots.stride;
+        const int e = TG > 1 ? group_expert(j) : s_exp[j];
+        const uint8_t *slot = a.slots.base + (size_t)uniform(e) * a.slots.stride;
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -1304,7 +1300,7 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
             if (gl == 0)
                 store(dots, r0, j);
         } else {
-            const uint32_t gp = uniform(s_grp[j]);
+            const uint32_t gp = uniform(group_info(j));
             const int p0 = (int)(gp & 0xFFFFu), n = (int)(gp >> 16);
             float dots[TG][NR];
             rows_dot_group<G, SLOTS, NR, TG>(dots, w, n, [&](int t, int s) {
@@ -1319,6 +1315,39 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
                 }
         }
     };
+
+    // TG > 1 with the plan in LDS: the wave's first item's weight loads go out now,
+    // while the rest of the setup runs
+    RowRegs<SLOTS> w_first[NR];
+    constexpr bool kEarly = ROUTE && TG > 1;
+    if constexpr (kEarly)
+        issue(w_first, blockIdx.x + gridDim.x * wave);
+    for (uint32_t i = threadIdx.x; i < P; i += blockDim.x) {
+        const uint32_t pair = (uint32_t)v.pair_of_pos[i];
+        if constexpr (TG == 1)
+            s_exp[i] = ids[pair];
+        s_xrow[i] = pair / a.k;
+    }
+    if constexpr (TG > 1 && !ROUTE) {
+        for (uint32_t i = threadIdx.x; i < ng; i += blockDim.x) {
+            s_exp[i] = v.groups[2 * i];
+            s_grp[i] = (uint32_t)v.groups[2 * i + 1];
+        }
+    }
+    if constexpr (XLDS && !ROUTE)
+        stage_rows(xl, rx, a.T, nchunks, x_row);
+    if (threadIdx.x == 0)
+        s_next = blockDim.x / 64;
+    if constexpr (kEarly) {
+        // the LDS writes above must be visible to every wave, but the first item's
+        // weight loads need not land before the barrier (__syncthreads would wait for
+        // them): wait for LDS only, then the bare barrier
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    } else {
+        __syncthreads();
+    }
 
     // TG == 1: consecutive items (which share weight rows) on the waves of one
     // workgroup.  TG > 1: consecutive items on consecutive workgroups, so every CU gets
@@ -1335,17 +1364,18 @@ __global__ __launch_bounds__(XLDS ? kXLdsThreads : 256, XLDS ? kXLdsThreads / 25
             compute(w, it);
         }
     } else {
-        for (uint32_t j = wave;;) {
+        bool issued = kEarly;
+        for (uint32_t j = wave;; issued = false) {
             const uint32_t it = blockIdx.x + gridDim.x * j;
             if (it >= items)
                 break;
-            RowRegs<SLOTS> w[NR];
-            issue(w, it);
+            if (!issued)
+                issue(w_first, it);
             uint32_t next = 0;
             if (lane == 0)
                 next = atomicAdd(&s_next, 1u);
             j = uniform(next);
-            compute(w, it);
+            compute(w_first, it);
         }
     }
 }
