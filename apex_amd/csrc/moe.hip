@@ -1130,11 +1130,16 @@ __device__ __forceinline__ void stage_issue(StageRegs &st, __amdgpu_buffer_rsrc_
     }
 }
 
+// Branch-free (a slot with nothing to stage writes a dummy LDS word instead), so the
+// compiler's load waits count exactly: a later load (the first item's weights) is not
+// waited for.
 __device__ __forceinline__ void stage_commit(const StageRegs &st, uint4 *xl) {
+    __shared__ uint4 s_discard;
 #pragma unroll
-    for (int k = 0; k < kStagePerThread; ++k)
-        if (st.dst[k] != 0xFFFFFFFFu)
-            xl[st.dst[k]] = __builtin_bit_cast(uint4, st.v[k]);
+    for (int k = 0; k < kStagePerThread; ++k) {
+        uint4 *dst = st.dst[k] != 0xFFFFFFFFu ? xl + st.dst[k] : &s_discard;
+        *dst = __builtin_bit_cast(uint4, st.v[k]);
+    }
 }
 
 template <typename RowOff>
@@ -1482,16 +1487,20 @@ __global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_gro
             g0 += nq;
         }
     };
+    // Loads of item it's weight rows; an item past the end loads row H of expert
+    // s_exp[0] -- past the descriptors' end, so nothing is read (zeros) -- so a caller
+    // need not branch around it.
     auto issue = [&](RowRegs<SLOTS> (&w)[NB], uint32_t it) {
-        uint32_t rb, i;
-        locate(it, rb, i);
+        const bool ok = it < items;
+        uint32_t rb = 0, i = 0;
+        locate(ok ? it : 0u, rb, i);
         const uint8_t *slot = a.slots.base + (size_t)uniform(s_exp[i]) * a.slots.stride;
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(slot + a.slots.down_w, wbytes);
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(slot + a.slots.down_s, sbytes);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const uint32_t row = rb * R * NB + b * R + sub;
-            load_row<SLOTS, G>(w[b], rc, rs, row < H ? row : H, gl, I, last_c, last_s);
+            load_row<SLOTS, G>(w[b], rc, rs, ok && row < H ? row : H, gl, I, last_c, last_s);
         }
     };
     // x chunk of slot s of staged row j (j < cap by the segment bound; the clamp only
@@ -1540,12 +1549,31 @@ __global__ __launch_bounds__(kXLdsThreads, kXLdsThreads / 256) void moe_down_gro
     };
     const uint32_t first = item(wave);
     RowRegs<SLOTS> wa[NB], wb[NB];
-    if (first < items)
-        issue(wa, first);
-    // the segment's h rows: staged row j = h[s_pos[j]]
-    stage_rows(xl, make_rsrc(a.h, P * I * 2), min(s_nrows, cap), nchunks,
-               [&](uint32_t j) { return s_pos[j] * I * 2; });
-    __syncthreads();
+    // the segment's h rows (staged row j = h[s_pos[j]]): the first batch's loads go out,
+    // then the first item's weight loads, so writing the batch to LDS waits only for
+    // the h loads (a wave's loads complete in order)
+    {
+        const __amdgpu_buffer_rsrc_t rh = make_rsrc(a.h, P * I * 2);
+        const uint32_t nrows = min(s_nrows, cap);
+        auto h_row = [&](uint32_t j) { return s_pos[j] * I * 2; };
+        StageRegs st;
+        stage_issue(st, rh, nrows, nchunks, 0, h_row);
+        asm volatile("" ::: "memory"); // keep the load order: h first
+        issue(wa, first);              // unconditional: the waits above stay exact
+        asm volatile("" ::: "memory");
+        stage_commit(st, xl);
+        const uint32_t n = nrows * 4 * ((uint32_t)nchunks + 1);
+        for (uint32_t base = kStagePerThread * blockDim.x; base < n; base += kStagePerThread * blockDim.x) {
+            stage_issue(st, rh, nrows, nchunks, base, h_row);
+            stage_commit(st, xl);
+        }
+    }
+    // the staged rows must be visible to every wave, but the first item's weight loads
+    // need not land before the barrier (__syncthreads would wait for them): wait for
+    // LDS only, then the bare barrier
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     // two register sets: the next item's weight loads are in flight during this item's
     // decode and dots
     for (uint32_t it = first; it < items;) {
