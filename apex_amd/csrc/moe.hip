@@ -545,82 +545,112 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *logits, 
     }
 }
 
-// Plan from per-expert pair counts `cnt` (LDS, kMoeMaxExperts entries, zero from E
-// on; one workgroup of >= kMoeMaxExperts threads): header, counts, offsets, the active
-// expert list and, with `tiles`, the m-tile list of the grouped GEMMs -- entries
-// (expert, first pos, rows, class) with class 0/1/2 = 256/128/64-row tiles: per
-// expert, full 256-row tiles and a tail tile of the smallest class that holds the
-// remainder, all class-0 tiles first.  Counts, offsets and tile slots come from
-// exclusive scans over the experts, so every expert's entries are written in
-// parallel.  `first` receives each expert's first position.
-constexpr int kPlanScans = 5; // pair counts, active flags, class 0/1/2 tile counts
+// Exclusive prefix sum over the 64 lanes of a wave; `total` receives the sum of all
+// lanes.  Inclusive scans within rows of 16 by DPP row shifts (lanes shifted in from
+// outside the row read 0), then each row adds the totals of the rows below it.
+__device__ __forceinline__ int wave_excl_scan(int x, int lane, int &total) {
+    int incl = x;
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true); // row_shr:1
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true); // row_shr:2
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true); // row_shr:4
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true); // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(incl, 15), r1 = __builtin_amdgcn_readlane(incl, 31),
+              r2 = __builtin_amdgcn_readlane(incl, 47), r3 = __builtin_amdgcn_readlane(incl, 63);
+    const int row = lane >> 4;
+    incl += (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+    total = r0 + r1 + r2 + r3;
+    return incl - x;
+}
+
+// Plan from per-expert pair counts `cnt` (kMoeMaxExperts entries, zero from E on; one
+// workgroup of >= kMoeMaxExperts threads): header, counts, offsets, the active expert
+// list and the m-tile list of the grouped GEMMs -- entries (expert, first pos, rows,
+// blocks): per expert, full tiles of 256 rows (8 blocks of 32) and a tail tile of as
+// many 32-row blocks as its remainder needs, ordered by blocks (8 first, then 7, ...,
+// 1) so the grid deals the longest tiles first.  The tail's 32-row granularity keeps
+// padding low (at the 4096-token Zipf routing 34,688 MFMA rows for 32,768 pairs,
+// against 38,080 with 256/128/64-row tails).  Counts, offsets and tile slots come from
+// exclusive scans over the experts (a wave scan per 64 experts, then the waves'
+// totals), so every expert's entries are written in parallel.  `first` receives each
+// expert's first position.
+constexpr int kTileClasses = 8; // tiles of 8, 7, ..., 1 blocks of 32 rows
+constexpr int kPlanScans = 2 + kTileClasses; // pair counts, active flags, tiles per class
 
 __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first) {
-    __shared__ int scan[kPlanScans][kMoeMaxExperts];
+    __shared__ int wsum[kPlanScans][kMoeMaxExperts / 64];
     const uint32_t E = a.E, P = a.T * a.k;
     const PlanView v = plan_view(a.plan, E, P);
-    const int tid = threadIdx.x;
-    // inclusive Hillis-Steele scans over the 256 expert slots (experts >= E count 0)
-    int val[kPlanScans] = {};
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int kWaves = kMoeMaxExperts / 64;
+    // experts 0..255 on the first 4 waves (experts >= E count 0): per scan, an exclusive
+    // wave scan plus the totals of the waves below
+    const bool mine = tid < (int)kMoeMaxExperts;
     const int c = tid < (int)E ? cnt[tid] : 0;
-    const int rem = c % 256;
-    if (tid < (int)kMoeMaxExperts) {
-        val[0] = c;
-        val[1] = c > 0;
-        val[2] = c / 256 + (rem > 128);
-        val[3] = rem > 64 && rem <= 128;
-        val[4] = rem > 0 && rem <= 64;
+    const int full = c / 256, blocks = (c % 256 + 31) / 32; // tail tile: 0..8 blocks
+    int val[kPlanScans] = {}, excl[kPlanScans] = {};
+    val[0] = c;
+    val[1] = c > 0;
+    val[2] = full + (blocks == 8);         // class 0: tiles of 8 blocks
 #pragma unroll
-        for (int q = 0; q < kPlanScans; ++q)
-            scan[q][tid] = val[q];
+    for (int i = 1; i < kTileClasses; ++i) // class i: a tail of 8 - i blocks
+        val[2 + i] = blocks == kTileClasses - i;
+    if (mine) {
+#pragma unroll
+        for (int q = 0; q < kPlanScans; ++q) {
+            int tot;
+            excl[q] = wave_excl_scan(val[q], lane, tot);
+            if (lane == 0)
+                wsum[q][wave] = tot;
+        }
     }
     __syncthreads();
-    for (int d = 1; d < (int)kMoeMaxExperts; d <<= 1) {
-        int add[kPlanScans] = {};
-        if (tid < (int)kMoeMaxExperts && tid >= d)
+    int total[kPlanScans];
 #pragma unroll
-            for (int q = 0; q < kPlanScans; ++q)
-                add[q] = scan[q][tid - d];
-        __syncthreads();
-        if (tid < (int)kMoeMaxExperts)
+    for (int q = 0; q < kPlanScans; ++q) {
+        total[q] = 0;
 #pragma unroll
-            for (int q = 0; q < kPlanScans; ++q)
-                scan[q][tid] += add[q];
-        __syncthreads();
+        for (int w = 0; w < kWaves; ++w) {
+            if (w < wave)
+                excl[q] += wsum[q][w];
+            total[q] += wsum[q][w];
+        }
     }
-    const int last = kMoeMaxExperts - 1;
-    const int n0 = scan[2][last], n1 = scan[3][last], n2 = scan[4][last];
+    // first tile slot of each class: 8 blocks first, then 7, ..., 1
+    int base[kTileClasses];
+    base[0] = 0;
+#pragma unroll
+    for (int i = 1; i < kTileClasses; ++i)
+        base[i] = base[i - 1] + total[2 + i - 1];
     if (tid < (int)E) {
         const int e = tid;
-        const int off = scan[0][e] - val[0]; // exclusive
+        const int off = excl[0];
         first[e] = off;
         v.off[e] = off;
         v.cnt[e] = c;
         if (c > 0)
-            v.act[scan[1][e] - 1] = e;
-        int slot = -1, cls = 0;
-        const int full = c / 256;
-        int t0 = scan[2][e] - val[2];
+            v.act[excl[1]] = e;
+        const int t0 = excl[2];
         for (int f = 0; f < full; ++f) {
             int32_t *t = v.tiles + 4 * (t0 + f);
-            t[0] = e, t[1] = off + 256 * f, t[2] = 256, t[3] = 0;
+            t[0] = e, t[1] = off + 256 * f, t[2] = 256, t[3] = kTileClasses;
         }
-        if (rem > 128)
-            slot = t0 + full, cls = 0;
-        else if (rem > 64)
-            slot = n0 + scan[3][e] - 1, cls = 1;
-        else if (rem > 0)
-            slot = n0 + n1 + scan[4][e] - 1, cls = 2;
-        if (slot >= 0) {
+        if (blocks > 0) {
+            const int cls = kTileClasses - blocks;
+            const int slot = cls == 0 ? t0 + full : base[cls] + excl[2 + cls];
             int32_t *t = v.tiles + 4 * slot;
-            t[0] = e, t[1] = off + 256 * full, t[2] = rem, t[3] = cls;
+            t[0] = e, t[1] = off + 256 * full, t[2] = c % 256, t[3] = blocks;
         }
     }
     if (tid == 0) {
-        v.off[E] = scan[0][last];
-        v.hdr[0] = scan[1][last];
-        v.hdr[1] = n0 + n1 + n2;
-        v.hdr[2] = n0;
+        v.off[E] = total[0];
+        v.hdr[0] = total[1];
+        int nt = 0;
+#pragma unroll
+        for (int i = 0; i < kTileClasses; ++i)
+            nt += total[2 + i];
+        v.hdr[1] = nt;
+        // tiles of more than 4 blocks (classes 0..3): the down GEMM splits them in halves
+        v.hdr[2] = total[2] + total[3] + total[4] + total[5];
     }
     __syncthreads();
 }
@@ -758,23 +788,6 @@ __global__ __launch_bounds__(256) void moe_plan_scatter_kernel(MoeArgs a) {
     const int pos = v.off[e] + a.hist[(size_t)b * a.E + e] + a.rank[p];
     v.pos_of_pair[p] = pos;
     v.pair_of_pos[pos] = (int32_t)p;
-}
-
-// Exclusive prefix sum over the 64 lanes of a wave; `total` receives the sum of all
-// lanes.  Inclusive scans within rows of 16 by DPP row shifts (lanes shifted in from
-// outside the row read 0), then each row adds the totals of the rows below it.
-__device__ __forceinline__ int wave_excl_scan(int x, int lane, int &total) {
-    int incl = x;
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true); // row_shr:1
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true); // row_shr:2
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true); // row_shr:4
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true); // row_shr:8
-    const int r0 = __builtin_amdgcn_readlane(incl, 15), r1 = __builtin_amdgcn_readlane(incl, 31),
-              r2 = __builtin_amdgcn_readlane(incl, 47), r3 = __builtin_amdgcn_readlane(incl, 63);
-    const int row = lane >> 4;
-    incl += (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
-    total = r0 + r1 + r2 + r3;
-    return incl - x;
 }
 
 // Decode plan from the experts' token masks (bit t of mask[e]: token t chose expert e),
@@ -1653,21 +1666,29 @@ __global__ __launch_bounds__(kThreads) void moe_gateup_gemm_kernel(MoeArgs a) {
     if (mt >= uniform(v.hdr[1]))
         return;
     const int32_t *t = v.tiles + 4 * mt;
-    const int e = uniform(t[0]), cls = uniform(t[3]);
+    const int e = uniform(t[0]), blocks = uniform(t[3]); // 32-row blocks, 1..8
     const uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]), c0 = nt * kGateUpCols;
-    if (c0 + kGateUpCols / 2 >= a.I) { // 64 h columns left
-        if (cls == 0)
-            gateup_tile<8, true>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
-        else if (cls == 1)
-            gateup_tile<4, true>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
-        else
-            gateup_tile<2, true>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
-    } else if (cls == 0)
-        gateup_tile<8, false>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
-    else if (cls == 1)
-        gateup_tile<4, false>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
-    else
-        gateup_tile<2, false>(a, lds, v.pair_of_pos, e, row0, nrows, c0);
+    const int32_t *pp = v.pair_of_pos;
+    if (c0 + kGateUpCols / 2 >= a.I) { // 64 h columns left: the half-width tile, whose
+        // two wave rows split the token rows (an odd block count runs one block more)
+        switch ((blocks + 1) / 2) {
+        case 4: gateup_tile<8, true>(a, lds, pp, e, row0, nrows, c0); break;
+        case 3: gateup_tile<6, true>(a, lds, pp, e, row0, nrows, c0); break;
+        case 2: gateup_tile<4, true>(a, lds, pp, e, row0, nrows, c0); break;
+        default: gateup_tile<2, true>(a, lds, pp, e, row0, nrows, c0); break;
+        }
+        return;
+    }
+    switch (blocks) {
+    case 8: gateup_tile<8, false>(a, lds, pp, e, row0, nrows, c0); break;
+    case 7: gateup_tile<7, false>(a, lds, pp, e, row0, nrows, c0); break;
+    case 6: gateup_tile<6, false>(a, lds, pp, e, row0, nrows, c0); break;
+    case 5: gateup_tile<5, false>(a, lds, pp, e, row0, nrows, c0); break;
+    case 4: gateup_tile<4, false>(a, lds, pp, e, row0, nrows, c0); break;
+    case 3: gateup_tile<3, false>(a, lds, pp, e, row0, nrows, c0); break;
+    case 2: gateup_tile<2, false>(a, lds, pp, e, row0, nrows, c0); break;
+    default: gateup_tile<1, false>(a, lds, pp, e, row0, nrows, c0); break;
+    }
 }
 
 template <int MT>
@@ -1693,10 +1714,11 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
 // The down GEMM's K (= I) is short, so a tile's prologue (plan lookups, first stages in
 // flight) and epilogue (output stores) are a large part of it.  It runs 128-row tiles
 // with two workgroups per CU (76.8 KB of LDS each): one workgroup's prologue and
-// epilogue overlap the other's MFMAs.  Class-0 tiles run as two 128-row halves, class-1
-// tiles as they are, class-2 tiles as 64-row tiles.  Virtual m-tiles: halves of class-0
-// tile k at 16 (k / 8) + k % 8 + 8 h (both on XCD k % 8, one after the other, so the
-// second finds the W tile in L2), then the class-1 and class-2 tiles.
+// epilogue overlap the other's MFMAs.  Tiles of more than 4 blocks (the first hdr[2]
+// of the list) run as two halves of up to 128 rows, the others as they are, each with
+// as many 32-row blocks as its rows need.  Virtual m-tiles: halves of big tile k at
+// 16 (k / 8) + k % 8 + 8 h (both on XCD k % 8, one after the other, so the second finds
+// the W tile in L2), then the small tiles.
 constexpr size_t kDownLds = Layout<4, 4>::kLds;
 
 __global__ __launch_bounds__(kThreads, 2) void moe_down_gemm_kernel(MoeArgs a) {
@@ -1713,18 +1735,20 @@ __global__ __launch_bounds__(kThreads, 2) void moe_down_gemm_kernel(MoeArgs a) {
     if (split ? k0 >= n0t : mt - nsplit + n0t >= ntiles)
         return;
     const int32_t *t = v.tiles + 4 * (split ? k0 : mt - nsplit + n0t);
-    const int e = uniform(t[0]), cls = uniform(t[3]);
+    const int e = uniform(t[0]);
     uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]);
     const uint32_t n0 = nt * BN;
     if (split) {
         const uint32_t h = (mt / 8) % 2;
         row0 += 128 * h;
         nrows = nrows - 128 * h < 128 ? nrows - 128 * h : 128;
-        down_tile<4>(a, lds, e, row0, nrows, n0);
-    } else if (cls == 1)
-        down_tile<4>(a, lds, e, row0, nrows, n0);
-    else
-        down_tile<2>(a, lds, e, row0, nrows, n0);
+    }
+    switch ((nrows + 31) / 32) {
+    case 4: down_tile<4>(a, lds, e, row0, nrows, n0); break;
+    case 3: down_tile<3>(a, lds, e, row0, nrows, n0); break;
+    case 2: down_tile<2>(a, lds, e, row0, nrows, n0); break;
+    default: down_tile<1>(a, lds, e, row0, nrows, n0); break;
+    }
 }
 
 // y[t] = sum_j w[t,j] d[pos(t,j)], slot order, fp32; 8 columns per thread.  Workgroup
@@ -2236,7 +2260,7 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     const uint32_t nn_gu = (a.I + kGateUpCols - 1) / kGateUpCols;
     hipLaunchKernelGGL(moe_gateup_gemm_kernel, dim3(mt8 * nn_gu), dim3(kThreads), kMaxLds, stream,
                        a);
-    // virtual m-tiles: at most 2 max_tiles + 16 (two halves per class-0 tile, padded
+    // virtual m-tiles: at most 2 max_tiles + 16 (two halves per big tile, padded
     // to whole groups of 8)
     const uint32_t nn_d = (a.H + BN - 1) / BN;
     const uint32_t vt8 = 8 * ((2 * a.max_tiles + 16 + 7) / 8);

@@ -163,9 +163,12 @@ def test_moe_hot_experts_span_many_tiles():
 
 
 def test_moe_tile_classes():
-    """Expert sizes hitting every tile class boundary (64, 65, 128, 129, 256, 257 rows)."""
+    """Expert sizes hitting every tail-tile size (1..8 blocks of 32 rows) at its
+    boundaries, whole 256-row tiles with and without a tail, and the down GEMM's split
+    of tiles over 4 blocks into 128-row halves (129, 160, 161 rows)."""
     rng = np.random.default_rng(6)
-    sizes = [1, 63, 64, 65, 127, 128, 129, 255, 256, 257, 300]
+    sizes = [1, 31, 32, 33, 63, 64, 65, 95, 96, 97, 127, 128, 129, 160, 161, 192, 193, 224,
+             225, 255, 256, 257, 300, 512, 545]
     E, H, I, k = len(sizes), 128, 64, 1
     T = sum(sizes)
     experts = np.repeat(np.arange(E), sizes)
