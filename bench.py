@@ -68,6 +68,19 @@ def geglu_workload(rows=21504, K=5376, seed=0):
     return x, gate, up, algo_bytes, flops
 
 
+def touch_weights(sets, stream):
+    """Read every weight copy once with the plain streaming-read probe, so that the
+    operands are resident and mapped before any launch is timed: the first kernel to
+    read a fresh allocation pays its page-table walks (measured: the launch that first
+    met the sixth copy took ~30 us against ~22 us).  A decode loop reads the same
+    weights every step, so its steady state has them mapped."""
+    sink = hip.DeviceArray((hip.read_probe_sink_words(),), np.uint32)
+    for s in sets:
+        for arr in s:
+            hip.read_probe(arr, sink, stream)
+    stream.synchronize()
+
+
 def time_geglu(steps: int, warmup: int, rows=21504, K=5376):
     x, gate, up, algo_bytes, flops = geglu_workload(rows, K)
     w_bytes = algo_bytes - x.nbytes - rows * 2
@@ -82,6 +95,7 @@ def time_geglu(steps: int, warmup: int, rows=21504, K=5376):
         sets.append(s)
     out = hip.DeviceArray((1, rows), np.uint16)
     stream = hip.Stream()
+    touch_weights(sets, stream)
 
     def step(i):
         gc, gs, uc, us = sets[i % copies]
