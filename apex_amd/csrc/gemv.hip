@@ -87,7 +87,10 @@ __global__ __launch_bounds__(kThreads) void read_probe_kernel(const void *p, uin
 
 } // namespace
 
-std::atomic<int> kTargetWavesPerCU{12};
+// 8 resident waves per CU, each with two row sets in flight: 21.6 us for the 130 MB
+// decode GeGLU against 22.0-22.3 us at 12 and 23.5 at 16 (9, 10 and 14 split the
+// persistent grid unevenly over the CUs: 24.7-26.6 us).
+std::atomic<int> kTargetWavesPerCU{8};
 std::atomic<int> kNumCUs{256};
 
 hipError_t gemv_launch(const GemvArgs &a, GemvMode mode, bool x_is_bf16, hipStream_t stream) {

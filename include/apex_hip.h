@@ -293,7 +293,7 @@ int apex_hip_event_elapsed_ms(void *start, void *stop, float *ms);
 int apex_hip_read_probe(const void *ptr, size_t bytes, uint32_t *sink, void *stream);
 int apex_hip_read_probe_sink_words(void);
 
-/* Launch tuning of the GEMV kernels: target resident waves per CU (default 12). */
+/* Launch tuning of the GEMV kernels: target resident waves per CU (default 8). */
 int apex_hip_set_gemv_waves_per_cu(int waves);
 
 /* Tokens from which apex_nvfp4_matmul_* and apex_nvfp4_geglu_* (and their registry
