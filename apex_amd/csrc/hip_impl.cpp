@@ -413,17 +413,9 @@ void router_impl(const apex_hip::MoeRouterArgs &a, hipStream_t stream) {
     if (!apex_hip::moe_router_supported(a, &why))
         fail(APEX_HIP_E_INVALID, std::string("moe_router: ") + why);
     init_device_tuning();
-    if (a.T >= apex_hip::kRouterMfmaMinTokens && apex_hip::moe_router_mfma_fits(a)) {
-        // prefill: MFMA form on the normed rows split into bf16 hi + lo
-        ScratchLease scratch(stream);
-        auto *split =
-            static_cast<uint16_t *>(scratch.get(0, apex_hip::gemm_split_bytes(a.T, a.H)));
-        hip_check(apex_hip::gemm_split_launch(a.h, a.norm_w, a.eps, split, a.T, a.H, stream),
-                  "moe_router split launch");
-        const uint32_t splits = apex_hip::moe_router_mfma_splits(a);
-        auto *part = static_cast<float *>(scratch.get(1, (size_t)splits * a.T * a.E * 4));
-        hip_check(apex_hip::moe_router_mfma_launch(a, split, part, splits, stream),
-                  "moe_router MFMA launch");
+    if (a.T >= apex_hip::kRouterMfmaMinTokens && apex_hip::moe_router_fused_fits(a)) {
+        // prefill: the fused MFMA form (bf16 hi + lo of the scaled rows made on the fly)
+        hip_check(apex_hip::moe_router_fused_launch(a, stream), "moe_router MFMA launch");
         return;
     }
     hip_check(apex_hip::moe_router_logits_launch(a, stream), "moe_router launch");

@@ -1964,190 +1964,311 @@ hipError_t router_launch_epl(const MoeRouterArgs &a, hipStream_t stream) {
 
 namespace {
 
-// Router logits on bf16 MFMA.  Workgroup: 4 waves = 128 tokens x 32 experts (wave w:
-// tokens t0 + 32 w + 0..31), the column groups [g0, g1) of its split.  Per group the
-// 8-bit codes (exact in bf16) multiply the hi and lo halves of x on the MFMAs into a
-// fresh accumulator (sum of q x over the group), the lane pair sums x over the group,
-// and the total gains s * sum(q x) + b * sum(x) in fp32 -- the reference's grouping
-// (orc_moe_router_logits_q8).  Accumulator element el of lane l: token l % 32, expert
-// 8 (el / 4) + 4 (l / 32) + el % 4 of the block (codes are the first MFMA operand).
-constexpr uint32_t kRouterMfmaGroups = kRouterMaxHidden / kQGroup;
+// Router logits, fused prefill form: one workgroup per block of kRfTokens tokens and
+// kRfExperts experts reads the tokens' fp32 rows once and produces their logits, with
+// no pass over the rows before it and no partials after it.  The RMSNorm's per-token
+// factor is taken out of the sums:
+//   logits[t][e] = inv[t] * sum_g (s[e][g] * sum_{k in g} q[e][k] x'[t][k]
+//                                  + b[e][g] * sum_{k in g} x'[t][k]),
+// x' = h * router.scale, inv = 1 / sqrt(mean(h^2) + eps) -- the reference's product
+// (orc_moe_router_logits_q8) regrouped, a few fp32 roundings apart.
+//   K advances in chunks of kRfGroups 64-column groups.  Four waves produce: thread p
+// owns token p / 16 and 4 columns of every group of every chunk, with kRfDepth
+// chunks' loads in flight (register ring); it multiplies by router.scale, adds h^2
+// into the token's sum of squares, splits x' into bf16 hi + lo (x' - hi: ~16
+// significant bits) straight into the MFMA operand layout in LDS, sums x' over each
+// group (16 lanes), and stages the chunk's group scales (p < 128) or biases.
+//   Four waves consume: consumer w takes group w of every chunk for all the block's
+// experts (4 tiles of 32), so no two waves read the same operands from LDS.  x is the
+// MFMA's first operand and the codes (exact in bf16, straight from L2 into registers,
+// one chunk ahead) its second, so each lane's accumulators are one expert's, for 16
+// tokens (of which rows 16..31 are zero padding and skipped): its group's scale and
+// bias are two scalars, and s * acc + b * sum(x') folds the group into the totals.
+// The four waves' totals are summed in wave order at the end.
+//   The roles meet at one barrier per chunk (LDS double-buffered); each keeps its own
+// loads in flight across it (a bare s_barrier: __syncthreads would wait for them).
+// Both run the same padded count of chunks (columns past H read zeros), so their
+// barriers pair up.
+//   At 4096 tokens x 128 experts x 2816: 32.7 us, against 53 us for a split pass
+// (normed rows -> bf16 hi + lo in HBM), an MFMA kernel on 128-token tiles with split
+// K and a partials sum.  What holds it there is the two roles together: each alone
+// (the other's work removed) takes 9-11 us; the consumers' instruction streams (code
+// conversion, fold) are the larger part.
+constexpr uint32_t kRfTokens = 16;
+constexpr uint32_t kRfGroups = 4;
+constexpr uint32_t kRfChunk = kRfGroups * kQGroup;
+constexpr uint32_t kRfSteps = kRfChunk / 16; // 32x32x16 k-steps per chunk
+constexpr uint32_t kRfDepth = 4;
+constexpr uint32_t kRfThreads = 512;
+constexpr uint32_t kRfExperts = 128;
 
-__global__ __launch_bounds__(256) void moe_router_mfma_kernel(MoeRouterArgs a, const uint16_t *split,
-                                                              float *part, uint32_t S) {
+__global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterArgs a) {
     typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-    __shared__ float s_sc[kRouterMfmaGroups][32], s_bi[kRouterMfmaGroups][32];
-    // the block's codes of the split's groups as bf16 (exact): [group][expert][72]
-    // (rows padded from 64 to 72 elements so the 32 lanes' 16-byte reads spread over
-    // the banks)
-    extern __shared__ u32x4_t s_codes[];
-    constexpr uint32_t kRow = 72 / 8;   // 16-byte pieces per expert row
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    typedef float f32x2_v __attribute__((ext_vector_type(2)));
+    typedef float f32x4_v __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
+    // [buffer][hi, lo][k-step ks][slot l ^ ks]: the MFMA's first operand, lane l = token
+    // l % 32, columns 8 (l / 32) .. +7 of the k-step; tokens 16..31 stay zero.  The
+    // XOR spreads a producer store instruction (16 k-steps of one token column) over
+    // the banks.  After the last chunk it holds the consumer waves' totals.
+    __shared__ u32x4_t s_x[2][2][kRfSteps][64];
+    __shared__ f32x2_v s_sb[2][kRfGroups][kRfExperts]; // [buffer][group][expert]: scale, bias
+    __shared__ float s_sx[2][kRfGroups][32];            // [buffer][group][token]: sum of x'
+    __shared__ float s_inv[kRfTokens];
     const uint32_t T = a.T, E = a.E, H = a.H, NG = H / kQGroup;
-    const uint32_t eb = (E + 31) / 32;
-    // Workgroups are dealt round-robin over the 8 XCDs: workgroup b takes unit
-    // (b % 8) * per_xcd + b / 8, expert block fastest, so the expert blocks that share
-    // one (token block, split) slice of x run one after another on one XCD and read it
-    // through one L2 (round-robin order: from HBM once per expert block, 4x the bytes).
-    const uint32_t units = ((T + 127) / 128) * eb * S;
-    const uint32_t per_xcd = (units + 7) / 8;
-    const uint32_t u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (u >= units)
-        return;
-    const uint32_t e0 = (u % eb) * 32;
-    const uint32_t s = (u / eb) % S, t0 = (u / eb / S) * 128;
-    const uint32_t g0 = s * NG / S, g1 = (s + 1) * NG / S;
-    for (uint32_t i = threadIdx.x; i < (g1 - g0) * 32; i += blockDim.x) {
-        const uint32_t g = g0 + i / 32, el = i % 32, e = e0 + el;
-        const bool ok = e < E;
-        s_sc[i / 32][el] = ok ? bf16_bits_to_f32(a.qs[(size_t)e * NG + g]) : 0.0f;
-        s_bi[i / 32][el] = ok ? bf16_bits_to_f32(a.qb[(size_t)e * NG + g]) : 0.0f;
-    }
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
-    for (uint32_t i = threadIdx.x; i < (g1 - g0) * 32 * 8; i += blockDim.x) {
-        // piece p (8 codes) of expert el in group g0 + gi
-        const uint32_t gi = i / 256, el = (i / 8) % 32, p = i % 8;
-        const uint32_t off = e0 + el < E ? (e0 + el) * H + (g0 + gi) * kQGroup + 8 * p : kOutOfRange;
-        const auto q2 = __builtin_amdgcn_raw_buffer_load_b64(rq, (int)off, 0, 0);
-        u32x4_t qb;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint32_t word = q2[c / 2], sh = 16 * (c % 2);
-            const float lo = (float)((word >> sh) & 0xFFu), hi = (float)((word >> (sh + 8)) & 0xFFu);
-            qb[c] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
-        }
-        s_codes[(gi * 32 + el) * kRow + p] = qb;
-    }
-    __syncthreads();
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t h = lane >> 5, r = lane & 31;
-    const uint32_t token = t0 + 32 * wave + r;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(split, T * 2 * H * 2);
-    const uint32_t arow = token < T ? token * 2 * H * 2 : kOutOfRange;
-    f32x16_t tot;
-#pragma unroll
-    for (int el = 0; el < 16; ++el)
-        tot[el] = 0.0f;
-    // One group's loads: per k-step the hi and lo pieces of x and 8 codes.
-    struct GroupRegs {
-        u32x4_t ahi[4], alo[4];
+    const uint32_t nc = (H + kRfChunk - 1) / kRfChunk;
+    const uint32_t ncp = (nc + kRfDepth - 1) / kRfDepth * kRfDepth; // a multiple of 2 as well
+    const uint32_t t0 = blockIdx.x * kRfTokens, e0 = blockIdx.y * kRfExperts;
+    const uint32_t wave = uniform(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63;
+    auto barrier = [] {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
-    auto load_group = [&](GroupRegs &G, uint32_t g) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const uint32_t k = kQGroup * g + 16 * ks + 8 * h;
-            const bool ok = g < g1;
-            G.ahi[ks] = load_b128(ra, arow == kOutOfRange || !ok ? kOutOfRange : arow + k * 2);
-            G.alo[ks] = load_b128(ra, arow == kOutOfRange || !ok ? kOutOfRange : arow + (H + k) * 2);
-        }
-    };
-    auto compute_group = [&](const GroupRegs &G, uint32_t g) {
-        f32x16_t acc;
-#pragma unroll
-        for (int el = 0; el < 16; ++el)
-            acc[el] = 0.0f;
-        float sx = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            // codes of expert r, columns 16 ks + 8 h .. +7 of the group
-            const bf16x8_t qv =
-                __builtin_bit_cast(bf16x8_t, s_codes[((g - g0) * 32 + r) * kRow + 2 * ks + h]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qv, __builtin_bit_cast(bf16x8_t, G.ahi[ks]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qv, __builtin_bit_cast(bf16x8_t, G.alo[ks]), acc, 0, 0, 0);
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-                sx += (__uint_as_float(G.ahi[ks][p] << 16) + __uint_as_float(G.ahi[ks][p] & 0xFFFF0000u)) +
-                      (__uint_as_float(G.alo[ks][p] << 16) + __uint_as_float(G.alo[ks][p] & 0xFFFF0000u));
-        }
-        sx = add_xor32(sx);   // the other half of the group's columns
-#pragma unroll
-        for (int el = 0; el < 16; ++el) {
-            const uint32_t ex = 8 * (el / 4) + 4 * h + el % 4;
-            tot[el] += s_sc[g - g0][ex] * acc[el] + s_bi[g - g0][ex] * sx;
-        }
-    };
-    // Two register sets: group g + 1's loads are in flight while group g is computed.
-    GroupRegs buf[2];
-    load_group(buf[0], g0);
-    for (uint32_t g = g0; g < g1; g += 2) {
-        load_group(buf[1], g + 1);
-        compute_group(buf[0], g);
-        if (g + 1 >= g1)
-            break;
-        load_group(buf[0], g + 2);
-        compute_group(buf[1], g + 1);
-    }
-    if (token >= T)
-        return;
-    float *out = part + ((size_t)s * T + token) * E;
-#pragma unroll
-    for (int el = 0; el < 16; ++el) {
-        const uint32_t e = e0 + 8 * (el / 4) + 4 * h + el % 4;
-        if (e < E)
-            out[e] = tot[el];
-    }
-}
 
-// logits[t][e] = sum over s = 0 .. S-1 of part[s][t][e], in that order.
-__global__ __launch_bounds__(256) void moe_router_partials_kernel(const float *part, uint32_t S,
-                                                                  float *logits, size_t n) {
-    for (size_t q = blockIdx.x * 256ull + threadIdx.x; q < n; q += (size_t)gridDim.x * 256) {
-        float acc = 0.0f;
-        for (uint32_t s = 0; s < S; ++s)
-            acc += part[s * n + q];
-        logits[q] = acc;
+    // Roles by SIMD (wave w runs on SIMD w % 4): waves 0, 1, 4, 5 produce and 2, 3, 6, 7
+    // consume, so no SIMD runs both (sharing one, the roles' instruction streams slowed
+    // each other down: 35.6 us at 4096 tokens against 9.9 and 9.3 for each alone).
+    const uint32_t ri = (wave >> 2) * 2 + (wave & 1); // index within the role, 0..3
+    if ((wave & 2) == 0) {
+        // ---- producers ----
+        const uint32_t p = ri * 64 + lane, tk = p >> 4, m = p & 15;
+        const __amdgpu_buffer_rsrc_t rh = make_rsrc(a.h, T * H * 4);
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.norm_w, H * 2);
+        // p < 128 stage the group scales, the others the biases, of expert e0 + p % 128
+        const __amdgpu_buffer_rsrc_t rsb = make_rsrc(ri < 2 ? a.qs : a.qb, E * NG * 2);
+        const uint32_t xrow = t0 + tk < T ? (t0 + tk) * H * 4 : kOutOfRange;
+        const uint32_t se = e0 + (p & (kRfExperts - 1));
+        // Load j of a chunk: thread p reads 16-byte piece pc = p % 16 + 16 j of its
+        // token's row segment (columns 4 pc .. +3, all in group j), so one load
+        // instruction reads 256 contiguous bytes of each of the wave's 4 rows.
+        struct Slot {
+            u32x4_t x[4];
+            u32x2_v w[4];
+            uint32_t sb[kRfGroups];
+        };
+        // chunk c's loads; columns past H, tokens past T and experts past E read zeros
+        auto issue = [&](Slot &s, uint32_t c) {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                const uint32_t k = c * kRfChunk + 4 * (m + 16 * j);
+                s.x[j] = load_b128<APEX_WEIGHT_CPOL>(rh, k < H && xrow != kOutOfRange ? xrow + k * 4 : kOutOfRange);
+                s.w[j] = __builtin_bit_cast(
+                    u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(rw, (int)(k < H ? k * 2 : kOutOfRange), 0, 0));
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < kRfGroups; ++j) {
+                const uint32_t g = kRfGroups * c + j;
+                uint32_t off = se < E && g < NG ? (se * NG + g) * 2 : kOutOfRange;
+                asm volatile("" : "+v"(off)); // no branch around the load (see issue_codes)
+                s.sb[j] = load_u16(rsb, off);
+            }
+        };
+        float ss = 0.0f;
+        auto split = [&](const Slot &s, int b) {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                float sx = 0.0f;
+                u32x2_v hi, lo;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const float h0 = __uint_as_float(s.x[j][2 * q]), h1 = __uint_as_float(s.x[j][2 * q + 1]);
+                    const uint32_t ww = s.w[j][q];
+                    const float v0 = h0 * __uint_as_float(ww << 16);
+                    const float v1 = h1 * __uint_as_float(ww & 0xFFFF0000u);
+                    ss = __builtin_fmaf(h0, h0, ss);
+                    ss = __builtin_fmaf(h1, h1, ss);
+                    sx += v0;
+                    sx += v1;
+                    const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{v0, v1}, bf16x2_v));
+                    const float r0 = v0 - __uint_as_float(hb << 16), r1 = v1 - __uint_as_float(hb & 0xFFFF0000u);
+                    hi[q] = hb;
+                    lo[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{r0, r1}, bf16x2_v));
+                }
+                // piece pc: k-step pc / 4, lane half (pc / 2) % 2, 8-byte quarter pc % 2
+                const uint32_t pc = m + 16 * j, ks = pc >> 2;
+                const uint32_t slot = (tk + 32 * ((pc >> 1) & 1)) ^ ks;
+                *reinterpret_cast<u32x2_v *>(reinterpret_cast<uint8_t *>(&s_x[b][0][ks][slot]) + 8 * (pc & 1)) = hi;
+                *reinterpret_cast<u32x2_v *>(reinterpret_cast<uint8_t *>(&s_x[b][1][ks][slot]) + 8 * (pc & 1)) = lo;
+                sx = group_sum<16>(sx); // the token's 16 lanes hold group j
+                if (m == 0)
+                    s_sx[b][j][tk] = sx;
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < kRfGroups; ++j)
+                reinterpret_cast<float *>(&s_sb[b][j][p & (kRfExperts - 1)])[p >> 7] =
+                    __uint_as_float(s.sb[j] << 16);
+        };
+        // Each slot's loads go out together and in slot order (compiler barriers: it
+        // would otherwise group the prologue's loads by kind, and the waits for slot 0
+        // would then cover the later slots' loads too).
+        Slot ring[kRfDepth];
+#pragma unroll
+        for (uint32_t d = 0; d < kRfDepth; ++d) {
+            issue(ring[d], d);
+            asm volatile("" ::: "memory");
+        }
+        // token columns 16..31 of both x buffers: never written, read as zeros
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const uint32_t q = p + 256 * i, r = q >> 5; // r: buffer, hi/lo, k-step
+            s_x[r >> 5][(r >> 4) & 1][r & 15][16 + (q & 15) + 32 * ((q >> 4) & 1)] = u32x4_t{0, 0, 0, 0};
+        }
+        barrier();
+        for (uint32_t c0 = 0; c0 < ncp; c0 += kRfDepth) {
+#pragma unroll
+            for (uint32_t d = 0; d < kRfDepth; ++d) {
+                split(ring[d], d & 1);
+                asm volatile("" ::: "memory");
+                issue(ring[d], c0 + d + kRfDepth);
+                asm volatile("" ::: "memory");
+                barrier();
+            }
+        }
+        ss = group_sum<16>(ss); // the token's 16 lanes
+        if (m == 0)
+            s_inv[tk] = 1.0f / sqrtf(ss / (float)H + a.eps);
+        barrier();
+        barrier(); // the consumers' totals are in LDS
+        return;
+    }
+
+    // ---- consumers ----
+    const uint32_t gl = ri, er = lane & 31, kh = lane >> 5;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
+    // codes of chunk c, this wave's group: tile i (experts e0 + 32 i ..), k-step kk,
+    // lane: expert e0 + 32 i + er, columns 8 kh .. +7 of the k-step
+    auto issue_codes = [&](u32x2_v (&cd)[4][4], uint32_t c) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t e = e0 + 32 * i + er;
+#pragma unroll
+            for (uint32_t kk = 0; kk < 4; ++kk) {
+                const uint32_t k = c * kRfChunk + kQGroup * gl + 16 * kk + 8 * kh;
+                uint32_t off = e < E && k < H ? e * H + k : kOutOfRange;
+                // opaque to the compiler: it would otherwise branch around the load
+                // for the out-of-range lanes instead of letting the descriptor drop it
+                asm volatile("" : "+v"(off));
+                cd[i][kk] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(rq, (int)off, 0, 0));
+            }
+        }
+    };
+    // 8 codes (bytes, low first) -> bf16, exact
+    auto cvt8 = [](u32x2_v w) {
+        u32x4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t word = w[j >> 1], sh = 16 * (j & 1);
+            const float f0 = (float)((word >> sh) & 0xFFu), f1 = (float)((word >> (sh + 8)) & 0xFFu);
+            o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{f0, f1}, bf16x2_v));
+        }
+        return __builtin_bit_cast(bf16x8_t, o);
+    };
+    // accumulator element el of a lane: expert column er, token row
+    // 8 (el / 4) + 4 kh + el % 4; rows 16..31 (el >= 8) are padding
+    float tot[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int el = 0; el < 8; ++el)
+            tot[i][el] = 0.0f;
+    // The chunk's LDS operands are read in one batch (read one by one right before
+    // their MFMAs, each waited out the LDS latency); four independent accumulator
+    // chains (one per tile) are interleaved.
+    auto consume = [&](const u32x2_v (&cd)[4][4], int b) {
+        u32x4_t xv[2][4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            xv[0][kk] = s_x[b][0][4 * gl + kk][lane ^ (4 * gl + kk)];
+            xv[1][kk] = s_x[b][1][4 * gl + kk][lane ^ (4 * gl + kk)];
+        }
+        f32x2_v sb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            sb[i] = s_sb[b][gl][32 * i + er];
+        const f32x4_v sx0 = *reinterpret_cast<const f32x4_v *>(&s_sx[b][gl][4 * kh]);
+        const f32x4_v sx1 = *reinterpret_cast<const f32x4_v *>(&s_sx[b][gl][8 + 4 * kh]);
+        asm volatile("" ::: "memory");
+        f32x16_t acc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int el = 0; el < 16; ++el)
+                acc[i][el] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            bf16x8_t q[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                q[i] = cvt8(cd[i][kk]);
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8_t, xv[hl][kk]), q[i], acc[i], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int el = 0; el < 8; ++el)
+                tot[i][el] += sb[i][0] * acc[i][el] + sb[i][1] * (el < 4 ? sx0[el] : sx1[el - 4]);
+    };
+    u32x2_v code[2][4][4];
+    issue_codes(code[0], 0);
+    if (ri * 64 + lane < 2 * kRfGroups * 32)
+        (&s_sx[0][0][0])[ri * 64 + lane] = 0.0f;
+    barrier();
+    for (uint32_t c0 = 0; c0 < ncp; c0 += 2) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            issue_codes(code[d ^ 1], c0 + d + 1);
+            asm volatile("" ::: "memory");
+            barrier();
+            consume(code[d], d);
+        }
+    }
+    barrier(); // s_inv is written; every wave is past its last read of s_x
+    // totals -> LDS [wave][tile][el][lane], summed in wave order by the wave owning the tile
+    float *red = reinterpret_cast<float *>(&s_x[0][0][0][0]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int el = 0; el < 8; ++el)
+            red[((gl * 4 + i) * 8 + el) * 64 + lane] = tot[i][el];
+    barrier();
+    const uint32_t e = e0 + 32 * gl + er;
+    if (e >= E)
+        return;
+#pragma unroll
+    for (int el = 0; el < 8; ++el) {
+        const uint32_t tk = 8 * (el >> 2) + 4 * kh + (el & 3), t = t0 + tk;
+        float v = 0.0f;
+#pragma unroll
+        for (uint32_t w = 0; w < 4; ++w)
+            v += red[((w * 4 + gl) * 8 + el) * 64 + lane];
+        if (t < T)
+            a.logits[(size_t)t * E + e] = v * s_inv[tk];
     }
 }
 
 } // namespace
 
-// Splits so that the workgroups cover the CUs about twice, at least 4 groups each.
-// at most this many groups per split: their converted codes (4.6 KB each) stay in LDS
-constexpr uint32_t kRouterMfmaMaxSplitGroups = 24;
-
-uint32_t moe_router_mfma_splits(const MoeRouterArgs &a) {
-    const uint32_t blocks = ((a.T + 127) / 128) * ((a.E + 31) / 32);
-    const uint32_t ng = a.H / kQGroup;
-    uint32_t s = (512 + blocks - 1) / blocks;
-    s = s < ng / 4 ? s : ng / 4;
-    const uint32_t smin = (ng + kRouterMfmaMaxSplitGroups - 1) / kRouterMfmaMaxSplitGroups;
-    s = s > smin ? s : smin;
-    return s >= 1 ? s : 1;
+bool moe_router_fused_fits(const MoeRouterArgs &a) {
+    return a.E <= kMoeMaxExperts && a.H <= kRouterMaxHidden && a.H % kQGroup == 0 &&
+           (uint64_t)a.T * a.H * 4 < (1ull << 31);
 }
 
-bool moe_router_mfma_fits(const MoeRouterArgs &a) {
-    const uint32_t splits = moe_router_mfma_splits(a);
-    return (uint64_t)a.T * a.H * 4 < (1ull << 31) &&
-           (uint64_t)splits * a.T * a.E * 4 < (1ull << 31) &&
-           (a.H / kQGroup + splits - 1) / splits <= kRouterMfmaMaxSplitGroups;
-}
-
-hipError_t moe_router_mfma_launch(const MoeRouterArgs &a, const uint16_t *split, float *part,
-                                  uint32_t splits, hipStream_t stream) {
+hipError_t moe_router_fused_launch(const MoeRouterArgs &a, hipStream_t stream) {
     if (a.T == 0)
         return hipSuccess;
-    if (splits < 1 || splits > a.H / kQGroup || (uint64_t)a.T * a.H * 4 >= (1ull << 31) ||
-        (a.H / kQGroup + splits - 1) / splits > kRouterMfmaMaxSplitGroups)
+    if (!moe_router_fused_fits(a))
         return hipErrorInvalidValue;
-    const uint32_t units = ((a.T + 127) / 128) * ((a.E + 31) / 32) * splits;
-    // converted codes: the largest split's groups x 32 experts x 72 bf16
-    const uint32_t ng = a.H / kQGroup, gmax = (ng + splits - 1) / splits;
-    const size_t lds = (size_t)gmax * 32 * 72 * 2;
-    // the limit is raised once, to what the largest split needs (any shape)
-    static std::atomic<uint64_t> attr{0};
-    if (hipError_t e = set_lds(moe_router_mfma_kernel, (size_t)kRouterMfmaMaxSplitGroups * 32 * 72 * 2,
-                               attr);
-        e != hipSuccess)
-        return e;
-    hipLaunchKernelGGL(moe_router_mfma_kernel, dim3(8 * ((units + 7) / 8)), dim3(256), lds, stream,
-                       a, split, part, splits);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess)
-        return e;
-    const size_t n = (size_t)a.T * a.E;
-    const uint32_t grid = (uint32_t)((n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048);
-    hipLaunchKernelGGL(moe_router_partials_kernel, dim3(grid), dim3(256), 0, stream, part, splits,
-                       a.logits, n);
+    // experts in blocks of kRfExperts (a second block re-reads the rows)
+    const dim3 grid((a.T + kRfTokens - 1) / kRfTokens, (a.E + kRfExperts - 1) / kRfExperts);
+    hipLaunchKernelGGL(moe_router_fused_kernel, grid, dim3(kRfThreads), 0, stream, a);
     return hipGetLastError();
 }
 

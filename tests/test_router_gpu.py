@@ -34,8 +34,8 @@ def test_router_small_shape_then_larger_shape():
     LDS: the LDS limit is raised once, to the kernel's largest possible size, so the
     second call must launch.  Placed first in the file so these are the process's first
     router launches.  VALU form (more than 256 tokens: 8-token tiles): 257 tokens at
-    H 64, E 8, then 300 at H 2816, E 64.  MFMA form (from 512 tokens): 512 tokens at
-    H 1024, E 8, then 8192 at H 2816, E 128, checked on a 64-token sample."""
+    H 64, E 8, then 300 at H 2816, E 64.  Fused MFMA form (from 512 tokens): 512 tokens
+    at H 1024, E 8, then 8192 at H 2816, E 128, checked on a 64-token sample."""
     rng = np.random.default_rng(21)
     for T, E, H, sample in [(257, 8, 64, None), (300, 64, 2816, None),
                             (512, 8, 1024, None), (8192, 128, 2816, 64)]:
@@ -51,8 +51,9 @@ def test_router_small_shape_then_larger_shape():
                                    (33, 64, 256), (9, 200, 4096), (257, 8, 64),
                                    (600, 128, 2816), (515, 200, 1024), (512, 8, 4096)])
 def test_router_logits_match_oracle(T, E, H):
-    """From 512 tokens the MFMA form runs (x split into bf16 hi + lo, codes exact in
-    bf16, split-K partials summed in order), below the VALU kernels."""
+    """From 512 tokens the fused MFMA form runs (the scaled rows split into bf16 hi + lo
+    on the fly, codes exact in bf16, the RMSNorm factor applied to the finished sums;
+    experts in blocks of 128, so E 200 takes two), below the VALU kernels."""
     h, rw = synth.router_case(seed=T + E, tokens=T, E=E, H=H)
     print(f"router logits T={T} E={E} H={H}", flush=True)
     got = router_logits(h, rw)
