@@ -49,11 +49,15 @@ def test_router_small_shape_then_larger_shape():
 
 @pytest.mark.parametrize("T,E,H", [(1, 128, 2816), (16, 128, 2816), (300, 128, 2816),
                                    (33, 64, 256), (9, 200, 4096), (257, 8, 64),
-                                   (600, 128, 2816), (515, 200, 1024), (512, 8, 4096)])
+                                   (600, 128, 2816), (515, 200, 1024), (512, 8, 4096),
+                                   (520, 128, 2880), (530, 16, 320), (512, 256, 192),
+                                   (513, 129, 64)])
 def test_router_logits_match_oracle(T, E, H):
     """From 512 tokens the fused MFMA form runs (the scaled rows split into bf16 hi + lo
     on the fly, codes exact in bf16, the RMSNorm factor applied to the finished sums;
-    experts in blocks of 128, so E 200 takes two), below the VALU kernels."""
+    experts in blocks of 128, so E 200 takes two), below the VALU kernels.  Its K
+    chunks are 256 columns: H 2880, 320, 192 and 64 end on a partial chunk of 1, 1, 3
+    and 1 groups; E 129 and 256 fill one expert block with one or all rows."""
     h, rw = synth.router_case(seed=T + E, tokens=T, E=E, H=H)
     print(f"router logits T={T} E={E} H={H}", flush=True)
     got = router_logits(h, rw)
