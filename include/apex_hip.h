@@ -345,8 +345,9 @@ int apex_moe_route_bf16(const uint16_t *logits, uint32_t tokens, uint32_t expert
  * with q the unsigned byte (k % 4) of proj_weights[e, k / 4] (u32 [experts, hidden/4]),
  * g = k / 64 and scales/biases bf16 [experts, hidden/64]; fp32 out [tokens, experts].
  * experts <= 256, hidden a multiple of 64 and at most 4096.  From 512 tokens the
- * product runs on bf16 MFMA (xn split into bf16 hi + lo, codes exact in bf16, group
- * scale and bias in fp32) using the dense GEMMs' per-device scratch. */
+ * product runs on bf16 MFMA in one kernel with no scratch (h * norm_weights split into
+ * bf16 hi + lo on the fly, codes exact in bf16, group scale and bias in fp32, the
+ * RMSNorm's per-token factor applied to the finished sums). */
 int apex_moe_router_logits_q8(const float *h, const uint16_t *norm_weights, float eps,
                               const uint32_t *proj_weights, const uint16_t *proj_scales,
                               const uint16_t *proj_biases, uint32_t tokens, uint32_t experts,
