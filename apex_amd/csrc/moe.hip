@@ -1989,11 +1989,11 @@ namespace {
 // loads in flight across it (a bare s_barrier: __syncthreads would wait for them).
 // Both run the same padded count of chunks (columns past H read zeros), so their
 // barriers pair up.
-//   At 4096 tokens x 128 experts x 2816: 32.7 us, against 53 us for a split pass
+//   At 4096 tokens x 128 experts x 2816: 24.8 us, against 53 us for a split pass
 // (normed rows -> bf16 hi + lo in HBM), an MFMA kernel on 128-token tiles with split
-// K and a partials sum.  What holds it there is the two roles together: each alone
-// (the other's work removed) takes 9-11 us; the consumers' instruction streams (code
-// conversion, fold) are the larger part.
+// K and a partials sum.  The small scattered loads weigh most: the codes as 16-byte
+// pieces (32.7 -> 26.0 us against 8-byte ones) and the scales as one 8-byte load per
+// chunk (-> 24.8 us against four 2-byte ones).
 constexpr uint32_t kRfTokens = 16;
 constexpr uint32_t kRfGroups = 4;
 constexpr uint32_t kRfChunk = kRfGroups * kQGroup;
@@ -2002,6 +2002,9 @@ constexpr uint32_t kRfDepth = 4;
 constexpr uint32_t kRfThreads = 512;
 constexpr uint32_t kRfExperts = 128;
 
+// SB4: the group count H / 64 is a multiple of 4, so a chunk's 4 group scales (and
+// biases) of an expert are one aligned 8-byte load instead of four 2-byte loads.
+template <bool SB4>
 __global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterArgs a) {
     typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
     typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
@@ -2009,9 +2012,11 @@ __global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterA
     typedef float f32x4_v __attribute__((ext_vector_type(4)));
     typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
     // [buffer][hi, lo][k-step ks][slot l ^ ks]: the MFMA's first operand, lane l = token
-    // l % 32, columns 8 (l / 32) .. +7 of the k-step; tokens 16..31 stay zero.  The
-    // XOR spreads a producer store instruction (16 k-steps of one token column) over
-    // the banks.  After the last chunk it holds the consumer waves' totals.
+    // l % 32; k-step kk of a group holds its columns 32 (l / 32) + 8 kk .. +7 (a
+    // permutation of the group's columns, applied to x and the codes alike, so a lane's
+    // codes of a group are 32 contiguous bytes); tokens 16..31 stay zero.  The XOR
+    // spreads a producer store instruction over the banks.  After the last chunk it
+    // holds the consumer waves' totals.
     __shared__ u32x4_t s_x[2][2][kRfSteps][64];
     __shared__ f32x2_v s_sb[2][kRfGroups][kRfExperts]; // [buffer][group][expert]: scale, bias
     __shared__ float s_sx[2][kRfGroups][32];            // [buffer][group][token]: sum of x'
@@ -2058,12 +2063,21 @@ __global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterA
                 s.w[j] = __builtin_bit_cast(
                     u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(rw, (int)(k < H ? k * 2 : kOutOfRange), 0, 0));
             }
-#pragma unroll
-            for (uint32_t j = 0; j < kRfGroups; ++j) {
-                const uint32_t g = kRfGroups * c + j;
+            if constexpr (SB4) {
+                const uint32_t g = kRfGroups * c;
                 uint32_t off = se < E && g < NG ? (se * NG + g) * 2 : kOutOfRange;
                 asm volatile("" : "+v"(off)); // no branch around the load (see issue_codes)
-                s.sb[j] = load_u16(rsb, off);
+                const u32x2_v v2 = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(rsb, (int)off, 0, 0));
+                s.sb[0] = v2[0];
+                s.sb[1] = v2[1];
+            } else {
+#pragma unroll
+                for (uint32_t j = 0; j < kRfGroups; ++j) {
+                    const uint32_t g = kRfGroups * c + j;
+                    uint32_t off = se < E && g < NG ? (se * NG + g) * 2 : kOutOfRange;
+                    asm volatile("" : "+v"(off)); // no branch around the load (see issue_codes)
+                    s.sb[j] = load_u16(rsb, off);
+                }
             }
         };
         float ss = 0.0f;
@@ -2087,19 +2101,22 @@ __global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterA
                     hi[q] = hb;
                     lo[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{r0, r1}, bf16x2_v));
                 }
-                // piece pc: k-step pc / 4, lane half (pc / 2) % 2, 8-byte quarter pc % 2
-                const uint32_t pc = m + 16 * j, ks = pc >> 2;
-                const uint32_t slot = (tk + 32 * ((pc >> 1) & 1)) ^ ks;
-                *reinterpret_cast<u32x2_v *>(reinterpret_cast<uint8_t *>(&s_x[b][0][ks][slot]) + 8 * (pc & 1)) = hi;
-                *reinterpret_cast<u32x2_v *>(reinterpret_cast<uint8_t *>(&s_x[b][1][ks][slot]) + 8 * (pc & 1)) = lo;
+                // group columns 4 m .. +3: k-step 4 j + (m / 2) % 4, lane half m / 8,
+                // 8-byte quarter m % 2 (the group's column order, see s_x)
+                const uint32_t ks = 4 * j + ((m >> 1) & 3);
+                const uint32_t slot = (tk + 32 * (m >> 3)) ^ ks;
+                *reinterpret_cast<u32x2_v *>(reinterpret_cast<uint8_t *>(&s_x[b][0][ks][slot]) + 8 * (m & 1)) = hi;
+                *reinterpret_cast<u32x2_v *>(reinterpret_cast<uint8_t *>(&s_x[b][1][ks][slot]) + 8 * (m & 1)) = lo;
                 sx = group_sum<16>(sx); // the token's 16 lanes hold group j
                 if (m == 0)
                     s_sx[b][j][tk] = sx;
             }
 #pragma unroll
-            for (uint32_t j = 0; j < kRfGroups; ++j)
-                reinterpret_cast<float *>(&s_sb[b][j][p & (kRfExperts - 1)])[p >> 7] =
-                    __uint_as_float(s.sb[j] << 16);
+            for (uint32_t j = 0; j < kRfGroups; ++j) {
+                const uint32_t bits = SB4 ? ((j & 1) ? s.sb[j >> 1] & 0xFFFF0000u : s.sb[j >> 1] << 16)
+                                          : s.sb[j] << 16;
+                reinterpret_cast<float *>(&s_sb[b][j][p & (kRfExperts - 1)])[p >> 7] = __uint_as_float(bits);
+            }
         };
         // Each slot's loads go out together and in slot order (compiler barriers: it
         // would otherwise group the prologue's loads by kind, and the waits for slot 0
@@ -2138,20 +2155,21 @@ __global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterA
     // ---- consumers ----
     const uint32_t gl = ri, er = lane & 31, kh = lane >> 5;
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
-    // codes of chunk c, this wave's group: tile i (experts e0 + 32 i ..), k-step kk,
-    // lane: expert e0 + 32 i + er, columns 8 kh .. +7 of the k-step
-    auto issue_codes = [&](u32x2_v (&cd)[4][4], uint32_t c) {
+    // codes of chunk c, this wave's group: tile i (experts e0 + 32 i ..), lane: expert
+    // e0 + 32 i + er; its four k-steps of the group are the expert's 32 code bytes
+    // 32 kh .. +31 (two 16-byte loads)
+    auto issue_codes = [&](u32x4_t (&cd)[4][2], uint32_t c) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t e = e0 + 32 * i + er;
 #pragma unroll
-            for (uint32_t kk = 0; kk < 4; ++kk) {
-                const uint32_t k = c * kRfChunk + kQGroup * gl + 16 * kk + 8 * kh;
+            for (uint32_t hh = 0; hh < 2; ++hh) {
+                const uint32_t k = c * kRfChunk + kQGroup * gl + 32 * kh + 16 * hh;
                 uint32_t off = e < E && k < H ? e * H + k : kOutOfRange;
                 // opaque to the compiler: it would otherwise branch around the load
                 // for the out-of-range lanes instead of letting the descriptor drop it
                 asm volatile("" : "+v"(off));
-                cd[i][kk] = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(rq, (int)off, 0, 0));
+                cd[i][hh] = load_b128(rq, off);
             }
         }
     };
@@ -2177,7 +2195,7 @@ __global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterA
     // The chunk's LDS operands are read in one batch (read one by one right before
     // their MFMAs, each waited out the LDS latency); four independent accumulator
     // chains (one per tile) are interleaved.
-    auto consume = [&](const u32x2_v (&cd)[4][4], int b) {
+    auto consume = [&](const u32x4_t (&cd)[4][2], int b) {
         u32x4_t xv[2][4];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -2202,7 +2220,7 @@ __global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterA
             bf16x8_t q[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                q[i] = cvt8(cd[i][kk]);
+                q[i] = cvt8(u32x2_v{cd[i][kk >> 1][2 * (kk & 1)], cd[i][kk >> 1][2 * (kk & 1) + 1]});
 #pragma unroll
             for (int hl = 0; hl < 2; ++hl)
 #pragma unroll
@@ -2216,7 +2234,7 @@ __global__ __launch_bounds__(kRfThreads) void moe_router_fused_kernel(MoeRouterA
             for (int el = 0; el < 8; ++el)
                 tot[i][el] += sb[i][0] * acc[i][el] + sb[i][1] * (el < 4 ? sx0[el] : sx1[el - 4]);
     };
-    u32x2_v code[2][4][4];
+    u32x4_t code[2][4][2];
     issue_codes(code[0], 0);
     if (ri * 64 + lane < 2 * kRfGroups * 32)
         (&s_sx[0][0][0])[ri * 64 + lane] = 0.0f;
@@ -2268,7 +2286,11 @@ hipError_t moe_router_fused_launch(const MoeRouterArgs &a, hipStream_t stream) {
         return hipErrorInvalidValue;
     // experts in blocks of kRfExperts (a second block re-reads the rows)
     const dim3 grid((a.T + kRfTokens - 1) / kRfTokens, (a.E + kRfExperts - 1) / kRfExperts);
-    hipLaunchKernelGGL(moe_router_fused_kernel, grid, dim3(kRfThreads), 0, stream, a);
+    // 8-byte scale / bias loads: 4 groups per expert row chunk, 8-byte aligned tables
+    if ((a.H / kQGroup) % kRfGroups == 0 && ((uintptr_t)a.qs | (uintptr_t)a.qb) % 8 == 0)
+        hipLaunchKernelGGL(moe_router_fused_kernel<true>, grid, dim3(kRfThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL(moe_router_fused_kernel<false>, grid, dim3(kRfThreads), 0, stream, a);
     return hipGetLastError();
 }
 
