@@ -576,7 +576,7 @@ __device__ __forceinline__ int wave_excl_scan(int x, int lane, int &total) {
 constexpr int kTileClasses = 8; // tiles of 8, 7, ..., 1 blocks of 32 rows
 constexpr int kPlanScans = 2 + kTileClasses; // pair counts, active flags, tiles per class
 
-__device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first) {
+__device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first, bool publish = true) {
     __shared__ int wsum[kPlanScans][kMoeMaxExperts / 64];
     const uint32_t E = a.E, P = a.T * a.k;
     const PlanView v = plan_view(a.plan, E, P);
@@ -625,6 +625,10 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first) {
         const int e = tid;
         const int off = excl[0];
         first[e] = off;
+    }
+    if (publish && tid < (int)E) {
+        const int e = tid;
+        const int off = excl[0];
         v.off[e] = off;
         v.cnt[e] = c;
         if (c > 0)
@@ -641,7 +645,7 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first) {
             t[0] = e, t[1] = off + 256 * full, t[2] = c % 256, t[3] = blocks;
         }
     }
-    if (tid == 0) {
+    if (publish && tid == 0) {
         v.off[E] = total[0];
         v.hdr[0] = total[1];
         int nt = 0;
@@ -655,15 +659,15 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first) {
     __syncthreads();
 }
 
-// Prefill grouping, deterministic and free of contended atomics, in three launches.
+// Prefill grouping, deterministic and free of contended atomics, in two launches.
 // 1. moe_route_hist_kernel: each workgroup routes kRouteBlockTokens tokens and marks,
 //    per expert, the bit of every one of its tokens that chose it (LDS atomicOr, whose
 //    result does not depend on order).  A pair's rank inside its workgroup's group is
 //    the popcount of its expert's mask below its token's bit; the mask's popcount is
 //    the workgroup's count for the expert -> hist[block][expert].
-// 2. moe_plan_scan_kernel (one workgroup): per expert, the exclusive scan of hist over
-//    the workgroups (written back in place) and the total count; plan_scan.
-// 3. moe_plan_scatter_kernel: pos = off[e] + hist[block][e] + rank, one pair per thread.
+// 2. moe_plan_place_kernel (one workgroup per routing block): the per-expert counts and
+//    the block's prefix over the blocks before it, plan_scan (published by workgroup
+//    0), and pos = off[e] + prefix[e] + rank for the block's pairs.
 // kRouteBlockTokens (moe.h) tokens per workgroup: one per wave of 1024 threads
 
 __global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
@@ -698,96 +702,61 @@ __global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
         a.hist[(size_t)blockIdx.x * E + e] = __popcll(mask[e]);
 }
 
-__global__ __launch_bounds__(1024) void moe_plan_scan_kernel(MoeArgs a) {
-    __shared__ int cnt[kMoeMaxExperts], first[kMoeMaxExperts];
-    __shared__ int part[1024];
-    constexpr uint32_t kChunk = 16; // hist loads in flight per thread
-    const uint32_t E = a.E;
+// One workgroup per routing block b: every workgroup sums hist over all blocks per
+// expert (the counts) and over the blocks before its own (its pairs' base within each
+// expert's group), scans the counts over the experts (the group offsets, plan_scan;
+// workgroup 0 also publishes the plan), and places its own pairs:
+// pos = off[e] + sum_{b' < b} hist[b'][e] + rank.  Every workgroup reading the whole
+// hist from L2 costs less than a one-workgroup scan and a launch between.
+__global__ __launch_bounds__(1024) void moe_plan_place_kernel(MoeArgs a) {
+    __shared__ int s_tot[1024], s_pre[1024];
+    __shared__ int cnt[kMoeMaxExperts], first[kMoeMaxExperts], pre[kMoeMaxExperts];
+    const uint32_t E = a.E, k = a.k, b = blockIdx.x;
     const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
-    // thread (e, q): expert e, part q of the workgroups
+    // thread (e, q): expert e, part q of the blocks
     const uint32_t nq = blockDim.x / E;
     const uint32_t e = threadIdx.x % E, q = threadIdx.x / E;
-    const bool active = q < nq;
     const uint32_t per = (nb + nq - 1) / nq;
-    const uint32_t b0 = q * per < nb ? q * per : nb;
-    const uint32_t b1 = b0 + per < nb ? b0 + per : nb;
-    if (threadIdx.x < kMoeMaxExperts)
-        cnt[threadIdx.x] = 0;
-    if (per <= 2 * kChunk) {
-        // one load of the part's counts, kept in registers for the write-back
-        int c[2 * kChunk];
-        int sum = 0;
+    const uint32_t b0 = q < nq ? min(q * per, nb) : nb, b1 = min(b0 + per, nb);
+    int tot = 0, below = 0;
+    for (uint32_t bb = b0; bb < b1; bb += 8) {
+        int c[8];
 #pragma unroll
-        for (uint32_t i = 0; i < 2 * kChunk; ++i) {
-            c[i] = active && b0 + i < b1 ? a.hist[(size_t)(b0 + i) * E + e] : 0;
-            sum += c[i];
-        }
-        part[threadIdx.x] = sum;
-        __syncthreads();
-        if (active) {
-            int run = 0;
-            for (uint32_t qq = 0; qq < q; ++qq)
-                run += part[qq * E + e];
+        for (uint32_t i = 0; i < 8; ++i)
+            c[i] = bb + i < b1 ? a.hist[(size_t)(bb + i) * E + e] : 0;
 #pragma unroll
-            for (uint32_t i = 0; i < 2 * kChunk; ++i)
-                if (b0 + i < b1) {
-                    a.hist[(size_t)(b0 + i) * E + e] = run;
-                    run += c[i];
-                }
-            if (q == nq - 1)
-                cnt[e] = run;
+        for (uint32_t i = 0; i < 8; ++i) {
+            tot += c[i];
+            below += bb + i < b ? c[i] : 0;
         }
-        __syncthreads();
-        plan_scan(a, cnt, first);
-        return;
     }
-    int sum = 0;
-    if (active)
-        for (uint32_t b = b0; b < b1; b += kChunk) {
-            int c[kChunk];
-#pragma unroll
-            for (uint32_t i = 0; i < kChunk; ++i)
-                c[i] = b + i < b1 ? a.hist[(size_t)(b + i) * E + e] : 0;
-#pragma unroll
-            for (uint32_t i = 0; i < kChunk; ++i)
-                sum += c[i];
-        }
-    part[threadIdx.x] = sum;
+    s_tot[threadIdx.x] = tot;
+    s_pre[threadIdx.x] = below;
     __syncthreads();
-    if (active) {
-        int run = 0; // this part's start: the earlier parts' totals
-        for (uint32_t qq = 0; qq < q; ++qq)
-            run += part[qq * E + e];
-        for (uint32_t b = b0; b < b1; b += kChunk) {
-            int c[kChunk];
-#pragma unroll
-            for (uint32_t i = 0; i < kChunk; ++i)
-                c[i] = b + i < b1 ? a.hist[(size_t)(b + i) * E + e] : 0;
-#pragma unroll
-            for (uint32_t i = 0; i < kChunk; ++i)
-                if (b + i < b1) {
-                    a.hist[(size_t)(b + i) * E + e] = run;
-                    run += c[i];
-                }
-        }
-        if (q == nq - 1)
-            cnt[e] = run;
+    if (threadIdx.x < kMoeMaxExperts) {
+        int t = 0, pb = 0;
+        if (threadIdx.x < E)
+            for (uint32_t qq = 0; qq < nq; ++qq) {
+                t += s_tot[qq * E + threadIdx.x];
+                pb += s_pre[qq * E + threadIdx.x];
+            }
+        cnt[threadIdx.x] = t;
+        pre[threadIdx.x] = pb;
     }
     __syncthreads();
-    plan_scan(a, cnt, first);
-}
-
-__global__ __launch_bounds__(256) void moe_plan_scatter_kernel(MoeArgs a) {
-    const uint32_t P = a.T * a.k;
-    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= P)
-        return;
-    const PlanView v = plan_view(a.plan, a.E, P);
-    const int e = a.ids[p];
-    const uint32_t b = p / a.k / kRouteBlockTokens;
-    const int pos = v.off[e] + a.hist[(size_t)b * a.E + e] + a.rank[p];
-    v.pos_of_pair[p] = pos;
-    v.pair_of_pos[pos] = (int32_t)p;
+    plan_scan(a, cnt, first, b == 0);
+    // this block's pairs
+    const uint32_t P = a.T * k;
+    const PlanView v = plan_view(a.plan, E, P);
+    const uint32_t p0 = b * kRouteBlockTokens * k;
+    const uint32_t np = min(kRouteBlockTokens * k, P - p0);
+    for (uint32_t i = threadIdx.x; i < np; i += blockDim.x) {
+        const uint32_t p = p0 + i;
+        const int ex = a.ids[p];
+        const int pos = first[ex] + pre[ex] + a.rank[p];
+        v.pos_of_pair[p] = pos;
+        v.pair_of_pos[pos] = (int32_t)p;
+    }
 }
 
 // Decode plan from the experts' token masks (bit t of mask[e]: token t chose expert e),
@@ -2397,8 +2366,7 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
         return err;
     const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
     hipLaunchKernelGGL(moe_route_hist_kernel, dim3(nb), dim3(64 * kRouteBlockTokens), 0, stream, a);
-    hipLaunchKernelGGL(moe_plan_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
-    hipLaunchKernelGGL(moe_plan_scatter_kernel, dim3((a.T * a.k + 255) / 256), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(moe_plan_place_kernel, dim3(nb), dim3(1024), 0, stream, a);
     const uint32_t mt8 = 8 * ((a.max_tiles + 7) / 8); // m-tiles rounded to whole XCD turns
     const uint32_t nn_gu = (a.I + kGateUpCols - 1) / kGateUpCols;
     hipLaunchKernelGGL(moe_gateup_gemm_kernel, dim3(mt8 * nn_gu), dim3(kThreads), kMaxLds, stream,
