@@ -466,34 +466,63 @@ __global__ __launch_bounds__(256) void moe_router_small_kernel(MoeRouterArgs a) 
     const int j = lane % 16;
     const uint32_t e = blockIdx.y * kRouterSmallExperts + 4 * wave + lane / 16;
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qw, E * H);
+    const __amdgpu_buffer_rsrc_t rqs = make_rsrc(a.qs, E * NG * 2), rqb = make_rsrc(a.qb, E * NG * 2);
+    // Every load of the kernel goes out at entry, with offsets the compiler cannot see
+    // through (a select it can see becomes a branch around the load) and no load
+    // waited for before the last is issued: codes, group scales and biases, the token's
+    // row and the norm weights.
     u32x4_t q4[kRouterSmallSlots][4];
-    uint32_t sb[kRouterSmallSlots];
+    uint32_t sc[kRouterSmallSlots], bi[kRouterSmallSlots];
 #pragma unroll
     for (int s = 0; s < kRouterSmallSlots; ++s) {
         const uint32_t g = j + 16 * s;
         const bool ok = e < E && g < NG;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            q4[s][i] = load_b128(rq, ok ? e * H + g * kQGroup + 16 * i : kOutOfRange);
-        sb[s] = ok ? (uint32_t)a.qs[(size_t)e * NG + g] | ((uint32_t)a.qb[(size_t)e * NG + g] << 16) : 0u;
+        for (int i = 0; i < 4; ++i) {
+            uint32_t off = ok ? e * H + g * kQGroup + 16 * i : kOutOfRange;
+            asm volatile("" : "+v"(off));
+            q4[s][i] = load_b128(rq, off);
+        }
+        uint32_t so = ok ? (e * NG + g) * 2 : kOutOfRange;
+        asm volatile("" : "+v"(so));
+        sc[s] = load_u16(rqs, so);
+        bi[s] = load_u16(rqb, so);
     }
-    // the token's row -> LDS, its sum of squares
+    // the token's row (4 floats per piece) and its norm weights, all pieces at once
+    constexpr int kRowPieces = kRouterMaxHidden / 4 / 256;
     const __amdgpu_buffer_rsrc_t rh = make_rsrc(a.h + (size_t)t * H, H * 4);
-    float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < H / 4; i += blockDim.x) {
-        const u32x4_t v = load_b128(rh, i * 16);
-        *reinterpret_cast<u32x4_t *>(xn + 4 * i) = v;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.norm_w, H * 2);
+    u32x4_t hv[kRowPieces];
+    uint32_t wv[kRowPieces][4];
+#pragma unroll
+    for (int r = 0; r < kRowPieces; ++r) {
+        const uint32_t i = threadIdx.x + 256 * r;
+        uint32_t off = i < H / 4 ? i * 16 : kOutOfRange;
+        asm volatile("" : "+v"(off));
+        hv[r] = load_b128(rh, off);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            ss += __uint_as_float(v[c]) * __uint_as_float(v[c]);
+            wv[r][c] = load_u16(rw, off == kOutOfRange ? kOutOfRange : off / 2 + 2 * c);
     }
+    float ss = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kRowPieces; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            ss += __uint_as_float(hv[r][c]) * __uint_as_float(hv[r][c]);
     ss = group_sum<64>(ss);
     if (lane == 0)
         red[wave] = ss;
     __syncthreads();
     const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + a.eps);
-    for (uint32_t i = threadIdx.x; i < H; i += blockDim.x)
-        xn[i] = xn[i] * inv * bf16_bits_to_f32(a.norm_w[i]);
+#pragma unroll
+    for (int r = 0; r < kRowPieces; ++r) {
+        const uint32_t i = threadIdx.x + 256 * r;
+        if (i < H / 4)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                xn[4 * i + c] = __uint_as_float(hv[r][c]) * inv * bf16_bits_to_f32((uint16_t)wv[r][c]);
+    }
     __syncthreads();
     for (uint32_t g = wave; g < NG; g += 4) { // a group of 64 per wave, summed by DPP
         const float sum = group_sum<64>(xn[g * kQGroup + lane]);
@@ -517,7 +546,7 @@ __global__ __launch_bounds__(256) void moe_router_small_kernel(MoeRouterArgs a) 
             aq = __builtin_fmaf(xv.z, (float)((wv >> 16) & 0xFFu), aq);
             aq = __builtin_fmaf(xv.w, (float)(wv >> 24), aq);
         }
-        acc += __uint_as_float(sb[s] << 16) * aq + __uint_as_float(sb[s] & 0xFFFF0000u) * gsum[g];
+        acc += __uint_as_float(sc[s] << 16) * aq + __uint_as_float(bi[s] << 16) * gsum[g];
     }
     acc = group_sum<16>(acc);
     if (j == 0 && e < E)
