@@ -1158,6 +1158,13 @@ int apex_hip_memset(void *dst, int value, size_t bytes) {
     return guard([&] { hip_check(hipMemset(dst, value, bytes), "memset"); });
 }
 
+int apex_hip_mem_info(size_t *free_bytes, size_t *total_bytes) {
+    return guard([&] {
+        require(free_bytes && total_bytes, "mem_info: null pointer");
+        hip_check(hipMemGetInfo(free_bytes, total_bytes), "hipMemGetInfo");
+    });
+}
+
 int apex_hip_device_synchronize(void) {
     return guard([&] { hip_check(hipDeviceSynchronize(), "device sync"); });
 }
@@ -1265,6 +1272,11 @@ size_t apex_moe_workspace_bytes(uint32_t tokens, uint32_t experts, uint32_t top_
     return apex_hip::moe_workspace(tokens, experts, top_k, hidden, inter, true).total;
 }
 
+size_t apex_moe_workspace_plan_offset(uint32_t tokens, uint32_t experts, uint32_t top_k,
+                                      uint32_t hidden, uint32_t inter) {
+    return apex_hip::moe_workspace(tokens, experts, top_k, hidden, inter, true).plan;
+}
+
 int apex_moe_route_bf16(const uint16_t *logits, uint32_t tokens, uint32_t experts, uint32_t top_k,
                         int32_t *ids, float *weights, void *stream) {
     return guard([&] { moe_route_impl(logits, tokens, experts, top_k, ids, weights, as_stream(stream)); });
@@ -1286,6 +1298,21 @@ int apex_moe_ffn_bf16_noalloc(const uint16_t *x, const uint16_t *logits,
                               uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
                               void *stream) {
     return guard([&] {
+        // The fixed workspace is one array per device: a second thread enqueuing on the
+        // same device while a call is in progress would race on it, so it is refused.
+        constexpr int kMaxDevices = 64;
+        static std::atomic<bool> busy[kMaxDevices] = {};
+        int dev = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        require(dev >= 0 && dev < kMaxDevices, "moe_ffn (no-allocation form): device index");
+        if (busy[dev].exchange(true, std::memory_order_acquire))
+            fail(APEX_HIP_E_INVALID,
+                 "moe_ffn (no-allocation form): another call is in progress on this device; calls "
+                 "sharing the fixed workspace must be serialised on one stream per device");
+        struct Release {
+            std::atomic<bool> &b;
+            ~Release() { b.store(false, std::memory_order_release); }
+        } release{busy[dev]};
         moe_impl(x, logits, nullptr, nullptr, slots, y, tokens, experts, top_k, hidden, inter,
                  nullptr, 0, as_stream(stream));
     });

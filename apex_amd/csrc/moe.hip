@@ -688,15 +688,19 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first, bool pub
     __syncthreads();
 }
 
-// Prefill grouping, deterministic and free of contended atomics, in two launches.
+// Prefill grouping, deterministic and free of contended atomics, in three launches whose
+// work is linear in the tokens (O(T/16 * E) reads in all):
 // 1. moe_route_hist_kernel: each workgroup routes kRouteBlockTokens tokens and marks,
 //    per expert, the bit of every one of its tokens that chose it (LDS atomicOr, whose
 //    result does not depend on order).  A pair's rank inside its workgroup's group is
 //    the popcount of its expert's mask below its token's bit; the mask's popcount is
 //    the workgroup's count for the expert -> hist[block][expert].
-// 2. moe_plan_place_kernel (one workgroup per routing block): the per-expert counts and
-//    the block's prefix over the blocks before it, plan_scan (published by workgroup
-//    0), and pos = off[e] + prefix[e] + rank for the block's pairs.
+// 2. moe_hist_scan_kernel: per expert, an exclusive scan of hist over the blocks (in
+//    place: hist[b][e] becomes the expert's pairs in blocks before b) and the expert's
+//    total into hist row nb.
+// 3. moe_place_kernel (one workgroup per routing block): plan_scan over the totals
+//    (published by workgroup 0) and pos = off[e] + hist[b][e] + rank for the block's
+//    pairs.
 // kRouteBlockTokens (moe.h) tokens per workgroup: one per wave of 1024 threads
 
 __global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
@@ -731,54 +735,73 @@ __global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
         a.hist[(size_t)blockIdx.x * E + e] = __popcll(mask[e]);
 }
 
-// One workgroup per routing block b: every workgroup sums hist over all blocks per
-// expert (the counts) and over the blocks before its own (its pairs' base within each
-// expert's group), scans the counts over the experts (the group offsets, plan_scan;
-// workgroup 0 also publishes the plan), and places its own pairs:
-// pos = off[e] + sum_{b' < b} hist[b'][e] + rank.  Every workgroup reading the whole
-// hist from L2 costs less than a one-workgroup scan and a launch between.
-__global__ __launch_bounds__(1024) void moe_plan_place_kernel(MoeArgs a) {
-    __shared__ int s_tot[1024], s_pre[1024];
-    __shared__ int cnt[kMoeMaxExperts], first[kMoeMaxExperts], pre[kMoeMaxExperts];
-    const uint32_t E = a.E, k = a.k, b = blockIdx.x;
+// Column scan of hist: workgroup g owns experts [64 g, 64 g + 64), one per lane; wave w
+// owns blocks [w per, (w + 1) per).  Pass 1 sums each thread's blocks; the waves' sums
+// are scanned through LDS; pass 2 rewrites each thread's blocks with their exclusive
+// prefixes.  Each hist entry is read twice and written once.
+constexpr uint32_t kHistScanWaves = 16;
+
+__global__ __launch_bounds__(64 * kHistScanWaves) void moe_hist_scan_kernel(MoeArgs a) {
+    __shared__ int s_sum[kHistScanWaves][64];
+    const uint32_t E = a.E;
     const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
-    // thread (e, q): expert e, part q of the blocks
-    const uint32_t nq = blockDim.x / E;
-    const uint32_t e = threadIdx.x % E, q = threadIdx.x / E;
-    const uint32_t per = (nb + nq - 1) / nq;
-    const uint32_t b0 = q < nq ? min(q * per, nb) : nb, b1 = min(b0 + per, nb);
-    int tot = 0, below = 0;
-    for (uint32_t bb = b0; bb < b1; bb += 8) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t e = blockIdx.x * 64 + lane;
+    const uint32_t per = (nb + kHistScanWaves - 1) / kHistScanWaves;
+    const uint32_t b0 = min(wave * per, nb), b1 = min(b0 + per, nb);
+    int32_t *col = a.hist + e;
+    const bool mine = e < E;
+    int sum = 0;
+    for (uint32_t b = b0; b < b1; b += 8) {
         int c[8];
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i)
-            c[i] = bb + i < b1 ? a.hist[(size_t)(bb + i) * E + e] : 0;
+            c[i] = mine && b + i < b1 ? col[(size_t)(b + i) * E] : 0;
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i)
+            sum += c[i];
+    }
+    s_sum[wave][lane] = sum;
+    __syncthreads();
+    int run = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < (int)kHistScanWaves; ++w) {
+        const int v = s_sum[w][lane];
+        run += w < wave ? v : 0;
+        total += v;
+    }
+    if (mine && wave == 0)
+        col[(size_t)nb * E] = total;
+    for (uint32_t b = b0; b < b1; b += 8) {
+        int c[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i)
+            c[i] = mine && b + i < b1 ? col[(size_t)(b + i) * E] : 0;
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) {
-            tot += c[i];
-            below += bb + i < b ? c[i] : 0;
+            if (mine && b + i < b1)
+                col[(size_t)(b + i) * E] = run;
+            run += c[i];
         }
     }
-    s_tot[threadIdx.x] = tot;
-    s_pre[threadIdx.x] = below;
-    __syncthreads();
-    if (threadIdx.x < kMoeMaxExperts) {
-        int t = 0, pb = 0;
-        if (threadIdx.x < E)
-            for (uint32_t qq = 0; qq < nq; ++qq) {
-                t += s_tot[qq * E + threadIdx.x];
-                pb += s_pre[qq * E + threadIdx.x];
-            }
-        cnt[threadIdx.x] = t;
-        pre[threadIdx.x] = pb;
-    }
+}
+
+// One workgroup per routing block b: the per-expert totals (hist row nb) scanned over
+// the experts (plan_scan; workgroup 0 publishes the plan), then the block's pairs:
+// pos = off[e] + hist[b][e] (pairs of e in the blocks before b) + rank.
+__global__ __launch_bounds__(256) void moe_place_kernel(MoeArgs a) {
+    __shared__ int cnt[kMoeMaxExperts], first[kMoeMaxExperts];
+    const uint32_t E = a.E, k = a.k, b = blockIdx.x;
+    const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
+    for (uint32_t e = threadIdx.x; e < kMoeMaxExperts; e += blockDim.x)
+        cnt[e] = e < E ? a.hist[(size_t)nb * E + e] : 0;
     __syncthreads();
     plan_scan(a, cnt, first, b == 0);
-    // this block's pairs
     const uint32_t P = a.T * k;
     const PlanView v = plan_view(a.plan, E, P);
     const uint32_t p0 = b * kRouteBlockTokens * k;
     const uint32_t np = min(kRouteBlockTokens * k, P - p0);
+    const int32_t *pre = a.hist + (size_t)b * E;
     for (uint32_t i = threadIdx.x; i < np; i += blockDim.x) {
         const uint32_t p = p0 + i;
         const int ex = a.ids[p];
@@ -2395,7 +2418,8 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
         return err;
     const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
     hipLaunchKernelGGL(moe_route_hist_kernel, dim3(nb), dim3(64 * kRouteBlockTokens), 0, stream, a);
-    hipLaunchKernelGGL(moe_plan_place_kernel, dim3(nb), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL(moe_hist_scan_kernel, dim3((a.E + 63) / 64), dim3(64 * kHistScanWaves), 0, stream, a);
+    hipLaunchKernelGGL(moe_place_kernel, dim3(nb), dim3(256), 0, stream, a);
     const uint32_t mt8 = 8 * ((a.max_tiles + 7) / 8); // m-tiles rounded to whole XCD turns
     const uint32_t nn_gu = (a.I + kGateUpCols - 1) / kGateUpCols;
     hipLaunchKernelGGL(moe_gateup_gemm_kernel, dim3(mt8 * nn_gu), dim3(kThreads), kMaxLds, stream,

@@ -86,6 +86,7 @@ _PROTOS = {
     "apex_hip_memcpy_d2h": (_I, [_P, _P, _SZ]),
     "apex_hip_memcpy_d2d": (_I, [_P, _P, _SZ]),
     "apex_hip_memset": (_I, [_P, _I, _SZ]),
+    "apex_hip_mem_info": (_I, [_P, _P]),
     "apex_hip_device_synchronize": (_I, []),
     "apex_hip_stream_create": (_I, [C.POINTER(_P)]),
     "apex_hip_stream_destroy": (_I, [_P]),
@@ -103,6 +104,7 @@ _PROTOS = {
     "apex_hip_gemm_tail_plan": (_I, [_U32, _U32, _I, _U32, _P]),
     "apex_moe_route_bf16": (_I, [_P, _U32, _U32, _U32, _P, _P, _P]),
     "apex_moe_workspace_bytes": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
+    "apex_moe_workspace_plan_offset": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
     "apex_moe_ffn_bf16": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _SZ, _P]),
     "apex_hip_set_moe_path": (_I, [_I]),
     "apex_moe_ffn_bf16_noalloc": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P]),
@@ -237,6 +239,13 @@ class Event:
         if self.handle:
             lib().apex_hip_event_destroy(self.handle)
             self.handle = None
+
+
+def mem_info() -> tuple:
+    """(free, total) bytes of the current device."""
+    free, total = C.c_size_t(0), C.c_size_t(0)
+    check(lib().apex_hip_mem_info(C.byref(free), C.byref(total)))
+    return free.value, total.value
 
 
 def synchronize():
@@ -396,6 +405,20 @@ def moe_ffn_f32logits_bf16(x, logits, per_expert_scale, slots: "MoeSlots", y, to
 
 def moe_workspace_bytes(tokens, experts, top_k, hidden, inter) -> int:
     return lib().apex_moe_workspace_bytes(tokens, experts, top_k, hidden, inter)
+
+
+def moe_workspace_plan(workspace, tokens, experts, top_k, hidden, inter) -> dict:
+    """The grouping plan apex_moe_ffn_bf16 left in `workspace` (apex_moe_workspace_plan_offset):
+    counts, offsets, active experts and both pair <-> position maps, as numpy arrays."""
+    off = lib().apex_moe_workspace_plan_offset(tokens, experts, top_k, hidden, inter)
+    E, P = experts, tokens * top_k
+    words = workspace.numpy()[off:off + 4 * (16 + 3 * E + 1 + 2 * P)].view(np.int32)
+    hdr, rest = words[:16], words[16:]
+    cnt, rest = rest[:E], rest[E:]
+    offs, rest = rest[:E + 1], rest[E + 1:]
+    act, rest = rest[:E], rest[E:]
+    return {"active": int(hdr[0]), "cnt": cnt.copy(), "off": offs.copy(), "act": act[:hdr[0]].copy(),
+            "pos_of_pair": rest[:P].copy(), "pair_of_pos": rest[P:2 * P].copy()}
 
 
 def moe_ffn_bf16(x, logits, slots: MoeSlots, y, tokens, experts, top_k, hidden, inter, workspace,

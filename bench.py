@@ -386,9 +386,9 @@ def time_moe_prefill(steps, warmup):
             "roofline_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(flops),
             "workload": "MoE prefill: x bf16 [4096,2816], Zipf(1.1) routing over 128 experts "
                         "(8 empty), top-8, NVFP4 gate/up [704x2816], down [2816x704], y bf16",
-            "path": "route + per-workgroup expert masks, plan scan, position scatter, "
-                    "grouped MFMA GEMM gate/up with GeGLU epilogue, grouped MFMA GEMM down, "
-                    "weighted combine (6 launches)"}
+            "path": "route + per-block expert masks, column scan of the block counts, "
+                    "placing (plan + positions), grouped MFMA GEMM gate/up with GeGLU "
+                    "epilogue, grouped MFMA GEMM down, weighted combine (6 launches)"}
 
 
 def time_gemm_prefill(steps, warmup, M=2048, N=21504, K=5376):

@@ -102,7 +102,15 @@ int apex_hip_contents(apex_hip_backend *backend, apex_hip_buffer *buffer, void *
 int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
 
 /* Backend::run (backend.h:57-60, metal_backend.cpp:151-174): queue kernel `kernel`
- * with positional arguments.  Returns at once; kernels run in queue order.
+ * with positional arguments.  Returns once the kernels are queued; they run in queue
+ * order.  The dense ops that run as an MFMA GEMM at prefill token counts (matmul_nvfp4
+ * with a full grid, matmul_nvfp4_bf16, the geglu_nvfp4 kernels, gemm_nvfp4_bf16) use the
+ * device's GEMM scratch when their activations are fp32 (the bf16 hi / lo split) or
+ * their grid has few tiles (split-K partials).  A call needing more scratch than any
+ * before grows it: that call allocates device memory and waits for the scratch's
+ * earlier users, so it does not return at once and cannot run under graph capture.
+ * Keep the GEMV with apex_hip_set_gemm_min_tokens, or make one warm-up call at the
+ * largest shape first.
  * Kernels and argument lists (B = buffer, U = uint32 value, F = float value):
  *   matmul_nvfp4      B input f32 [T,K], B weights u32 [rows,K/8], B scales u8
  *                     [rows,K/16], B output f32 [T,w_rows], U hidden_dim K, U w_rows.
@@ -110,9 +118,10 @@ int apex_hip_release(apex_hip_backend *backend, apex_hip_buffer *buffer);
  *                     threadgroups.x * threads/32), as the reference launch
  *                     (src/ops.h:34-46, shaders/matmul.metal:14-18) implies.  A grid
  *                     covering every row (the reference's ceil(w_rows/8) x 256) runs
- *                     apex_nvfp4_matmul_f32: an MFMA GEMM at prefill token counts, a
- *                     GEMV below them; a grid covering fewer rows runs the GEMV on
- *                     those rows (output rows strided by w_rows).
+ *                     apex_nvfp4_matmul_f32: an MFMA GEMM at prefill token counts
+ *                     (on the GEMM scratch, see above), a GEMV below them; a grid
+ *                     covering fewer rows runs the GEMV on those rows (output rows
+ *                     strided by w_rows).
  *   geglu_f32         B gate, B up, B output, U count (in place allowed);
  *                     src/ops.h:48-55, shaders/geglu.metal:6-24.
  *   matmul_nvfp4_bf16 B input bf16 [T,K], B weights, B scales, B output bf16 [T,rows],
@@ -277,6 +286,8 @@ int apex_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int apex_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
 int apex_hip_memcpy_d2d(void *dst, const void *src, size_t bytes);
 int apex_hip_memset(void *dst, int value, size_t bytes);
+/* Free and total device memory of the current device (hipMemGetInfo). */
+int apex_hip_mem_info(size_t *free_bytes, size_t *total_bytes);
 int apex_hip_device_synchronize(void);
 int apex_hip_stream_create(void **out);
 int apex_hip_stream_destroy(void *stream);
@@ -379,6 +390,15 @@ int apex_experts_to_device(const char *path, uint64_t stride, uint64_t slot_byte
 size_t apex_moe_workspace_bytes(uint32_t tokens, uint32_t experts, uint32_t top_k, uint32_t hidden,
                                 uint32_t inter);
 
+/* No counterpart in the reference (for inspection and tests): byte offset, inside the
+ * workspace of apex_moe_ffn_bf16 for these sizes, of the grouping plan a call leaves
+ * there: int32 header[16] | cnt[E] | off[E + 1] | act[E] | pos_of_pair[P] |
+ * pair_of_pos[P], P = tokens * top_k, pair p = t * top_k + j.  Pairs are grouped by
+ * expert, experts ascending, each expert's tokens ascending; header[0] is the number of
+ * experts with pairs.  The rest of the workspace is internal. */
+size_t apex_moe_workspace_plan_offset(uint32_t tokens, uint32_t experts, uint32_t top_k,
+                                      uint32_t hidden, uint32_t inter);
+
 /* y[t] = sum_j w[t,j] * down_e(gelu_tanh(gate_e x_t) * up_e x_t), e = ids[t,j], for
  * x, y bf16 [tokens, hidden] and logits bf16 [tokens, experts].  Up to 32 tokens (and
  * 256 token-expert pairs, hidden <= 3072, inter <= 1024) run as grouped GEMVs, the
@@ -400,7 +420,9 @@ int apex_moe_ffn_bf16(const uint16_t *x, const uint16_t *logits, const apex_moe_
  * argument.  Limits: tokens <= 32, tokens * top_k <= 256, experts <= 256, hidden <= 3072,
  * inter <= 1024 (larger shapes return APEX_HIP_E_INVALID).  Results are identical to
  * apex_moe_ffn_bf16 on the same shapes.  Every call on one GPU shares that GPU's array:
- * calls that overlap on one GPU (different streams or threads) race. */
+ * callers must serialise their calls on one stream per GPU -- calls whose kernels
+ * overlap on one GPU (different streams) race.  A call made while another thread is
+ * still enqueuing one on the same GPU returns APEX_HIP_E_INVALID without launching. */
 int apex_moe_ffn_bf16_noalloc(const uint16_t *x, const uint16_t *logits,
                               const apex_moe_slots *slots, uint16_t *y, uint32_t tokens,
                               uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,

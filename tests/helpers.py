@@ -53,6 +53,49 @@ def count_outside(got, want, rel: float, abs_frac: float) -> int:
     return int(np.count_nonzero(np.abs(got - want) > rel * np.abs(want) + abs_frac * rms))
 
 
+# Per-element bound of a bf16 output: round to nearest even moves a value by at most
+# half a bf16 step, 2^-8 of its magnitude, so an output computed in fp32 and rounded once
+# lies within 2^-8 |want| of the fp32/fp64 oracle value plus the fp32 accumulation error.
+BF16_REL = 2.0 ** -8
+
+
+def outside_bf16(got, want, abs_frac: float = 1e-5) -> int:
+    """count_outside with the bf16 rounding bound: a single zeroed, doubled or misplaced
+    output whose magnitude is above abs_frac of the rms is counted.  1e-5 of the rms
+    covers the fp32 accumulation of the GEMVs (a few fp32 steps of a dot product) and
+    the fp32 cancellation in the oracle's 1 + tanh for strongly negative gates."""
+    max_excess(got, want)
+    return count_outside(got, want, BF16_REL, abs_frac)
+
+
+def max_excess(got, want) -> float:
+    """Largest |got - want| beyond 2^-8 |want|, in units of rms(want), printed so a run's
+    log shows how much of a bound's absolute term was used."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    rms = np.sqrt(np.mean(want * want))
+    ex = float(np.max(np.abs(got - want) - BF16_REL * np.abs(want)) / rms) if rms > 0 else 0.0
+    print(f"max excess over 2^-8|want|: {ex:.3g} of the rms", flush=True)
+    return ex
+
+
+def moe_outside(got, want_r, terms, abs_frac: float = 1e-2) -> int:
+    """Elements of a MoE FFN output farther from the composition with bf16-rounded
+    intermediates (`want_r`, from moe_ffn_full(..., bf16_intermediates=True,
+    with_abs=True)) than one bf16 step of the output and of every term,
+    2^-8 (|y| + sum_j |w_j d_j|), plus abs_frac of the output rms.  The abs_frac term
+    covers intermediates that round the other way after a different fp32 summation
+    order (one bf16 step of an h element moves y by far less than 1e-2 of the rms)."""
+    got = np.asarray(got, np.float64)
+    want_r = np.asarray(want_r, np.float64)
+    assert got.shape == want_r.shape and np.all(np.isfinite(got))
+    rms = np.sqrt(np.mean(want_r * want_r))
+    slack = np.abs(got - want_r) - (BF16_REL * (np.abs(want_r) + terms) + abs_frac * rms)
+    print(f"moe: max excess over one bf16 step of output and terms: {slack.max() / rms + abs_frac:.3g}"
+          " of the rms", flush=True)
+    return int(np.count_nonzero(slack > 0))
+
+
 def dequant_f64(codes, scales) -> np.ndarray:
     """The oracle's exact dequantisation (fp32, every value exact), as fp64 for a numpy
     contraction."""

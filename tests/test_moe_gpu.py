@@ -9,7 +9,7 @@ import pytest
 
 import oracle
 from apex_amd import hip, synth
-from tests.helpers import TOL_BF16, bf16, moe_ffn_full, rel_l2
+from tests.helpers import TOL_BF16, bf16, moe_ffn_full, moe_outside, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -73,6 +73,17 @@ def moe_ref(x, logits, slots, k, rows=None):
     return oracle.moe_ffn(slots, xf, ids, w)
 
 
+def check_moe(got, x, logits, slots, k, what=None):
+    """Rel L2 against the oracle's composition, and every element against the same
+    composition with h and d rounded to bf16 as both paths store them (moe_outside: one
+    bf16 step of the output and of every term plus 1e-2 of the rms), so one wrong,
+    doubled or misplaced output element fails."""
+    ids, w = oracle.moe_route(bf16(logits), k)
+    want_r, terms = moe_ffn_full(slots, bf16(x), ids, w, bf16_intermediates=True, with_abs=True)
+    assert moe_outside(got, want_r, terms) == 0, what
+    assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16, what
+
+
 def run_moe(x, logits, slots, k, path=0):
     hip.set_moe_path(path)
     return bf16(hip.moe_forward(x, logits, slots, top_k=k))
@@ -86,7 +97,7 @@ def test_moe_small(path):
     logits = synth.normal_bf16(rng, (T, E))
     slots = synth.expert_slots(rng, E, H, I)
     got = run_moe(x, logits, slots, k, path)
-    assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16
+    check_moe(got, x, logits, slots, k)
 
 
 @pytest.mark.parametrize("path", [1, 2])
@@ -98,7 +109,7 @@ def test_moe_odd_shapes(path):
         logits = synth.normal_bf16(rng, (T, E))
         slots = synth.expert_slots(rng, E, H, I)
         got = run_moe(x, logits, slots, k, path)
-        assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16, (T, E, H, I, k)
+        check_moe(got, x, logits, slots, k, (T, E, H, I, k))
 
 
 def test_moe_decode_gemv_variants():
@@ -115,17 +126,18 @@ def test_moe_decode_gemv_variants():
         logits = synth.normal_bf16(rng, (T, E))
         slots = synth.expert_slots(rng, E, H, I)
         got = run_moe(x, logits, slots, k, 1)
-        assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16, (T, E, H, I, k)
+        check_moe(got, x, logits, slots, k, (T, E, H, I, k))
 
 
 def test_moe_decode_full_size_both_paths():
-    """MoE decode: 16 tokens, hidden 2816, 128 experts, top-8, intermediate 704, seed 0."""
+    """MoE decode: 16 tokens, hidden 2816, 128 experts, top-8, intermediate 704, seed 0.
+    Both paths, every one of the 45,056 outputs against the composition with bf16
+    intermediates (check_moe), plus the rel L2 gate against the unrounded oracle."""
     x, logits, slots = synth.moe_decode_case(seed=0)
-    want = moe_ref(x, logits, slots, 8)
     got_gemv = run_moe(x, logits, slots, 8, 0)  # 16 tokens: the grouped-GEMV path
-    assert rel_l2(got_gemv, want) < TOL_BF16
+    check_moe(got_gemv, x, logits, slots, 8, "gemv")
     got_gemm = run_moe(x, logits, slots, 8, 2)
-    assert rel_l2(got_gemm, want) < TOL_BF16
+    check_moe(got_gemm, x, logits, slots, 8, "gemm")
     # deterministic: a second run is bit-identical
     assert np.array_equal(run_moe(x, logits, slots, 8, 0), got_gemv)
 
@@ -144,7 +156,7 @@ def test_moe_decode_hot_experts():
         lg[:, hot_e] += 20.0
         logits = synth.bf16_from_f32(lg)
         got = run_moe(x, logits, slots, kk, 1)
-        assert rel_l2(got, moe_ref(x, logits, slots, kk)) < TOL_BF16, (T, len(hot_e), kk)
+        check_moe(got, x, logits, slots, kk, (T, len(hot_e), kk))
         assert np.array_equal(run_moe(x, logits, slots, kk, 1), got)
 
 
@@ -159,7 +171,7 @@ def test_moe_hot_experts_span_many_tiles():
     logits = synth.bf16_from_f32(lg)
     slots = synth.expert_slots(rng, E, H, I)
     got = run_moe(x, logits, slots, k)
-    assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16
+    check_moe(got, x, logits, slots, k)
 
 
 def test_moe_tile_classes():
@@ -178,7 +190,7 @@ def test_moe_tile_classes():
     x = synth.normal_bf16(rng, (T, H))
     slots = synth.expert_slots(rng, E, H, I)
     got = run_moe(x, logits, slots, k)
-    assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16
+    check_moe(got, x, logits, slots, k)
 
 
 def test_moe_prefill_full_size():
@@ -204,6 +216,7 @@ def test_moe_prefill_full_size():
     print(f"moe prefill full: max |diff|/rms {np.abs(got - want_r).max() / rms:.4g}, "
           f"{outside} past the bound, worst by {slack.max() / rms:.4g} of the rms", flush=True)
     assert outside <= 1e-5 * got.size
+    assert moe_outside(got, want_r, terms) == 0
     assert np.abs(got - want_r).max() < 0.05 * rms
     want = moe_ffn_full(slots, bf16(x), ids, w)
     assert rel_l2(got, want) < TOL_BF16
@@ -255,4 +268,37 @@ def test_moe_random_shapes(path):
         slots = synth.expert_slots(rng, E, H, I)
         print(f"moe path {path} T={T} E={E} k={k} H={H} I={I}", flush=True)
         got = run_moe(x, logits, slots, k, path)
-        assert rel_l2(got, moe_ref(x, logits, slots, k)) < TOL_BF16, (T, E, k, H, I)
+        check_moe(got, x, logits, slots, k, (T, E, k, H, I))
+
+
+@pytest.mark.parametrize("T", [4096, 32768])
+def test_moe_prefill_plan_maps(T):
+    """The prefill grouping (per-block routing masks, a column scan of the block counts
+    over the blocks, then placing) at 4096 and 32,768 tokens, Zipf(1.1) routing with empty
+    experts: the plan the call leaves in its workspace puts the pairs in the order the
+    plan defines -- the stable sort of the pairs by routed expert (experts ascending,
+    each expert's tokens ascending) -- pos_of_pair is its inverse, and the counts,
+    offsets and active-expert list follow from the routed ids."""
+    rng = np.random.default_rng(T)
+    E, H, I, k = 128, 256, 128, 8
+    slots = synth.expert_slots(rng, E, H, I)
+    x = synth.normal_bf16(rng, (T, H))
+    logits = synth.zipf_logits(rng, T, E)
+    hip.set_moe_path(2)
+    ds = dev(slots.data)
+    y = hip.DeviceArray((T, H), np.uint16)
+    ws = hip.DeviceArray((hip.moe_workspace_bytes(T, E, k, H, I),), np.uint8)
+    hip.moe_ffn_bf16(dev(x), dev(logits), hip.moe_slots(ds, slots.stride, slots.offsets), y, T, E, k,
+                     H, I, ws)
+    hip.synchronize()
+    plan = hip.moe_workspace_plan(ws, T, E, k, H, I)
+    ids, _ = oracle.moe_route(bf16(logits), k)
+    order = np.argsort(ids.ravel(), kind="stable")
+    assert np.array_equal(plan["pair_of_pos"], order)
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    assert np.array_equal(plan["pos_of_pair"], inv)
+    cnt = np.bincount(ids.ravel(), minlength=E)
+    assert np.array_equal(plan["cnt"], cnt)
+    assert np.array_equal(plan["off"], np.concatenate([[0], np.cumsum(cnt)]))
+    assert np.array_equal(plan["act"], np.nonzero(cnt)[0])

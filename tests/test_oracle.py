@@ -528,3 +528,87 @@ def test_router_logits_byte_order_and_bias():
     qb1 = synth.bf16_from_f32(np.full((E, H // 64), 0.25, np.float32))
     lg = oracle.moe_router_logits(h, ones, q.view(np.uint32), qs0, qb1, 0.0)
     assert np.allclose(lg[0], np.full(E, xn5 * 0.25), rtol=1e-6)
+
+
+# ---- the per-element checkers of the GPU parity tests --------------------------------
+
+def _zero_and_swap(good, want, bound, rng, n=200):
+    """Zero one output, or swap two, n times each at random; return how many of each
+    changed the output by more than `bound` allows at the touched elements and assert
+    the checker caught every one of those."""
+    from tests.helpers import outside_bf16
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    zero_cases = swap_cases = 0
+    for i in rng.choice(want.size, n, replace=False):
+        bad = good.copy()
+        bad[i] = 0.0
+        if abs(want[i]) > 2 * bound(want[i], rms):
+            zero_cases += 1
+            assert outside_bf16(bad, want) == 1, i
+    for i, j in rng.choice(want.size, (n, 2)):
+        bad = good.copy()
+        bad[i], bad[j] = good[j], good[i]
+        if abs(float(want[i]) - float(want[j])) > 2 * (bound(want[i], rms) + bound(want[j], rms)):
+            swap_cases += 1
+            assert outside_bf16(bad, want) >= 1, (i, j)
+    return zero_cases, swap_cases
+
+
+def test_elementwise_checker_catches_one_wrong_output():
+    """outside_bf16 (the bound of the bf16 GEMV and decode GeGLU parity tests: half a
+    bf16 step plus 1e-5 of the rms) on the oracle's own outputs rounded to bf16 as a
+    correct kernel stores them: the 2048 x 2048 GEMV (seed 0) and the full-size decode
+    GeGLU (x [1,5376], gate/up [21504 x 5376], seed 0).  The bound holds; zeroing one
+    output, or swapping two, fails it for every one of 200 random choices whose change
+    is more than twice the bound's slack at the touched elements -- all of the GEMV's;
+    about two thirds of the GeGLU's, whose other third are gelu of strongly negative
+    gates, zero to within 1e-5 of the rms, where zeroing changes nothing measurable."""
+    from tests.helpers import BF16_REL, outside_bf16
+    bound = lambda v, rms: BF16_REL * abs(v) + 1e-5 * rms
+    rng = np.random.default_rng(0)
+    x, w = synth.gemv_case(seed=0)
+    want = oracle.matvec(w.codes, w.scales, synth.bf16_to_f32(x)).ravel()
+    good = synth.bf16_to_f32(synth.bf16_from_f32(want))
+    assert outside_bf16(good, want) == 0
+    zc, sc = _zero_and_swap(good, want, bound, rng)
+    assert zc >= 198 and sc >= 195, (zc, sc)
+    x, gate, up = synth.geglu_case(seed=0)
+    xf = synth.bf16_to_f32(x)
+    want = oracle.geglu(oracle.matvec(gate.codes, gate.scales, xf),
+                        oracle.matvec(up.codes, up.scales, xf)).ravel()
+    good = synth.bf16_to_f32(synth.bf16_from_f32(want))
+    assert outside_bf16(good, want) == 0
+    zc, sc = _zero_and_swap(good, want, bound, rng)
+    assert zc >= 110 and sc >= 150, (zc, sc)
+
+
+def test_moe_checker_catches_one_wrong_output():
+    """moe_outside (the MoE bound: one bf16 step of the output and of every term plus
+    1e-2 of the rms) on the oracle's 16-token MoE decode composition (seed 0) with h and
+    d rounded to bf16, the output rounded to bf16 as a correct kernel stores it: the bound
+    holds.  Zeroing any one output of magnitude above 5e-2 of the rms (most of them)
+    fails it, and so does swapping two outputs that differ by more than that."""
+    from tests.helpers import moe_ffn_full, moe_outside
+    x, logits, slots = synth.moe_decode_case(seed=0)
+    ids, w = oracle.moe_route(synth.bf16_to_f32(logits), 8)
+    want_r, terms = moe_ffn_full(slots, synth.bf16_to_f32(x), ids, w, bf16_intermediates=True,
+                                 with_abs=True)
+    good = synth.bf16_to_f32(synth.bf16_from_f32(want_r.astype(np.float32))).astype(np.float64)
+    assert moe_outside(good, want_r, terms) == 0
+    rms = float(np.sqrt(np.mean(want_r ** 2)))
+    rng = np.random.default_rng(1)
+    flat = want_r.ravel()
+    zero_cases = swap_cases = 0
+    for i in rng.choice(flat.size, 200, replace=False):
+        bad = good.copy().ravel()
+        bad[i] = 0.0
+        if abs(flat[i]) > 5e-2 * rms:
+            zero_cases += 1
+            assert moe_outside(bad.reshape(good.shape), want_r, terms) == 1, i
+    for i, j in rng.choice(flat.size, (200, 2)):
+        bad = good.copy().ravel()
+        bad[i], bad[j] = good.ravel()[j], good.ravel()[i]
+        if abs(flat[i] - flat[j]) > 1e-1 * rms:
+            swap_cases += 1
+            assert moe_outside(bad.reshape(good.shape), want_r, terms) >= 1, (i, j)
+    assert zero_cases >= 150 and swap_cases >= 150, (zero_cases, swap_cases)
