@@ -690,34 +690,50 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first, bool pub
 
 // Prefill grouping, deterministic and free of contended atomics, in three launches whose
 // work is linear in the tokens (O(T/16 * E) reads in all):
-// 1. moe_route_hist_kernel: each workgroup routes kRouteBlockTokens tokens and marks,
+// 1. moe_route_hist_kernel: each workgroup routes kRouteBlockTokens (16) tokens and marks,
 //    per expert, the bit of every one of its tokens that chose it (LDS atomicOr, whose
 //    result does not depend on order).  A pair's rank inside its workgroup's group is
 //    the popcount of its expert's mask below its token's bit; the mask's popcount is
 //    the workgroup's count for the expert -> hist[block][expert].
-// 2. moe_hist_scan_kernel: per expert, an exclusive scan of hist over the blocks (in
-//    place: hist[b][e] becomes the expert's pairs in blocks before b) and the expert's
-//    total into hist row nb.
-// 3. moe_place_kernel (one workgroup per routing block): plan_scan over the totals
-//    (published by workgroup 0) and pos = off[e] + hist[b][e] + rank for the block's
-//    pairs.
-// kRouteBlockTokens (moe.h) tokens per workgroup: one per wave of 1024 threads
+// 2. moe_hist_scan_kernel: per expert, an exclusive scan of hist over the blocks of each
+//    of kScanChunks chunks (in place: hist[b][e] becomes the expert's pairs in the
+//    chunk's blocks before b) and the chunks' totals into hist rows nb ...
+// 3. moe_place_kernel (one workgroup per routing block): the totals summed and scanned
+//    over the experts (plan_scan, published by workgroup 0) and pos = off[e] + (pairs in
+//    earlier chunks) + hist[b][e] + rank for the block's pairs.
+// kRouteBlockTokens (moe.h) tokens per workgroup of 16 waves, one per wave: a wave's
+// top-k rounds are a chain of dependent wave reductions, so more tokens per wave
+// lengthen the workgroup (4 per wave: 15.2 against 7.2 us at 4096 tokens).
+constexpr uint32_t kRouteWaves = 16;
+constexpr uint32_t kRouteTokensPerWave = kRouteBlockTokens / kRouteWaves;
+static_assert(kRouteBlockTokens <= 64, "a block's tokens are bits of one 64-bit mask");
 
-__global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
+__global__ __launch_bounds__(64 * kRouteWaves) void moe_route_hist_kernel(MoeArgs a) {
     __shared__ unsigned long long mask[kMoeMaxExperts];
     __shared__ int32_t s_id[kRouteBlockTokens * kMoeMaxTopK];
     const uint32_t E = a.E, k = a.k;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t t0 = blockIdx.x * kRouteBlockTokens;
     const uint32_t nt = a.T - t0 < kRouteBlockTokens ? a.T - t0 : kRouteBlockTokens;
+    TokenLogits pre[kRouteTokensPerWave];
+#pragma unroll
+    for (uint32_t i = 0; i < kRouteTokensPerWave; ++i) {
+        const uint32_t tl = wave + kRouteWaves * i;
+        if (tl < nt)
+            pre[i] = load_token_logits(a, t0 + tl, lane);
+    }
     for (uint32_t e = threadIdx.x; e < kMoeMaxExperts; e += blockDim.x)
         mask[e] = 0;
     __syncthreads();
-    for (uint32_t tl = wave; tl < nt; tl += blockDim.x / 64) {
+#pragma unroll
+    for (uint32_t i = 0; i < kRouteTokensPerWave; ++i) {
+        const uint32_t tl = wave + kRouteWaves * i;
+        if (tl >= nt)
+            break;
         const uint32_t t = t0 + tl;
         int32_t id;
         float wt;
-        route_token_args(a, t, lane, id, wt);
+        route_token_loaded(a, pre[i], lane, id, wt);
         if ((uint32_t)lane < k) {
             a.ids[(size_t)t * k + lane] = id;
             a.w[(size_t)t * k + lane] = wt;
@@ -735,66 +751,86 @@ __global__ __launch_bounds__(1024) void moe_route_hist_kernel(MoeArgs a) {
         a.hist[(size_t)blockIdx.x * E + e] = __popcll(mask[e]);
 }
 
-// Column scan of hist: workgroup g owns experts [64 g, 64 g + 64), one per lane; wave w
-// owns blocks [w per, (w + 1) per).  Pass 1 sums each thread's blocks; the waves' sums
-// are scanned through LDS; pass 2 rewrites each thread's blocks with their exclusive
-// prefixes.  Each hist entry is read twice and written once.
-constexpr uint32_t kHistScanWaves = 16;
+// Column scan of hist in kScanChunks chunks of blocks, one workgroup per (64 experts,
+// chunk): lane l owns expert 64 g + l, wave w a quarter of the chunk's blocks.  Pass 1
+// sums each thread's blocks; the waves' sums are scanned through LDS; pass 2 rewrites
+// each block's count with the expert's pairs in the chunk's blocks before it.  The
+// chunk's totals go to hist row nb + chunk.  Each entry is read twice and written once,
+// and every workgroup walks at most ceil(nb / kScanChunks / 4) blocks per thread.
+constexpr uint32_t kScanWaves = 4;
 
-__global__ __launch_bounds__(64 * kHistScanWaves) void moe_hist_scan_kernel(MoeArgs a) {
-    __shared__ int s_sum[kHistScanWaves][64];
+__global__ __launch_bounds__(64 * kScanWaves) void moe_hist_scan_kernel(MoeArgs a) {
+    __shared__ int s_sum[kScanWaves][64];
     const uint32_t E = a.E;
     const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t e = blockIdx.x * 64 + lane;
-    const uint32_t per = (nb + kHistScanWaves - 1) / kHistScanWaves;
-    const uint32_t b0 = min(wave * per, nb), b1 = min(b0 + per, nb);
+    const uint32_t e = blockIdx.x * 64 + lane, c = blockIdx.y;
+    const uint32_t bpc = (nb + kScanChunks - 1) / kScanChunks;
+    const uint32_t spw = (bpc + kScanWaves - 1) / kScanWaves;
+    const uint32_t c0 = min(c * bpc, nb), c1 = min(c0 + bpc, nb);
+    const uint32_t b0 = min(c0 + wave * spw, c1), b1 = min(b0 + spw, c1);
     int32_t *col = a.hist + e;
     const bool mine = e < E;
     int sum = 0;
     for (uint32_t b = b0; b < b1; b += 8) {
-        int c[8];
+        int v[8];
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i)
-            c[i] = mine && b + i < b1 ? col[(size_t)(b + i) * E] : 0;
+            v[i] = mine && b + i < b1 ? col[(size_t)(b + i) * E] : 0;
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i)
-            sum += c[i];
+            sum += v[i];
     }
     s_sum[wave][lane] = sum;
     __syncthreads();
     int run = 0, total = 0;
 #pragma unroll
-    for (int w = 0; w < (int)kHistScanWaves; ++w) {
+    for (int w = 0; w < (int)kScanWaves; ++w) {
         const int v = s_sum[w][lane];
         run += w < wave ? v : 0;
         total += v;
     }
     if (mine && wave == 0)
-        col[(size_t)nb * E] = total;
+        col[(size_t)(nb + c) * E] = total;
     for (uint32_t b = b0; b < b1; b += 8) {
-        int c[8];
+        int v[8];
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i)
-            c[i] = mine && b + i < b1 ? col[(size_t)(b + i) * E] : 0;
+            v[i] = mine && b + i < b1 ? col[(size_t)(b + i) * E] : 0;
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) {
             if (mine && b + i < b1)
                 col[(size_t)(b + i) * E] = run;
-            run += c[i];
+            run += v[i];
         }
     }
 }
 
-// One workgroup per routing block b: the per-expert totals (hist row nb) scanned over
-// the experts (plan_scan; workgroup 0 publishes the plan), then the block's pairs:
-// pos = off[e] + hist[b][e] (pairs of e in the blocks before b) + rank.
+// One workgroup per routing block b of chunk c: the per-expert totals (the sums of the
+// chunk totals, hist rows nb ..) scanned over the experts (plan_scan; workgroup 0
+// publishes the plan), then the block's pairs: pos = off[e] + (pairs of e in the chunks
+// before c) + hist[b][e] (pairs of e in c's blocks before b) + rank.
 __global__ __launch_bounds__(256) void moe_place_kernel(MoeArgs a) {
-    __shared__ int cnt[kMoeMaxExperts], first[kMoeMaxExperts];
+    __shared__ int cnt[kMoeMaxExperts], first[kMoeMaxExperts], before[kMoeMaxExperts];
     const uint32_t E = a.E, k = a.k, b = blockIdx.x;
     const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
-    for (uint32_t e = threadIdx.x; e < kMoeMaxExperts; e += blockDim.x)
-        cnt[e] = e < E ? a.hist[(size_t)nb * E + e] : 0;
+    const uint32_t c = b / ((nb + kScanChunks - 1) / kScanChunks);
+    for (uint32_t e = threadIdx.x; e < kMoeMaxExperts; e += blockDim.x) {
+        int tot = 0, pre = 0;
+        if (e < E) {
+            int v[kScanChunks];
+#pragma unroll
+            for (uint32_t q = 0; q < kScanChunks; ++q)
+                v[q] = a.hist[(size_t)(nb + q) * E + e];
+#pragma unroll
+            for (uint32_t q = 0; q < kScanChunks; ++q) {
+                pre += q < c ? v[q] : 0;
+                tot += v[q];
+            }
+        }
+        cnt[e] = tot;
+        before[e] = pre;
+    }
     __syncthreads();
     plan_scan(a, cnt, first, b == 0);
     const uint32_t P = a.T * k;
@@ -805,7 +841,7 @@ __global__ __launch_bounds__(256) void moe_place_kernel(MoeArgs a) {
     for (uint32_t i = threadIdx.x; i < np; i += blockDim.x) {
         const uint32_t p = p0 + i;
         const int ex = a.ids[p];
-        const int pos = first[ex] + pre[ex] + a.rank[p];
+        const int pos = first[ex] + before[ex] + pre[ex] + a.rank[p];
         v.pos_of_pair[p] = pos;
         v.pair_of_pos[pos] = (int32_t)p;
     }
@@ -2417,8 +2453,9 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     if (err != hipSuccess)
         return err;
     const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
-    hipLaunchKernelGGL(moe_route_hist_kernel, dim3(nb), dim3(64 * kRouteBlockTokens), 0, stream, a);
-    hipLaunchKernelGGL(moe_hist_scan_kernel, dim3((a.E + 63) / 64), dim3(64 * kHistScanWaves), 0, stream, a);
+    hipLaunchKernelGGL(moe_route_hist_kernel, dim3(nb), dim3(64 * kRouteWaves), 0, stream, a);
+    hipLaunchKernelGGL(moe_hist_scan_kernel, dim3((a.E + 63) / 64, kScanChunks), dim3(64 * kScanWaves), 0,
+                       stream, a);
     hipLaunchKernelGGL(moe_place_kernel, dim3(nb), dim3(256), 0, stream, a);
     const uint32_t mt8 = 8 * ((a.max_tiles + 7) / 8); // m-tiles rounded to whole XCD turns
     const uint32_t nn_gu = (a.I + kGateUpCols - 1) / kGateUpCols;
