@@ -31,10 +31,34 @@ hipError_t gemm_launch(const GemmArgs &a, hipStream_t stream);
 // How gemm_launch covers C on ncu CUs: whole tiles (256 x 256; GeGLU 256 rows x 128 h
 // columns) for the first nf n-tiles, narrow tiles of nt (1 or 2) 32-row W blocks for
 // the columns past them; nt = 0: whole tiles only (nf = all n-tiles).
+// Tail plan of a grid whose whole tiles leave the last round of CUs partly empty: whole
+// tiles cover n-tiles [0, nf); the columns past them run either as narrow tiles of nt
+// 32-row W blocks (nt > 0) or as ns short tiles (ns > 0): each a contiguous range of at
+// most 8 32-row blocks of one tail n-tile column, full width, one per CU of the last
+// round.  nt = ns = 0: whole tiles only.
 struct GemmTailPlan {
-    uint32_t nf, nt;
+    uint32_t nf, nt, ns;
 };
 GemmTailPlan gemm_tail_plan(uint32_t M, uint32_t N, bool geglu, uint32_t ncu);
+
+// Short tile v of ns over C tail columns of B 32-row blocks: column c (r_c = ns / C
+// workgroups, one more for the first ns % C columns) and its i-th of r_c contiguous block
+// ranges (B / r_c blocks, one more for the first B % r_c ranges).
+struct ShortTile {
+    uint32_t col, block0, blocks;
+};
+__host__ __device__ inline ShortTile short_tile(uint32_t v, uint32_t ns, uint32_t C, uint32_t B) {
+    const uint32_t q = ns / C, rem = ns % C;
+    uint32_t c, i, r;
+    if (v < (q + 1) * rem) {
+        c = v / (q + 1), i = v % (q + 1), r = q + 1;
+    } else {
+        const uint32_t u = v - (q + 1) * rem;
+        c = rem + u / q, i = u % q, r = q;
+    }
+    const uint32_t base = B / r, extra = B % r;
+    return ShortTile{c, i * base + (i < extra ? i : extra), base + (i < extra ? 1u : 0u)};
+}
 
 // Split-K form for grids of few tiles: S workgroups per tile each run a contiguous
 // range of K stages (for a_k = 2K none crosses from the hi half to the lo half) and

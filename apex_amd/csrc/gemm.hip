@@ -91,15 +91,32 @@ __device__ __forceinline__ void gemm_one_tile(const GemmArgs &a, uint8_t *lds, u
 // each (3 and 5 measured the same).
 constexpr int kNarrowVpm = 8;
 constexpr uint32_t kNarrowMaxBlocks = 2; // widest narrow tile (32-row W blocks)
+constexpr uint32_t kShortMaxBlocks = 6;  // tallest short tile worth running (32-row blocks)
 
 // Workgroups [0, G_full): the 256 x 256 tiles of n-tiles [0, nf), XCD-aware (workgroup g
 // on tile (g % 8) * per_xcd + g / 8, tiles M-fastest: the tiles resident on one XCD
-// share A row blocks and W column blocks in its L2).  Workgroups past G_full: the
-// narrow tiles (nt = 1 or 2 W blocks each; GeGLU 2: one gate and one up block) of the
-// columns past nf n-tiles, dealt the same way; they fill the CUs of the last round,
-// which whole tiles would leave partly empty.
+// share A row blocks and W column blocks in its L2).  Workgroups past G_full: the tail
+// columns past nf n-tiles, either as narrow tiles (nt = 1 or 2 W blocks each; GeGLU 2:
+// one gate and one up block) or as ns short tiles (full-width 1 x 4 tiles of at most
+// kShortMaxBlocks 32-row blocks of one column, short_tile), dealt the same way; they fill the CUs of
+// the last round, which whole tiles would leave partly empty.
 template <bool GEGLU, bool F32>
-__global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a, uint32_t nf, uint32_t nt) {
+__device__ __forceinline__ void short_gemm_tile(const GemmArgs &a, uint8_t *lds, uint32_t blocks,
+                                                uint32_t m0, uint32_t n0) {
+    static_assert(kShortMaxBlocks == 6, "one case per short tile height");
+    switch (blocks) {
+    case 6: gemm_one_tile<GEGLU, F32, 6, WC, 2, 3>(a, lds, m0, n0); break;
+    case 5: gemm_one_tile<GEGLU, F32, 5, WC, 2, 3>(a, lds, m0, n0); break;
+    case 4: gemm_one_tile<GEGLU, F32, 4, WC, 2, 3>(a, lds, m0, n0); break;
+    case 3: gemm_one_tile<GEGLU, F32, 3, WC, 2, 3>(a, lds, m0, n0); break;
+    case 2: gemm_one_tile<GEGLU, F32, 2, WC, 2, 3>(a, lds, m0, n0); break;
+    default: gemm_one_tile<GEGLU, F32, 1, WC, 2, 3>(a, lds, m0, n0); break;
+    }
+}
+
+template <bool GEGLU, bool F32>
+__global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a, uint32_t nf, uint32_t nt,
+                                                              uint32_t ns) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr uint32_t TN = GEGLU ? kGegluCols : BN;
     const uint32_t tiles_m = (a.M + BM - 1) / BM;
@@ -113,11 +130,22 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a, uint32
         gemm_one_tile<GEGLU, F32, MT, WC, 8 / WC, 3>(a, lds, (t % tiles_m) * BM, (t / tiles_m) * TN);
         return;
     }
-    const uint32_t tc = GEGLU ? 16 * nt : 32 * nt; // output columns of a narrow tile
     const uint32_t c_tail = nf * TN;
+    const uint32_t u = blockIdx.x - g_full;
+    if (ns) {
+        // consecutive short tiles (mostly of one column) on one XCD: they share W in its L2
+        const uint32_t per_xcd = (ns + 7) / 8;
+        const uint32_t v = (u % 8) * per_xcd + u / 8;
+        if (v >= ns)
+            return;
+        const uint32_t C = (a.N - c_tail + TN - 1) / TN, B = (a.M + 31) / 32;
+        const ShortTile st = short_tile(v, ns, C, B);
+        short_gemm_tile<GEGLU, F32>(a, lds, st.blocks, 32 * st.block0, c_tail + st.col * TN);
+        return;
+    }
+    const uint32_t tc = GEGLU ? 16 * nt : 32 * nt; // output columns of a narrow tile
     const uint32_t tiles = tiles_m * ((a.N - c_tail + tc - 1) / tc);
     const uint32_t per_xcd = (tiles + 7) / 8;
-    const uint32_t u = blockIdx.x - g_full;
     const uint32_t t = (u % 8) * per_xcd + u / 8;
     if (t >= tiles)
         return;
@@ -135,13 +163,16 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a, uint32
 // (GeGLU: 2).  The narrow tiles are decode-bound (each wave decodes every W element of
 // the tile for its 64 rows): measured at 2048 x 21504 x 5376, a round of 2-block tiles
 // took 0.73 of a whole-tile round (the GeGLU GEMM 835 -> 795 us), a round of 5-block
-// tiles 1.16 (404 -> 426 us), so wider narrow tiles are not used.  nt = 0: whole
-// tiles only.
+// tiles 1.16 (404 -> 426 us), so wider narrow tiles are not used.  Where no narrow
+// width fits, short tiles (full width, contiguous 32-row block ranges of one tail
+// column, at most kShortMaxBlocks blocks) take the last round's CUs, one each: at
+// 2048 x 21504 x 5376 (20 tail columns of 64 blocks on 256 CUs, 5-6 blocks each) 407 ->
+// 403 us.  nt = ns = 0: whole tiles only.
 GemmTailPlan plan_tail(uint32_t M, uint32_t N, bool geglu, uint32_t ncu) {
     const uint32_t tn = geglu ? kGegluCols : BN;
     const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + tn - 1) / tn;
     const uint64_t tiles = (uint64_t)tiles_m * tiles_n;
-    GemmTailPlan p{tiles_n, 0};
+    GemmTailPlan p{tiles_n, 0, 0};
     if (ncu == 0 || tiles <= ncu || tiles % ncu == 0)
         return p;
     const uint64_t R = tiles / ncu;
@@ -153,7 +184,15 @@ GemmTailPlan plan_tail(uint32_t M, uint32_t N, bool geglu, uint32_t ncu) {
     for (uint32_t nt = geglu ? 2 : 1; nt <= kNarrowMaxBlocks; ++nt) {
         const uint64_t tc = geglu ? 16 * nt : 32 * nt;
         if (tiles_m * ((cols + tc - 1) / tc) <= slots)
-            return GemmTailPlan{nf, nt};
+            return GemmTailPlan{nf, nt, 0};
+    }
+    // Short tiles: the tail columns' 32-row blocks dealt over the last round's CUs; worth
+    // it when no tile needs more than kShortMaxBlocks blocks (a whole tile has 8).
+    const uint64_t C = (cols + tn - 1) / tn, B = (M + 31) / 32;
+    if (slots >= C && slots <= 0xFFFFFFFFull) {
+        const uint64_t q = slots / C;
+        if ((B + q - 1) / q <= kShortMaxBlocks) // at most C * B tiles: none empty
+            return GemmTailPlan{nf, 0, (uint32_t)std::min(slots, C * B)};
     }
     return p;
 }
@@ -166,13 +205,15 @@ template <bool GEGLU, bool F32> hipError_t launch_kernel(const GemmArgs &a, hipS
         const uint32_t tc = GEGLU ? 16 * p.nt : 32 * p.nt;
         const uint32_t c_tail = p.nf * (GEGLU ? kGegluCols : BN);
         grid += 8 * ((tiles_m * ((a.N - c_tail + tc - 1) / tc) + 7) / 8);
+    } else if (p.ns) {
+        grid += 8 * ((p.ns + 7) / 8);
     }
     constexpr size_t lds = Layout<MT, WC>::kLds;
     static std::atomic<uint64_t> attr_set{0};
     if (hipError_t e = allow_dynamic_lds(nvfp4_gemm_kernel<GEGLU, F32>, lds, attr_set); e != hipSuccess)
         return e;
     hipLaunchKernelGGL((nvfp4_gemm_kernel<GEGLU, F32>), dim3(grid), dim3(kThreads), lds, stream, a,
-                       p.nf, p.nt);
+                       p.nf, p.nt, p.ns);
     return hipGetLastError();
 }
 

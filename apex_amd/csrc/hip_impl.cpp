@@ -1246,7 +1246,7 @@ int apex_hip_dense_dispatch_counts(uint64_t counts[4]) {
     });
 }
 
-int apex_hip_gemm_tail_plan(uint32_t m, uint32_t n, int geglu, uint32_t ncu, uint32_t out[2]) {
+int apex_hip_gemm_tail_plan(uint32_t m, uint32_t n, int geglu, uint32_t ncu, uint32_t out[3]) {
     return guard([&] {
         require(out != nullptr, "out is null");
         require(m > 0 && n > 0, "empty product");
@@ -1257,6 +1257,7 @@ int apex_hip_gemm_tail_plan(uint32_t m, uint32_t n, int geglu, uint32_t ncu, uin
         const apex_hip::GemmTailPlan p = apex_hip::gemm_tail_plan(m, n, geglu != 0, ncu);
         out[0] = p.nf;
         out[1] = p.nt;
+        out[2] = p.ns;
     });
 }
 

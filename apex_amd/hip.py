@@ -355,11 +355,12 @@ def dense_dispatch_counts() -> dict:
 
 
 def gemm_tail_plan(m: int, n: int, geglu: bool = False, ncu: int = 0) -> tuple:
-    """(whole n-tiles, narrow-tile W blocks) of the MFMA GEMM's cover of an m x n
-    output on ncu CUs (0: the current device's); narrow 0: whole tiles only."""
-    out = (C.c_uint32 * 2)()
+    """(whole n-tiles, narrow-tile W blocks, short tiles) of the MFMA GEMM's cover of an
+    m x n output on ncu CUs (0: the current device's); narrow and short 0: whole tiles
+    only."""
+    out = (C.c_uint32 * 3)()
     check(lib().apex_hip_gemm_tail_plan(m, n, int(geglu), ncu, C.cast(out, C.c_void_p)))
-    return out[0], out[1]
+    return out[0], out[1], out[2]
 
 
 # ---- MoE expert FFN --------------------------------------------------------------

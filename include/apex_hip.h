@@ -325,9 +325,11 @@ int apex_hip_dense_dispatch_counts(uint64_t counts[4]);
 
 /* How the MFMA GEMM covers an M x N output (N: output columns; GeGLU: h columns) on
  * `ncu` CUs (0: the current device's): out[0] = n-tiles of whole tiles (256 x 256, GeGLU
- * 256 x 128 h columns), out[1] = W blocks (32 rows) of the narrow tiles that cover the
- * columns past them and fill the last round's CUs (0: whole tiles only).  No launch. */
-int apex_hip_gemm_tail_plan(uint32_t m, uint32_t n, int geglu, uint32_t ncu, uint32_t out[2]);
+ * 256 x 128 h columns); the columns past them fill the last round's CUs either as
+ * narrow tiles of out[1] W blocks (32 rows) each or as out[2] short tiles (full width,
+ * at most 6 32-row blocks of one column each); out[1] = out[2] = 0: whole tiles only.
+ * No launch. */
+int apex_hip_gemm_tail_plan(uint32_t m, uint32_t n, int geglu, uint32_t ncu, uint32_t out[3]);
 
 /* ---- MoE expert FFN (no reference kernel) ------------------------------------------
  * Semantics: tools/dump_reference.py:208-219 (router top-k, experts combined with the

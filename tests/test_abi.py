@@ -198,37 +198,47 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
 
 def test_gemm_tail_plan_covers_and_fits():
     """The MFMA GEMM's cover of C on 256 CUs (host logic, no device): whole tiles for the
-    first nf n-tiles, narrow tiles of nt (1 or 2; GeGLU 2) 32-row W blocks past them.
+    first nf n-tiles; past them either narrow tiles of nt (1 or 2; GeGLU 2) 32-row W
+    blocks or ns short tiles (full width, at most 6 32-row blocks of one tail column).
     Whenever narrow tiles are used they cover every column, fit in the CUs left by the
-    whole tiles' rounds plus one, and no narrower width would fit; the benchmark's GeGLU
-    shape takes 2 blocks, its plain shape (5 needed) whole tiles only."""
+    whole tiles' rounds plus one, and no narrower width would fit; short tiles only when
+    no narrow width fits, one per CU left, none empty.  The benchmark's GeGLU shape takes
+    2-block narrow tiles, its plain shape short tiles."""
     ncu = 256
-    assert hip.gemm_tail_plan(2048, 21504, False, ncu) == (84, 0)
-    assert hip.gemm_tail_plan(2048, 21504, True, ncu) == (160, 2)
-    assert hip.gemm_tail_plan(256, 76800, False, ncu) == (256, 2)
-    assert hip.gemm_tail_plan(2048, 16384, False, ncu) == (64, 0)  # exactly 2 rounds
-    assert hip.gemm_tail_plan(256, 256 * 200, False, ncu) == (200, 0)  # one round
+    assert hip.gemm_tail_plan(2048, 21504, False, ncu) == (64, 0, 256)
+    assert hip.gemm_tail_plan(2048, 21504, True, ncu) == (160, 2, 0)
+    assert hip.gemm_tail_plan(256, 76800, False, ncu) == (256, 2, 0)
+    assert hip.gemm_tail_plan(2048, 16384, False, ncu) == (64, 0, 0)  # exactly 2 rounds
+    assert hip.gemm_tail_plan(256, 256 * 200, False, ncu) == (200, 0, 0)  # one round
+    assert hip.gemm_tail_plan(30, 102187, False, ncu) == (256, 0, 144)  # one block per tail column
     rng = __import__("numpy").random.default_rng(5)
-    used = 0
+    used = short = 0
     for _ in range(400):
         M, N = int(rng.integers(1, 5000)), int(rng.integers(1, 200000))
         for geglu in (False, True):
             tn = 128 if geglu else 256
             tm, tiles_n = -(-M // 256), -(-N // tn)
-            nf, nt = hip.gemm_tail_plan(M, N, geglu, ncu)
-            if nt == 0:
+            nf, nt, ns = hip.gemm_tail_plan(M, N, geglu, ncu)
+            if nt == 0 and ns == 0:
                 assert nf == tiles_n
                 continue
-            used += 1
-            assert 0 < nf < tiles_n and (nt == 2 if geglu else 1 <= nt <= 2)
+            assert nt == 0 or ns == 0
             R = tm * tiles_n // ncu
             slots = (R + 1) * ncu - tm * nf
-            assert tm * nf <= R * ncu
+            assert 0 < nf < tiles_n and tm * nf <= R * ncu
+            if ns:
+                short += 1
+                C, B = -(-(N - nf * tn) // tn), -(-M // 32)
+                assert C <= ns <= min(slots, C * B)
+                assert -(-B // (ns // C)) <= 6
+                continue
+            used += 1
+            assert nt == 2 if geglu else 1 <= nt <= 2
             tc = (16 if geglu else 32) * nt
             assert tm * -(-(N - nf * tn) // tc) <= slots
             if nt > (2 if geglu else 1):
                 tc1 = (16 if geglu else 32) * (nt - (2 if geglu else 1))
                 assert tm * -(-(N - nf * tn) // tc1) > slots
-    assert used > 20
+    assert used > 20 and short > 20
     with pytest.raises(hip.ApexHipError):
         hip.gemm_tail_plan(0, 5, False, ncu)

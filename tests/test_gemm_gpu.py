@@ -89,7 +89,7 @@ def test_geglu_prefill_full_size():
     want = oracle.geglu(gate, up)
     assert count_outside(got, want, 2.0 ** -7, 2e-3) == 0
     assert rel_l2(got, want) < TOL_BF16
-    nf, nt = hip.gemm_tail_plan(2048, g.rows, True)
+    nf, nt, _ = hip.gemm_tail_plan(2048, g.rows, True)
     assert nt == 0 or rel_l2(got[:, nf * 128:], want[:, nf * 128:]) < TOL_BF16
 
 
@@ -149,6 +149,52 @@ def test_gemm_narrow_tail_tiles_exact(M, N, nt):
         X = rng.standard_normal((M, K), dtype=np.float32)
         got = run_matmul_f32(X, w)
         assert rel_l2(got[:, ni], oracle.matvec_rows(w.codes, w.scales, X, ni)) < TOL_REF_GATE
+
+
+# (M, N, GeGLU): the columns past the whole tiles' rounds run as short tiles (full
+# width, 1 to 6 32-row blocks of one tail column each, one per CU of the last round);
+# ragged M and N
+SHORT = [(2048, 21504, False), (2000, 21404, False), (1300, 30000, False), (30, 102187, False),
+         (1024, 21504, True), (1300, 30000, True)]
+
+
+@pytest.mark.parametrize("M,N,geglu", SHORT)
+def test_gemm_short_tail_tiles_exact(M, N, geglu, gemm_threshold):
+    """Short tail tiles: plain GEMM with one-hot rows (every output one weight,
+    bit-exact), then random rows against the oracle on the tail columns and a sample of
+    the rest, bf16 and fp32 (hi + lo split A) out; GeGLU bf16 and fp32 out against the
+    oracle's GeGLU on every column."""
+    nf, nt, ns = hip.gemm_tail_plan(M, N, geglu, 256)
+    tiles_m = (M + 255) // 256
+    assert nt == 0 and 0 < ns <= 256 + tiles_m  # the CUs left in the last round
+    assert hip.gemm_tail_plan(M, N, geglu)[2] > 0  # this device takes short tiles too
+    rng = np.random.default_rng(M + N)
+    K = 64 if geglu else 128
+    if geglu:
+        g, u = synth.nvfp4_weights(rng, N, K), synth.nvfp4_weights(rng, N, K)
+        x = synth.normal_bf16(rng, (M, K))
+        xf = bf16(x)
+        want = oracle.geglu(oracle.matvec(g.codes, g.scales, xf), oracle.matvec(u.codes, u.scales, xf))
+        got = run_geglu(x, g, u, False)
+        assert count_outside(got, want, 2.0 ** -7, 2e-3) == 0
+        assert rel_l2(got, want) < TOL_BF16
+        assert rel_l2(run_geglu(xf, g, u, True), want) < TOL_REF_GATE
+        return
+    w = synth.nvfp4_weights(rng, N, K)
+    perm = rng.integers(0, K, size=M)
+    A = np.zeros((M, K), np.float32)
+    A[np.arange(M), perm] = 1.0
+    got = bf16(gemm(synth.bf16_from_f32(A), w))
+    want = oracle.decode(w.codes, w.scales)[:, perm].T + np.float32(0.0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    A = synth.normal_bf16(rng, (M, K))
+    C = bf16(gemm(A, w))
+    ni = np.concatenate([np.sort(rng.choice(nf * 256, 512, replace=False)), np.arange(nf * 256, N)])
+    want = oracle.matvec_rows(w.codes, w.scales, bf16(A), ni)
+    assert count_outside(C[:, ni], want, 2.0 ** -7, 2e-3) == 0
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    got = run_matmul_f32(X, w)
+    assert rel_l2(got[:, ni], oracle.matvec_rows(w.codes, w.scales, X, ni)) < TOL_REF_GATE
 
 
 @pytest.mark.parametrize("T,N,nt", [(256, 38400, 2), (300, 20000, 2), (520, 13000, 2)])
