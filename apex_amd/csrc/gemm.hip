@@ -69,8 +69,10 @@ __device__ __forceinline__ void gemm_one_tile(const GemmArgs &a, uint8_t *lds, u
     auto w_code = [=](int r) { return w_ok(r) ? w_row(r) * (K / 2) : kOut; };
     auto w_scale = [=](int r) { return w_ok(r) ? w_row(r) * (K / 16) : kOut; };
 
+    // bf16 A: chunked W loads; fp32 [hi | lo] A meets W twice, wrapping at K, which a
+    // 2-stage code chunk may straddle: per-stage W there
     Acc<MTW, WCW, NTW> acc;
-    gemm_tile<MTW, WCW, NTW, VPM>(lds, ra, rc, rs, ak, a_row, w_code, w_scale, acc, K);
+    gemm_tile<MTW, WCW, NTW, VPM, F32 ? 4 : 0>(lds, ra, rc, rs, ak, a_row, w_code, w_scale, acc, K);
 
     const bool wide = uniform_wide<GEGLU, F32>(a);
     if constexpr (GEGLU) {
@@ -208,7 +210,7 @@ template <bool GEGLU, bool F32> hipError_t launch_kernel(const GemmArgs &a, hipS
     } else if (p.ns) {
         grid += 8 * ((p.ns + 7) / 8);
     }
-    constexpr size_t lds = Layout<MT, WC>::kLds;
+    constexpr size_t lds = kMaxLds;
     static std::atomic<uint64_t> attr_set{0};
     if (hipError_t e = allow_dynamic_lds(nvfp4_gemm_kernel<GEGLU, F32>, lds, attr_set); e != hipSuccess)
         return e;

@@ -31,11 +31,22 @@
 //    lanes reading one piece of 32 consecutive rows spread over all banks.
 //  * W's packed codes (32 bytes per row per stage) and scales (4 bytes; tile row r at
 //    entry 128 ((r / 32) % 2) + 32 (r / 64) + r % 32, so every 64-entry DMA load reads
-//    one matrix) ride the same ring with the same DMA loads; each wave reads its B
-//    fragments' code words from
-//    LDS and dequantises them in registers right before its MFMAs
-//    (cvt_scalef32_pk_f32_fp4, x E4M3 scale, keep the exact high halves as bf16).
-//    The packed form keeps W's LDS traffic 4x smaller than a bf16 copy.
+//    one matrix) stream through LDS buffers of their own, one stage ahead of A: stage
+//    s+1's codes and scales are in LDS while stage s runs, so a wave reads them and
+//    decodes the scales during steps 1 and 2 of stage s, and the step after the
+//    barrier carries only the DMA issue, the next stage's first A fragments and its
+//    first dequantisation (with the W reads and the scale decode there too, that step
+//    overflowed its MFMAs' issue slots).  W's load cost follows the cache lines a DMA
+//    instruction touches more than its bytes: per stage a row's codes are 32 bytes and
+//    its scales 4, one line each.  Chunked (WS = 0, bf16 A): codes arrive two stages
+//    per load (64 bytes of a row, 16 rows per instruction) and scales four (16 bytes
+//    of a row), about 3.5x fewer line touches than one stage per load.  Per stage
+//    (WS = 4 or 3 buffers): fp32 [hi | lo] A, whose W wraps at K mid-chunk when K / 64
+//    is odd, and tiles that must fit two workgroups per CU.  Each
+//    wave dequantises its B fragments in registers right before its MFMAs
+//    (cvt_scalef32_pk_f32_fp4 with 2^120 in the scale operand, x 2^-120 E4M3 scale,
+//    keep the exact high halves as bf16).  The packed form keeps W's LDS traffic 4x
+//    smaller than a bf16 copy.
 //  * K order: within a 64-wide stage, MFMA step q (0..3) and lane half h = lane/32
 //    take the 8 k values of piece 4h + q (a permutation of k applied to A and W alike,
 //    which leaves the dot products unchanged), so a lane's four code words of a stage
@@ -66,16 +77,23 @@ constexpr int kWCpol = 0;
 
 // NT (32-row W blocks per wave) defaults to the full 256-row W tile; with WC = 2 and
 // NT = 2 only W rows 0..127 are used (the half-width tile: 2 x 2 waves, both wave rows
-// on the same 128 W rows), the stage layout staying that of 256 rows.
-template <int MT, int WC = 4, int NT = 8 / WC> struct Layout {
+// on the same 128 W rows), the stage layout staying that of 256 rows.  WS: W's LDS
+// buffers -- 0: chunked (two 2-stage code buffers, two 4-stage scale buffers; no K wrap);
+// 4: per-stage ring, W loads with the same two stages of latency cover as A's; 3:
+// per-stage ring with one stage of cover, for tiles that must fit two workgroups per CU.
+constexpr int kCodeChunk = 2 * kWCode;   // 16 KiB: codes of 2 stages, 64 bytes per row
+constexpr int kScaleChunk = 4 * kWScale; // 4 KiB: scales of 4 stages, 16 bytes per row
+template <int MT, int WC = 4, int NT = 8 / WC, int WS = 0> struct Layout {
+    static_assert(WS == 0 || WS == 3 || WS == 4, "W buffers");
     static constexpr int kWR = 4 / WC;
     static constexpr int kNT = NT;
     static constexpr int kBM = 32 * MT * kWR;
     static constexpr int kAStage = kBM * kARow;
-    static constexpr int kStage = kAStage + kWCode + kWScale;
-    static constexpr size_t kLds = (size_t)kStages * kStage;
+    static constexpr int kWStage = kWCode + kWScale;
+    static constexpr size_t kLds = (size_t)kStages * kAStage +
+                                   (WS == 0 ? 2 * (size_t)(kCodeChunk + kScaleChunk) : (size_t)WS * kWStage);
 };
-constexpr size_t kMaxLds = Layout<8>::kLds;
+constexpr size_t kMaxLds = Layout<8>::kLds > Layout<8, 4, 2, 4>::kLds ? Layout<8>::kLds : Layout<8, 4, 2, 4>::kLds;
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -131,7 +149,7 @@ template <int WC, int NT = 8 / WC> __device__ __forceinline__ int wave_col0() {
 
 // VPM: VALU slots after each MFMA in the interleaved schedule (the decode work per MFMA
 // grows as MT shrinks: 2 fragments of 16 ops per 2 MT MFMAs).
-template <int MT, int WC, int NT = 8 / WC, int VPM = 3, typename ARow, typename WCode,
+template <int MT, int WC, int NT = 8 / WC, int VPM = 3, int WS = 0, typename ARow, typename WCode,
           typename WScale>
 __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t ra,
                                           const __amdgpu_buffer_rsrc_t (&rc)[2],
@@ -139,12 +157,30 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
                                           ARow a_row, WCode w_code, WScale w_scale,
                                           Acc<MT, WC, NT> &acc, uint32_t kw_wrap = 0xFFFFFFFFu) {
     static_assert(WC * NT * 32 <= BN, "the waves' W blocks lie in the staged W tile");
+    using L = Layout<MT, WC, NT, WS>;
     constexpr int WR = 4 / WC;
-    constexpr int kAStage = Layout<MT, WC, NT>::kAStage;
-    constexpr int kStage = Layout<MT, WC, NT>::kStage;
+    constexpr int kAStage = L::kAStage;
+    constexpr int kWStage = L::kWStage;
     constexpr int kARows = 8 * MT * WR;       // A rows each wave copies per stage
     constexpr int kALoads = MT * WR;          // DMA loads of 8 A rows per wave per stage
     constexpr int kLoadsPerStage = kALoads + 2 + 1;
+    // Loads a wave may leave in flight at the wait before stage s's barrier, which needs
+    // A(s+1) and W(s+2): WS = 4 issues W(s+2) with A(s+1), so the latest batch (A(s+2),
+    // W(s+3)) may be pending; WS = 3 issues W(s+2) first in the latest batch, so only
+    // that batch's A loads may.
+    constexpr int kInFlight = WS == 4 ? kLoadsPerStage * (kStages - 2) : kALoads;
+    uint8_t *const wring = lds + kStages * kAStage;
+    // Chunked W (WS = 0): code chunk c (stages 2c, 2c+1) in buffer c % 2, scale chunk d
+    // (stages 4d .. 4d+3) in buffer d % 2, each issued four stages before its first
+    // stage: 4 code loads per wave per chunk, 1 scale load per wave per chunk.
+    constexpr bool kChunk = WS == 0;
+    constexpr int kCodeLoads = 4;
+    // Chunked mode also spreads A(s+3)'s loads: the first kAFirst right after stage s's
+    // barrier, the rest in step 1 of stage s+1, so fewer DMA instructions queue behind
+    // one barrier.
+    constexpr int kAFirst = (kALoads + 1) / 2;
+    uint8_t *const cring = wring;
+    uint8_t *const sring = wring + 2 * kCodeChunk;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -181,25 +217,42 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     }
     const int se = wave * 64 + lane;   // scale entry -> tile row
     const uint32_t ws_off = w_scale(64 * ((se % 128) / 32) + 32 * (se / 128) + se % 32);
+    // Chunked codes: 16-byte slot q of a chunk holds piece (q%4) ^ ((q/16)%4) of tile row
+    // q/4 (piece p = bytes 16p .. 16p+15 of the row's 64: stage 2c + p/2, lane half p%2),
+    // so the 16 lanes reading one piece of 16 consecutive rows hit distinct bank groups;
+    // wave w copies slots [256w, 256w+256) with 4 DMA loads (load k: rows 64w + 16k +
+    // 0..15, all of matrix k/2).
+    uint32_t cc_off[kCodeLoads];
+#pragma unroll
+    for (int k = 0; k < kCodeLoads; ++k) {
+        const int q = wave * 256 + k * 64 + lane;
+        const int trow = q / 4;
+        const int piece = (q & 3) ^ ((trow >> 2) & 3);
+        const uint32_t ro = w_code(trow);
+        cc_off[k] = ro == kOut ? kOut : ro + piece * 16;
+    }
 
     // The stage's K position rides in the scalar offset: the per-lane offsets are fixed
     // for the whole tile (a valid row plus k0 stays inside its row; an out-of-range
     // lane offset stays out of range).
-    auto load_stage = [&](int buf, uint32_t k0) {
-        uint8_t *base = lds + buf * kStage;
-        const uint32_t kw = k0 >= kw_wrap ? k0 - kw_wrap : k0;
+    auto load_a = [&](int buf, uint32_t k0, int i0, int i1) {
+        uint8_t *base = lds + buf * kAStage;
 #pragma unroll
-        for (int i = 0; i < kALoads; ++i)
+        for (int i = i0; i < i1; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ra, (lds_void_t *)(base + (wave * kARows + 8 * i) * kARow), 16, a_off[i],
                 (int)(k0 * 2), 0, 0);
+    };
+    auto load_w = [&](int wbuf, uint32_t k0) {
+        uint8_t *base = wring + wbuf * kWStage;
+        const uint32_t kw = k0 >= kw_wrap ? k0 - kw_wrap : k0;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rc[i], (lds_void_t *)(base + kAStage + (wave * 128 + i * 64) * 16), 16,
-                wc_off[i], (int)(kw / 2), 0, kWCpol);
+                rc[i], (lds_void_t *)(base + (wave * 128 + i * 64) * 16), 16, wc_off[i],
+                (int)(kw / 2), 0, kWCpol);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs[wave / 2], (lds_void_t *)(base + kAStage + kWCode + wave * 64 * 4), 4, ws_off,
+            rs[wave / 2], (lds_void_t *)(base + kWCode + wave * 64 * 4), 4, ws_off,
             (int)(kw / 16), 0, kWCpol);
     };
 
@@ -213,27 +266,70 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
 
     const uint32_t nk = K / BK;
     auto kofs = [&](uint32_t st) { return st < nk ? st * BK : 0u; }; // past the end: harmless re-read
-
-    u32x4_t wcode[NT];
-    f32x2_t wsc[NT];
-    bf16x8_v af[2][MT], bf[2][NT];
-    auto read_w = [&](int buf) {
-        const uint8_t *lwc = lds + buf * kStage + kAStage;
-        const uint8_t *lws = lwc + kWCode;
+    // A chunk's bytes past the row's last stage (K / 64 not a multiple of the chunk) are
+    // the next row's or, past the matrix, zeros: loaded, never read.
+    auto load_codes = [&](uint32_t c) {
+        uint8_t *base = cring + (c & 1) * kCodeChunk;
+        const uint32_t k0 = kofs(2 * c);
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            // rows wn + 32 j + frow, half h (code words 4h .. 4h+3 = scale blocks 2h,
-            // 2h+1), slot 2r + (h ^ ((r/8)%2))
-            const int r = wn + 32 * j + frow;
-            wcode[j] = *reinterpret_cast<const u32x4_t *>(lwc + (2 * r + (h ^ ((r >> 3) & 1))) * 16);
-            const int se = 128 * ((r >> 5) & 1) + 32 * (r >> 6) + (r & 31);
-            const uint32_t sb = *reinterpret_cast<const uint16_t *>(lws + se * 4 + 2 * h);
-            wsc[j] = f32x2_t{e4m3_to_f32(sb), e4m3_to_f32(sb >> 8)};
+        for (int k = 0; k < kCodeLoads; ++k)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rc[k >> 1], (lds_void_t *)(base + (wave * 256 + k * 64) * 16), 16, cc_off[k],
+                (int)(k0 / 2), 0, kWCpol);
+    };
+    auto load_scales = [&](uint32_t d) {
+        uint8_t *base = sring + (d & 1) * kScaleChunk;
+        const uint32_t k0 = kofs(4 * d);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs[wave / 2], (lds_void_t *)(base + wave * 64 * 16), 16,
+                                                 ws_off, (int)(k0 / 16), 0, kWCpol);
+    };
+
+    // Two register sets of a stage's W: codes (4 words per fragment), raw scale bytes
+    // and the decoded scales; set p holds the running stage's, set 1-p is filled with
+    // the next stage's during steps 1 and 2.
+    u32x4_t wcode[2][NT];
+    uint32_t wsraw[2][NT];
+    f32x2_t wsc[2][NT];
+    bf16x8_v af[2][MT], bf[2][NT];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    // W of stage x into register set P: rows wn + 32 j + frow, half h (code words
+    // 4h .. 4h+3 = scale blocks 2h, 2h+1).
+    auto read_w = [&](auto P, uint32_t x) {
+        constexpr int p = decltype(P)::value;
+        if constexpr (kChunk) {
+            const uint8_t *lwc = cring + ((x >> 1) & 1) * kCodeChunk;
+            const uint8_t *lws = sring + ((x >> 2) & 1) * kScaleChunk + (x & 3) * 4 + 2 * h;
+            const int piece = 2 * (int)(x & 1) + h;
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const int r = wn + 32 * j + frow;
+                wcode[p][j] = *reinterpret_cast<const u32x4_t *>(lwc + r * 64 + ((piece ^ ((r >> 2) & 3)) * 16));
+                const int e = 128 * ((r >> 5) & 1) + 32 * (r >> 6) + (r & 31);
+                wsraw[p][j] = *reinterpret_cast<const uint16_t *>(lws + e * 16);
+            }
+        } else {
+            const uint8_t *lwc = wring + (x % WS) * kWStage;
+            const uint8_t *lws = lwc + kWCode;
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                // slot 2r + (h ^ ((r/8)%2))
+                const int r = wn + 32 * j + frow;
+                wcode[p][j] = *reinterpret_cast<const u32x4_t *>(lwc + (2 * r + (h ^ ((r >> 3) & 1))) * 16);
+                const int e = 128 * ((r >> 5) & 1) + 32 * (r >> 6) + (r & 31);
+                wsraw[p][j] = *reinterpret_cast<const uint16_t *>(lws + e * 4 + 2 * h);
+            }
         }
+    };
+    auto decode_scales = [&](auto P) {
+        constexpr int p = decltype(P)::value;
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+            wsc[p][j] = f32x2_t{e4m3_to_f32_x2m120(wsraw[p][j]), e4m3_to_f32_x2m120(wsraw[p][j] >> 8)};
     };
     // A fragments of step q: rows 32 i + frow, logical piece 4h + q.
     auto read_a = [&](bf16x8_v (&dst)[MT], int buf, int q) {
-        const uint8_t *la = lds + buf * kStage;
+        const uint8_t *la = lds + buf * kAStage;
         const int piece = 4 * h + q;
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
@@ -241,13 +337,15 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
             dst[i] = *reinterpret_cast<const bf16x8_v *>(la + r * kARow + ((piece ^ ((r >> 1) & 7)) * 16));
         }
     };
-    // B fragments of step q: word q of each tile's codes (8 weights), scale block 2h + q/2.
-    auto dequant_b = [&](bf16x8_v (&dst)[NT], int q) {
+    // B fragments of step q: word q of each tile's codes (8 weights), scale block 2h + q/2;
+    // (code x 2^120) x (scale x 2^-120) is the exact product.
+    auto dequant_b = [&](bf16x8_v (&dst)[NT], auto P, int q) {
+        constexpr int p = decltype(P)::value;
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
             f32x2_t v[4];
-            e2m1x8_to_f32(wcode[j][q], v);
-            const float sc = wsc[j][q >> 1];
+            e2m1x8_to_f32_x2p120(wcode[p][j][q], v);
+            const float sc = wsc[p][j][q >> 1];
             u32x4_t bw;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -277,46 +375,110 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         // slots, or their fragment reads end up right before them (exposed latency).
         __builtin_amdgcn_sched_barrier(0);
     };
-
-    // Prologue: stages 0 .. kStages-1 in flight; stage 0 visible; step 0 prepared.
+    // DMA batches: W(x) lives in W buffer x % WS, A(x) in A buffer x % kStages.  WS = 4:
+    // batch b is A(b) and W(b + 1), after a lone W(0); WS = 3: batch b is W(b) then A(b),
+    // so the wait before a barrier can leave the latest batch's A loads in flight.
+    // Prologue: batches 0 .. kStages-1 in flight; A(0), W(0) and W(1) visible; step 0
+    // prepared.
+    if constexpr (kChunk) {
+        // scales 0, codes 0, A(0) | codes 1, A(1) | A(2): the first group visible
+        load_scales(0);
+        load_codes(0);
+        load_a(0, kofs(0), 0, kALoads);
+        load_codes(1);
+        load_a(1, kofs(1), 0, kALoads);
+        load_a(2, kofs(2), 0, kAFirst); // the rest in stage 0's step 1
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCodeLoads + kALoads + kAFirst) : "memory");
+    } else if constexpr (WS == 4) {
+        load_w(0, kofs(0));
 #pragma unroll
-    for (int st = 0; st < kStages; ++st)
-        load_stage(st, kofs(st));
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerStage * (kStages - 1)) : "memory");
+        for (uint32_t st = 0; st < (uint32_t)kStages; ++st) {
+            load_a((int)st, kofs(st), 0, kALoads);
+            load_w((int)(st + 1), kofs(st + 1));
+        }
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerStage * (kStages - 1)) : "memory");
+    } else {
+#pragma unroll
+        for (uint32_t st = 0; st < (uint32_t)kStages; ++st) {
+            load_w((int)st, kofs(st));
+            load_a((int)st, kofs(st), 0, kALoads);
+        }
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerStage * (kStages - 2) + kALoads) : "memory");
+    }
     __syncthreads();
-    read_w(0);
+    read_w(I0{}, 0u);
+    decode_scales(I0{});
     read_a(af[0], 0, 0);
-    dequant_b(bf[0], 0);
+    dequant_b(bf[0], I0{}, 0);
 
-    // Stage s (buffer s % kStages): after step 2 every read of the buffer has been
-    // issued: the wave waits for them and for its part of stage s+1, meets the barrier
-    // (stage s+1 visible everywhere, buffer s retired) and refills buffer s with stage
-    // s + kStages; step 3 then hides stage s+1's first reads and dequantisation.
-    for (uint32_t s = 0; s < nk; ++s) {
+    // Stage s (A buffer s % kStages, W in register set P = s % 2): steps 1 and 2 also
+    // read W(s+1) into the other set and decode its scales.  After step 2 every read of
+    // A buffer s % kStages has been issued: the wave waits for them and for A(s+1) and
+    // W(s+2), meets the barrier (both visible everywhere, A buffer s and W buffer
+    // s % WS retired) and issues batch s + kStages (A(s+3), W(s+4); WS = 3: W(s+3) and
+    // A(s+3)); step 3 then hides stage s+1's first reads and dequantisation.
+    auto stage = [&](uint32_t s, auto P) {
+        constexpr int p = decltype(P)::value;
+        using N = std::integral_constant<int, 1 - p>;
         const int buf = s % kStages;
         const int nbuf = (s + 1) % kStages;
         read_a(af[1], buf, 1);
-        dequant_b(bf[1], 1);
+        dequant_b(bf[1], P, 1);
+        read_w(N{}, s + 1);
+        if constexpr (kChunk)
+            load_a((int)((s + 2) % kStages), kofs(s + 2), kAFirst, kALoads);
         mfmas(af[0], bf[0]);
         interleave();
         read_a(af[0], buf, 2);
-        dequant_b(bf[0], 2);
+        dequant_b(bf[0], P, 2);
+        decode_scales(N{});
         mfmas(af[1], bf[1]);
         interleave();
         read_a(af[1], buf, 3);
-        dequant_b(bf[1], 3);
+        dequant_b(bf[1], P, 3);
         mfmas(af[0], bf[0]);
         interleave();
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kLoadsPerStage * (kStages - 2))
-                     : "memory");
-        __syncthreads();
-        load_stage(buf, kofs(s + kStages));
-        read_w(nbuf);
+        // The explicit wait covers what the barrier must order (this wave's LDS reads,
+        // A(s+1) and W(s+2) landed), so the barrier is the bare instruction: with
+        // __syncthreads' fence the compiler added a wait for every DMA load in flight
+        // before one of the two unrolled stages' barriers.
+        if constexpr (kChunk) {
+            // the previous stage's batch may stay in flight: A only after an odd stage,
+            // codes and A after an even one (its scale load, issued first, must land)
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(p == 0 ? kALoads : kALoads + kCodeLoads)
+                         : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kInFlight) : "memory");
+        }
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if constexpr (kChunk) {
+            // even stages issue the W chunks whose first stage is s + 4
+            if (p == 0) {
+                if ((s & 3) == 0)
+                    load_scales(s / 4 + 1);
+                load_codes(s / 2 + 2);
+            }
+            load_a(buf, kofs(s + kStages), 0, kAFirst);
+        } else if constexpr (WS == 4) {
+            load_a(buf, kofs(s + kStages), 0, kALoads);
+            load_w((int)(s % WS), kofs(s + WS));
+        } else {
+            load_w((int)(s % WS), kofs(s + WS));
+            load_a(buf, kofs(s + kStages), 0, kALoads);
+        }
         read_a(af[0], nbuf, 0);
-        dequant_b(bf[0], 0);
+        dequant_b(bf[0], N{}, 0);
         mfmas(af[1], bf[1]);
         interleave();
+    };
+    uint32_t s = 0;
+    for (; s + 2 <= nk; s += 2) {
+        stage(s, I0{});
+        stage(s + 1, I1{});
     }
+    if (s < nk)
+        stage(s, I0{});
     // Drain the DMA loads of the stages past the end, so the LDS is free for the
     // caller (epilogue staging or the next tile).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

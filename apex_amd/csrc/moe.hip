@@ -1748,6 +1748,10 @@ __global__ __launch_bounds__(kThreads) void moe_gateup_gemm_kernel(MoeArgs a) {
     }
 }
 
+// The down tiles run two workgroups per CU, so their W ring is 3 stages deep (one stage
+// of latency cover for W's loads) to fit two in the LDS.
+constexpr int kDownWS = 3;
+
 template <int MT>
 __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e, uint32_t row0,
                                           uint32_t nrows, uint32_t n0) {
@@ -1761,7 +1765,7 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
     auto w_scale = [=](int r) { return n0 + r < H ? ds + (n0 + r) * (I / 16) : kOut; };
     const __amdgpu_buffer_rsrc_t rw2[2] = {rw, rw};
     Acc<MT, 4> acc;
-    gemm_tile<MT, 4>(lds, ra, rw2, rw2, I, a_row, w_code, w_scale, acc);
+    gemm_tile<MT, 4, 2, 3, kDownWS>(lds, ra, rw2, rw2, I, a_row, w_code, w_scale, acc);
     // Whole-row stores staged through the drained LDS ring: 3% faster than the direct
     // 16-byte pieces on this short-K GEMM (the GeGLU gate/up epilogue was 5% slower
     // staged, so it stores directly).
@@ -1776,7 +1780,8 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
 // as many 32-row blocks as its rows need.  Virtual m-tiles: halves of big tile k at
 // 16 (k / 8) + k % 8 + 8 h (both on XCD k % 8, one after the other, so the second finds
 // the W tile in L2), then the small tiles.
-constexpr size_t kDownLds = Layout<4, 4>::kLds;
+constexpr size_t kDownLds = Layout<4, 4, 2, kDownWS>::kLds;
+static_assert(2 * kDownLds <= 160 * 1024, "two down workgroups per CU");
 
 __global__ __launch_bounds__(kThreads, 2) void moe_down_gemm_kernel(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];

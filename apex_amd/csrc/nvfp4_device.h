@@ -58,6 +58,14 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
     return __uint_as_float(__float_as_uint(mag) | ((b & 0x80u) << 24));
 }
 
+// The same construction without the final 2^120: E4M3 byte -> 2^-120 times its value
+// (a normal or denormal fp32, sign included).  Paired with e2m1x8_to_f32_x2p120 -- the
+// codes converted with the power-of-two 2^120 in the conversion's scale operand -- the
+// product code * scale is the same exact fp32 value with one multiply fewer per scale.
+__device__ __forceinline__ float e4m3_to_f32_x2m120(uint32_t b) {
+    return __uint_as_float(((b & 0x7Fu) << 20) | ((b & 0x80u) << 24));
+}
+
 // Eight E2M1 codes of one word -> four bf16 pairs (elements 2j, 2j+1 in pair j).
 __device__ __forceinline__ void e2m1x8_to_bf16(uint32_t w, bf16x2_t out[4]) {
     out[0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 0);
@@ -72,6 +80,15 @@ __device__ __forceinline__ void e2m1x8_to_f32(uint32_t w, f32x2_t out[4]) {
     out[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
     out[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
     out[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+}
+
+// Eight E2M1 codes of one word -> eight fp32 values times 2^120 (exact: the scale
+// operand is a power of two, which the conversion applies as an exponent offset).
+__device__ __forceinline__ void e2m1x8_to_f32_x2p120(uint32_t w, f32x2_t out[4]) {
+    out[0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 0x1p120f, 0);
+    out[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 0x1p120f, 1);
+    out[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 0x1p120f, 2);
+    out[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 0x1p120f, 3);
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
