@@ -175,10 +175,14 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     // stage: 4 code loads per wave per chunk, 1 scale load per wave per chunk.
     constexpr bool kChunk = WS == 0;
     constexpr int kCodeLoads = 4;
-    // Chunked mode also spreads A(s+3)'s loads: the first kAFirst right after stage s's
-    // barrier, the rest in step 1 of stage s+1, so fewer DMA instructions queue behind
-    // one barrier.
-    constexpr int kAFirst = (kALoads + 1) / 2;
+    // Chunked mode also spreads the loads issued after stage s's barrier (window s:
+    // scales, codes, A(s+3)) over that step and steps 1 and 2 of stage s+1 -- one burst
+    // of DMA instructions behind each barrier stalled the waves' issue (measured: two
+    // parts 1-2 % faster than one, three parts faster again).  Window s's loads all go
+    // out before stage s+1's wait, so the waits count the same loads in flight.
+    constexpr int kA1 = (kALoads + 2) / 3;          // A loads right after the barrier
+    constexpr int kA2 = kA1 + (kALoads - kA1 + 1) / 2; // ... up to here in step 1
+    constexpr int kAFirst = kA1;
     uint8_t *const cring = wring;
     uint8_t *const sring = wring + 2 * kCodeChunk;
 
@@ -268,11 +272,11 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     auto kofs = [&](uint32_t st) { return st < nk ? st * BK : 0u; }; // past the end: harmless re-read
     // A chunk's bytes past the row's last stage (K / 64 not a multiple of the chunk) are
     // the next row's or, past the matrix, zeros: loaded, never read.
-    auto load_codes = [&](uint32_t c) {
+    auto load_codes_part = [&](uint32_t c, int k0_, int k1_) {
         uint8_t *base = cring + (c & 1) * kCodeChunk;
         const uint32_t k0 = kofs(2 * c);
 #pragma unroll
-        for (int k = 0; k < kCodeLoads; ++k)
+        for (int k = k0_; k < k1_; ++k)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rc[k >> 1], (lds_void_t *)(base + (wave * 256 + k * 64) * 16), 16, cc_off[k],
                 (int)(k0 / 2), 0, kWCpol);
@@ -383,11 +387,11 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     if constexpr (kChunk) {
         // scales 0, codes 0, A(0) | codes 1, A(1) | A(2): the first group visible
         load_scales(0);
-        load_codes(0);
+        load_codes_part(0, 0, kCodeLoads);
         load_a(0, kofs(0), 0, kALoads);
-        load_codes(1);
+        load_codes_part(1, 0, kCodeLoads);
         load_a(1, kofs(1), 0, kALoads);
-        load_a(2, kofs(2), 0, kAFirst); // the rest in stage 0's step 1
+        load_a(2, kofs(2), 0, kAFirst); // the rest in stage 0's steps 1 and 2
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCodeLoads + kALoads + kAFirst) : "memory");
     } else if constexpr (WS == 4) {
         load_w(0, kofs(0));
@@ -405,7 +409,10 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         }
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerStage * (kStages - 2) + kALoads) : "memory");
     }
-    __syncthreads();
+    // bare barrier: __syncthreads' fence made the compiler wait for every DMA load in
+    // flight here
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     read_w(I0{}, 0u);
     decode_scales(I0{});
     read_a(af[0], 0, 0);
@@ -425,13 +432,23 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         read_a(af[1], buf, 1);
         dequant_b(bf[1], P, 1);
         read_w(N{}, s + 1);
-        if constexpr (kChunk)
-            load_a((int)((s + 2) % kStages), kofs(s + 2), kAFirst, kALoads);
+        // window s-1's parts 1 and 2: its codes (when s-1 is even: chunk (s+3) / 2) and
+        // the rest of A(s+2)
+        if constexpr (kChunk) {
+            if (p == 1)
+                load_codes_part((s + 3) / 2, 0, kCodeLoads / 2);
+            load_a((int)((s + 2) % kStages), kofs(s + 2), kA1, kA2);
+        }
         mfmas(af[0], bf[0]);
         interleave();
         read_a(af[0], buf, 2);
         dequant_b(bf[0], P, 2);
         decode_scales(N{});
+        if constexpr (kChunk) {
+            if (p == 1)
+                load_codes_part((s + 3) / 2, kCodeLoads / 2, kCodeLoads);
+            load_a((int)((s + 2) % kStages), kofs(s + 2), kA2, kALoads);
+        }
         mfmas(af[1], bf[1]);
         interleave();
         read_a(af[1], buf, 3);
@@ -453,13 +470,11 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if constexpr (kChunk) {
-            // even stages issue the W chunks whose first stage is s + 4
-            if (p == 0) {
-                if ((s & 3) == 0)
-                    load_scales(s / 4 + 1);
-                load_codes(s / 2 + 2);
-            }
-            load_a(buf, kofs(s + kStages), 0, kAFirst);
+            // window s: after an even stage the W chunks whose first stage is s + 4 (the
+            // codes in stage s+1's steps 1 and 2), then A(s+3)'s first part
+            if (p == 0 && (s & 3) == 0)
+                load_scales(s / 4 + 1);
+            load_a(buf, kofs(s + kStages), 0, kA1);
         } else if constexpr (WS == 4) {
             load_a(buf, kofs(s + kStages), 0, kALoads);
             load_w((int)(s % WS), kofs(s + WS));
