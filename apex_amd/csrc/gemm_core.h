@@ -164,25 +164,18 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     constexpr int kARows = 8 * MT * WR;       // A rows each wave copies per stage
     constexpr int kALoads = MT * WR;          // DMA loads of 8 A rows per wave per stage
     constexpr int kLoadsPerStage = kALoads + 2 + 1;
-    // Loads a wave may leave in flight at the wait before stage s's barrier, which needs
-    // A(s+1) and W(s+2): WS = 4 issues W(s+2) with A(s+1), so the latest batch (A(s+2),
-    // W(s+3)) may be pending; WS = 3 issues W(s+2) first in the latest batch, so only
-    // that batch's A loads may.
-    constexpr int kInFlight = WS == 4 ? kLoadsPerStage * (kStages - 2) : kALoads;
     uint8_t *const wring = lds + kStages * kAStage;
     // Chunked W (WS = 0): code chunk c (stages 2c, 2c+1) in buffer c % 2, scale chunk d
     // (stages 4d .. 4d+3) in buffer d % 2, each issued four stages before its first
     // stage: 4 code loads per wave per chunk, 1 scale load per wave per chunk.
     constexpr bool kChunk = WS == 0;
     constexpr int kCodeLoads = 4;
-    // Chunked mode also spreads the loads issued after stage s's barrier (window s:
-    // scales, codes, A(s+3)) over that step and steps 1 and 2 of stage s+1 -- one burst
-    // of DMA instructions behind each barrier stalled the waves' issue (measured: two
-    // parts 1-2 % faster than one, three parts faster again).  Window s's loads all go
-    // out before stage s+1's wait, so the waits count the same loads in flight.
+    // The loads issued after stage s's barrier (window s: W, A(s+3)) are spread over that
+    // step and steps 1 and 2 of stage s+1 -- one burst of DMA instructions behind each
+    // barrier stalled the waves' issue (measured: two parts 1-2 % faster than one, three
+    // parts faster again).  Window s's loads all go out before stage s+1's wait.
     constexpr int kA1 = (kALoads + 2) / 3;          // A loads right after the barrier
     constexpr int kA2 = kA1 + (kALoads - kA1 + 1) / 2; // ... up to here in step 1
-    constexpr int kAFirst = kA1;
     uint8_t *const cring = wring;
     uint8_t *const sring = wring + 2 * kCodeChunk;
 
@@ -379,35 +372,35 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         // slots, or their fragment reads end up right before them (exposed latency).
         __builtin_amdgcn_sched_barrier(0);
     };
-    // DMA batches: W(x) lives in W buffer x % WS, A(x) in A buffer x % kStages.  WS = 4:
-    // batch b is A(b) and W(b + 1), after a lone W(0); WS = 3: batch b is W(b) then A(b),
-    // so the wait before a barrier can leave the latest batch's A loads in flight.
-    // Prologue: batches 0 .. kStages-1 in flight; A(0), W(0) and W(1) visible; step 0
-    // prepared.
+    // DMA windows.  A(x) lives in A buffer x % kStages; per-stage W(x) in W buffer x % WS,
+    // chunked W as above.  Window s goes out after stage s's barrier and during steps 1
+    // and 2 of stage s+1: A(s+3) and the W four stages ahead (per stage: W(s+4), into the
+    // buffer whose stage, s+1 or s, was read before the barrier; chunked: after a stage
+    // s = 0 mod 4 the scale chunk of stages s+4 .. s+7, after an even one the code chunk
+    // of stages s+4, s+5).  Stage x's wait needs A(x+1) and W(x+2), both in window x-2,
+    // and leaves window x-1 in flight: two stages of latency cover for every load.
+    // The prologue issues windows -4 .. -1 (W(0) alone, then W(1) A(0), W(2) A(1), W(3)
+    // A(2)); with WS = 3, W(3) would overwrite W(0) before it is read, so window -1
+    // repeats W(2) (the same bytes into the same buffer: harmless to a concurrent read)
+    // and window 0 adds W(3) first (the wait before stage 1's barrier, which needs it,
+    // makes it land).
     if constexpr (kChunk) {
-        // scales 0, codes 0, A(0) | codes 1, A(1) | A(2): the first group visible
         load_scales(0);
         load_codes_part(0, 0, kCodeLoads);
         load_a(0, kofs(0), 0, kALoads);
         load_codes_part(1, 0, kCodeLoads);
         load_a(1, kofs(1), 0, kALoads);
-        load_a(2, kofs(2), 0, kAFirst); // the rest in stage 0's steps 1 and 2
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCodeLoads + kALoads + kAFirst) : "memory");
-    } else if constexpr (WS == 4) {
-        load_w(0, kofs(0));
-#pragma unroll
-        for (uint32_t st = 0; st < (uint32_t)kStages; ++st) {
-            load_a((int)st, kofs(st), 0, kALoads);
-            load_w((int)(st + 1), kofs(st + 1));
-        }
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerStage * (kStages - 1)) : "memory");
+        load_a(2, kofs(2), 0, kA1); // the rest in stage 0's steps 1 and 2
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCodeLoads + kALoads + kA1) : "memory");
     } else {
-#pragma unroll
-        for (uint32_t st = 0; st < (uint32_t)kStages; ++st) {
-            load_w((int)st, kofs(st));
-            load_a((int)st, kofs(st), 0, kALoads);
-        }
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerStage * (kStages - 2) + kALoads) : "memory");
+        load_w(0, kofs(0));
+        load_w(1, kofs(1));
+        load_a(0, kofs(0), 0, kALoads);
+        load_w(2, kofs(2));
+        load_a(1, kofs(1), 0, kALoads);
+        load_w((WS == 4 ? 3 : 2), kofs(WS == 4 ? 3 : 2));
+        load_a(2, kofs(2), 0, kA1);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 + kALoads + kA1) : "memory");
     }
     // bare barrier: __syncthreads' fence made the compiler wait for every DMA load in
     // flight here
@@ -418,82 +411,79 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     read_a(af[0], 0, 0);
     dequant_b(bf[0], I0{}, 0);
 
-    // Stage s (A buffer s % kStages, W in register set P = s % 2): steps 1 and 2 also
-    // read W(s+1) into the other set and decode its scales.  After step 2 every read of
-    // A buffer s % kStages has been issued: the wave waits for them and for A(s+1) and
-    // W(s+2), meets the barrier (both visible everywhere, A buffer s and W buffer
-    // s % WS retired) and issues batch s + kStages (A(s+3), W(s+4); WS = 3: W(s+3) and
-    // A(s+3)); step 3 then hides stage s+1's first reads and dequantisation.
-    auto stage = [&](uint32_t s, auto P) {
-        constexpr int p = decltype(P)::value;
+    // Stage s (phase PH = s % 4, A buffer s % kStages, W in register set s % 2): steps 1
+    // and 2 also read W(s+1) into the other set, decode its scales and issue window s-1's
+    // later parts.  After step 3's reads the wave waits, meets the barrier (A(s+1),
+    // W(s+2) visible everywhere; A buffer s and the W just read retired), issues window
+    // s's first part, and step 3's MFMAs hide stage s+1's first reads and dequantisation.
+    auto stage = [&](uint32_t s, auto PH) {
+        constexpr int ph = decltype(PH)::value;
+        constexpr int p = ph & 1;
+        constexpr int pph = (ph + 3) & 3; // phase of stage s-1
+        using P = std::integral_constant<int, p>;
         using N = std::integral_constant<int, 1 - p>;
         const int buf = s % kStages;
         const int nbuf = (s + 1) % kStages;
+        const int abuf = (s + 2) % kStages; // window s-1's A(s+2)
         read_a(af[1], buf, 1);
-        dequant_b(bf[1], P, 1);
+        dequant_b(bf[1], P{}, 1);
         read_w(N{}, s + 1);
-        // window s-1's parts 1 and 2: its codes (when s-1 is even: chunk (s+3) / 2) and
-        // the rest of A(s+2)
-        if constexpr (kChunk) {
-            if (p == 1)
-                load_codes_part((s + 3) / 2, 0, kCodeLoads / 2);
-            load_a((int)((s + 2) % kStages), kofs(s + 2), kA1, kA2);
-        }
+        if constexpr (kChunk && (pph & 1) == 0)
+            load_codes_part((s + 3) / 2, 0, kCodeLoads / 2);
+        load_a(abuf, kofs(s + 2), kA1, kA2);
         mfmas(af[0], bf[0]);
         interleave();
         read_a(af[0], buf, 2);
-        dequant_b(bf[0], P, 2);
+        dequant_b(bf[0], P{}, 2);
         decode_scales(N{});
-        if constexpr (kChunk) {
-            if (p == 1)
-                load_codes_part((s + 3) / 2, kCodeLoads / 2, kCodeLoads);
-            load_a((int)((s + 2) % kStages), kofs(s + 2), kA2, kALoads);
-        }
+        if constexpr (kChunk && (pph & 1) == 0)
+            load_codes_part((s + 3) / 2, kCodeLoads / 2, kCodeLoads);
+        load_a(abuf, kofs(s + 2), kA2, kALoads);
         mfmas(af[1], bf[1]);
         interleave();
         read_a(af[1], buf, 3);
-        dequant_b(bf[1], P, 3);
+        dequant_b(bf[1], P{}, 3);
         mfmas(af[0], bf[0]);
         interleave();
         // The explicit wait covers what the barrier must order (this wave's LDS reads,
         // A(s+1) and W(s+2) landed), so the barrier is the bare instruction: with
-        // __syncthreads' fence the compiler added a wait for every DMA load in flight
-        // before one of the two unrolled stages' barriers.
-        if constexpr (kChunk) {
-            // the previous stage's batch may stay in flight: A only after an odd stage,
-            // codes and A after an even one (its scale load, issued first, must land)
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(p == 0 ? kALoads : kALoads + kCodeLoads)
-                         : "memory");
-        } else {
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kInFlight) : "memory");
-        }
+        // __syncthreads' fence the compiler added a wait for every DMA load in flight.
+        constexpr int kWindow = kChunk ? kALoads + ((pph & 1) == 0 ? kCodeLoads : 0) + (pph == 0 ? 1 : 0)
+                                       : kLoadsPerStage;
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kWindow) : "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if constexpr (kChunk) {
-            // window s: after an even stage the W chunks whose first stage is s + 4 (the
-            // codes in stage s+1's steps 1 and 2), then A(s+3)'s first part
-            if (p == 0 && (s & 3) == 0)
+            if constexpr (ph == 0)
                 load_scales(s / 4 + 1);
-            load_a(buf, kofs(s + kStages), 0, kA1);
-        } else if constexpr (WS == 4) {
-            load_a(buf, kofs(s + kStages), 0, kALoads);
-            load_w((int)(s % WS), kofs(s + WS));
         } else {
-            load_w((int)(s % WS), kofs(s + WS));
-            load_a(buf, kofs(s + kStages), 0, kALoads);
+            if constexpr (WS == 3 && ph == 0) {
+                if (s == 0)
+                    load_w(0, kofs(3));
+            }
+            load_w((int)((s + 4) % WS), kofs(s + 4));
         }
+        load_a(buf, kofs(s + kStages), 0, kA1);
         read_a(af[0], nbuf, 0);
         dequant_b(bf[0], N{}, 0);
         mfmas(af[1], bf[1]);
         interleave();
     };
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
     uint32_t s = 0;
-    for (; s + 2 <= nk; s += 2) {
+    for (; s + 4 <= nk; s += 4) {
         stage(s, I0{});
         stage(s + 1, I1{});
+        stage(s + 2, I2{});
+        stage(s + 3, I3{});
     }
     if (s < nk)
         stage(s, I0{});
+    if (s + 1 < nk)
+        stage(s + 1, I1{});
+    if (s + 2 < nk)
+        stage(s + 2, I2{});
     // Drain the DMA loads of the stages past the end, so the LDS is free for the
     // caller (epilogue staging or the next tile).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -561,6 +551,7 @@ __device__ __forceinline__ void store_tile_bf16_lds(const Acc<MT, 4> &acc, uint8
                                                     uint32_t N, float scale) {
     constexpr int kRows = 32 * MT;
     constexpr int kPassRows = kRows > 128 ? 128 : kRows;
+    constexpr int kPasses = (kRows + kPassRows - 1) / kPassRows; // the last may be partial
     constexpr int kRowBytes = BN * 2;
     constexpr int kChunks = kRowBytes / 16; // 32
     const int lane = threadIdx.x & 63;
@@ -569,13 +560,17 @@ __device__ __forceinline__ void store_tile_bf16_lds(const Acc<MT, 4> &acc, uint8
     const __amdgpu_buffer_rsrc_t rc =
         make_rsrc(C + (size_t)m0 * ldc + n0, bytes < 0x80000000ull ? (uint32_t)bytes : 0x7FFFFFF0u);
 #pragma unroll
-    for (int ps = 0; ps < kRows / kPassRows; ++ps) {
+    for (int ps = 0; ps < kPasses; ++ps) {
         if (ps > 0)
             __syncthreads(); // the previous pass's reads are done
-        // block (i, j), piece p -> row 32 i + lane % 32, chunk 8 wave + 4 j + 2 p + lane / 32
+        // block (i, j), piece p -> row 32 i + lane % 32, chunk 8 wave + 4 j + 2 p + lane / 32;
+        // a partial last pass stages its blocks only (its other LDS rows hold stale data
+        // that is stored to rows past the tile, which the descriptor ending at row M drops)
 #pragma unroll
         for (int ii = 0; ii < kPassRows / 32; ++ii) {
             const int i = ps * (kPassRows / 32) + ii;
+            if (i >= MT)
+                break;
             const int r = 32 * ii + (lane & 31);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {

@@ -682,7 +682,7 @@ __device__ void plan_scan(const MoeArgs &a, const int *cnt, int *first, bool pub
         for (int i = 0; i < kTileClasses; ++i)
             nt += total[2 + i];
         v.hdr[1] = nt;
-        // tiles of more than 4 blocks (classes 0..3): the down GEMM splits them in halves
+        // tiles of more than 4 blocks (classes 0..3), reported with the plan
         v.hdr[2] = total[2] + total[3] + total[4] + total[5];
     }
     __syncthreads();
@@ -1748,10 +1748,6 @@ __global__ __launch_bounds__(kThreads) void moe_gateup_gemm_kernel(MoeArgs a) {
     }
 }
 
-// The down tiles run two workgroups per CU, so their W ring is 3 stages deep (one stage
-// of latency cover for W's loads) to fit two in the LDS.
-constexpr int kDownWS = 3;
-
 template <int MT>
 __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e, uint32_t row0,
                                           uint32_t nrows, uint32_t n0) {
@@ -1765,47 +1761,37 @@ __device__ __forceinline__ void down_tile(const MoeArgs &a, uint8_t *lds, int e,
     auto w_scale = [=](int r) { return n0 + r < H ? ds + (n0 + r) * (I / 16) : kOut; };
     const __amdgpu_buffer_rsrc_t rw2[2] = {rw, rw};
     Acc<MT, 4> acc;
-    gemm_tile<MT, 4, 2, 3, kDownWS>(lds, ra, rw2, rw2, I, a_row, w_code, w_scale, acc);
+    gemm_tile<MT, 4>(lds, ra, rw2, rw2, I, a_row, w_code, w_scale, acc);
     // Whole-row stores staged through the drained LDS ring: 3% faster than the direct
     // 16-byte pieces on this short-K GEMM (the GeGLU gate/up epilogue was 5% slower
     // staged, so it stores directly).
     store_tile_bf16_lds<MT>(acc, lds, a.d + (size_t)row0 * H, H, 0, n0, nrows, H, 1.0f);
 }
 
-// The down GEMM's K (= I) is short, so a tile's prologue (plan lookups, first stages in
-// flight) and epilogue (output stores) are a large part of it.  It runs 128-row tiles
-// with two workgroups per CU (76.8 KB of LDS each): one workgroup's prologue and
-// epilogue overlap the other's MFMAs.  Tiles of more than 4 blocks (the first hdr[2]
-// of the list) run as two halves of up to 128 rows, the others as they are, each with
-// as many 32-row blocks as its rows need.  Virtual m-tiles: halves of big tile k at
-// 16 (k / 8) + k % 8 + 8 h (both on XCD k % 8, one after the other, so the second finds
-// the W tile in L2), then the small tiles.
-constexpr size_t kDownLds = Layout<4, 4, 2, kDownWS>::kLds;
-static_assert(2 * kDownLds <= 160 * 1024, "two down workgroups per CU");
-
-__global__ __launch_bounds__(kThreads, 2) void moe_down_gemm_kernel(MoeArgs a) {
+// Down GEMM over the gate/up GEMM's m-tiles (up to 256 rows: 1-8 blocks of 32), one
+// workgroup per CU on the chunked-W tile core, tiles dealt as the gate/up GEMM's
+// (xcd_tile).  Measured against 128-row halves at two workgroups per CU (the previous
+// form, whose 3-stage per-stage W ring fit two in the LDS but left W one stage of
+// latency cover): the same 178 us (fastest of ~100 launches) and 185 vs 189 us on
+// average, with one tile list for both GEMMs.
+__global__ __launch_bounds__(kThreads) void moe_down_gemm_kernel(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t E = a.E, P = a.T * a.k;
     const PlanView v = plan_view(a.plan, E, P);
     const uint32_t nn = (a.H + BN - 1) / BN;
     uint32_t mt, nt;
     xcd_tile(nn, mt, nt);
-    const uint32_t n0t = uniform(v.hdr[2]), ntiles = uniform(v.hdr[1]);
-    const uint32_t nsplit = 16 * ((n0t + 7) / 8);
-    const bool split = mt < nsplit;
-    const uint32_t k0 = 8 * (mt / 16) + mt % 8;
-    if (split ? k0 >= n0t : mt - nsplit + n0t >= ntiles)
+    if (mt >= uniform(v.hdr[1]))
         return;
-    const int32_t *t = v.tiles + 4 * (split ? k0 : mt - nsplit + n0t);
+    const int32_t *t = v.tiles + 4 * mt;
     const int e = uniform(t[0]);
-    uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]);
+    const uint32_t row0 = uniform(t[1]), nrows = uniform(t[2]);
     const uint32_t n0 = nt * BN;
-    if (split) {
-        const uint32_t h = (mt / 8) % 2;
-        row0 += 128 * h;
-        nrows = nrows - 128 * h < 128 ? nrows - 128 * h : 128;
-    }
     switch ((nrows + 31) / 32) {
+    case 8: down_tile<8>(a, lds, e, row0, nrows, n0); break;
+    case 7: down_tile<7>(a, lds, e, row0, nrows, n0); break;
+    case 6: down_tile<6>(a, lds, e, row0, nrows, n0); break;
+    case 5: down_tile<5>(a, lds, e, row0, nrows, n0); break;
     case 4: down_tile<4>(a, lds, e, row0, nrows, n0); break;
     case 3: down_tile<3>(a, lds, e, row0, nrows, n0); break;
     case 2: down_tile<2>(a, lds, e, row0, nrows, n0); break;
@@ -2454,7 +2440,7 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     static std::atomic<uint64_t> lds_gateup{0}, lds_down{0};
     hipError_t err = set_lds(moe_gateup_gemm_kernel, kMaxLds, lds_gateup);
     if (err == hipSuccess)
-        err = set_lds(moe_down_gemm_kernel, kDownLds, lds_down);
+        err = set_lds(moe_down_gemm_kernel, kMaxLds, lds_down);
     if (err != hipSuccess)
         return err;
     const uint32_t nb = (a.T + kRouteBlockTokens - 1) / kRouteBlockTokens;
@@ -2466,11 +2452,8 @@ hipError_t moe_ffn_launch(const MoeArgs &a, bool gemm, hipStream_t stream) {
     const uint32_t nn_gu = (a.I + kGateUpCols - 1) / kGateUpCols;
     hipLaunchKernelGGL(moe_gateup_gemm_kernel, dim3(mt8 * nn_gu), dim3(kThreads), kMaxLds, stream,
                        a);
-    // virtual m-tiles: at most 2 max_tiles + 16 (two halves per big tile, padded
-    // to whole groups of 8)
     const uint32_t nn_d = (a.H + BN - 1) / BN;
-    const uint32_t vt8 = 8 * ((2 * a.max_tiles + 16 + 7) / 8);
-    hipLaunchKernelGGL(moe_down_gemm_kernel, dim3(vt8 * nn_d), dim3(kThreads), kDownLds, stream, a);
+    hipLaunchKernelGGL(moe_down_gemm_kernel, dim3(mt8 * nn_d), dim3(kThreads), kMaxLds, stream, a);
     hipLaunchKernelGGL(moe_combine_kernel, dim3(a.T, (a.H + kCombineCols - 1) / kCombineCols),
                        dim3(256), 0, stream, a);
     return hipGetLastError();
