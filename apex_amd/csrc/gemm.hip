@@ -89,6 +89,10 @@ __device__ __forceinline__ void gemm_one_tile(const GemmArgs &a, uint8_t *lds, u
     }
 }
 
+// A whole tile's 16 MFMAs per step leave room for its 2 fragments' decode at 2 VALU ops
+// after each (2: 370.6 / 370.5 us, 3: 373.1 / 372.6, 4: 376.1 / 375.8 at 2048 x 21504 x
+// 5376, same box).
+constexpr int kWholeVpm = 2;
 // A narrow tile's 2 NT MFMAs per step share NT fragments' decode: up to 8 VALU ops after
 // each (3 and 5 measured the same).
 constexpr int kNarrowVpm = 8;
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(kThreads) void nvfp4_gemm_kernel(GemmArgs a, uint32
         const uint32_t t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
         if (t >= full)
             return;
-        gemm_one_tile<GEGLU, F32, MT, WC, 8 / WC, 3>(a, lds, (t % tiles_m) * BM, (t / tiles_m) * TN);
+        gemm_one_tile<GEGLU, F32, MT, WC, 8 / WC, kWholeVpm>(a, lds, (t % tiles_m) * BM, (t / tiles_m) * TN);
         return;
     }
     const uint32_t c_tail = nf * TN;
