@@ -188,24 +188,24 @@ def cpu_baselines(budget_s: float = 4.0):
         return {"value": value, "unit": unit, "cores": 1, "kind": kind,
                 "sample": f"{sample}; single-threaded, host nproc={nproc}"}
 
-    # 0: GEMV 2048 x 2048, bf16 x (widened exactly), batch 1
+    # GEMV 2048 x 2048, bf16 x (widened exactly), batch 1
     x, w = synth.gemv_case(seed=0)
     xf = synth.bf16_to_f32(x)
     algo = w.codes.nbytes + w.scales.nbytes + x.nbytes + w.rows * 2
     sec, n = _repeat(lambda: mv(w.codes, w.scales, xf), budget_s / 4)
     out["gemv_2048"] = rec(round(algo / sec / 1e9, 4), "GB/s",
-                           f"config 0 whole: matvecNvfp4Cpu 2048x2048, batch 1, {n} calls, "
+                           f"whole workload: matvecNvfp4Cpu 2048x2048, batch 1, {n} calls, "
                            f"{sec * 1e3:.2f} ms each")
 
-    # 1: decode fused GeGLU 2 x [21504 x 5376], batch 1 (the headline workload)
+    # decode fused GeGLU 2 x [21504 x 5376], batch 1 (the headline workload)
     x, gate, up, algo, _ = geglu_workload()
     xf = synth.bf16_to_f32(x)
     sec, n = _repeat(lambda: geglu((gate.codes, gate.scales), (up.codes, up.scales), xf), budget_s)
     out["geglu_decode"] = rec(round(algo / sec / 1e9, 4), "GB/s",
-                              f"config 1 whole: gate and up matvecNvfp4Cpu [21504x5376] + "
+                              f"whole workload: gate and up matvecNvfp4Cpu [21504x5376] + "
                               f"geluTanh(gate) * up, batch 1, {n} calls, {sec:.2f} s each")
 
-    # 2: MoE decode, 16 tokens
+    # MoE decode, 16 tokens
     x, logits, slots = _case("moe_decode")
     T, H, E, I = x.shape[0], x.shape[1], logits.shape[1], slots.I
     ids, wts = oracle.moe_route(synth.bf16_to_f32(logits), 8)
@@ -214,11 +214,11 @@ def cpu_baselines(budget_s: float = 4.0):
     xf = synth.bf16_to_f32(x)
     sec, n = _repeat(lambda: moe(slots, xf, ids, wts, E), budget_s / 2)
     out["moe_decode"] = rec(round(algo / sec / 1e9, 4), "GB/s",
-                            f"config 2 whole: 16 tokens x top-8 over {U} experts, per expert "
+                            f"whole workload: 16 tokens x top-8 over {U} experts, per expert "
                             f"gate/up/down matvecNvfp4Cpu + geluTanh, weighted sum; {n} calls, "
                             f"{sec:.2f} s each")
 
-    # 3: prefill GEMM 2048 x 21504 x 5376 on a slice of W's rows
+    # prefill GEMM 2048 x 21504 x 5376 on a slice of W's rows
     A, w = _case("gemm")
     Af = synth.bf16_to_f32(A)
     M, N, K = A.shape[0], w.rows, w.K
@@ -231,11 +231,11 @@ def cpu_baselines(budget_s: float = 4.0):
     dt = time.perf_counter() - t
     full = dt * N / rows
     out["gemm_prefill"] = rec(round(2.0 * M * N * K / full / 1e12, 6), "TFLOP/s",
-                              f"config 3 slice: rows 0..{rows - 1} of {N} x all {M} tokens "
+                              f"slice: rows 0..{rows - 1} of {N} x all {M} tokens "
                               f"(K={K}) in {dt:.2f} s, extrapolated x{N / rows:.1f} to "
                               f"{full:.0f} s for the whole GEMM")
 
-    # 4: MoE prefill, 4096 tokens, on two slices of tokens
+    # MoE prefill, 4096 tokens, on two slices of tokens
     x, logits, slots = _case("moe_prefill")
     T, H, E, I = x.shape[0], x.shape[1], logits.shape[1], slots.I
     ids, wts = oracle.moe_route(synth.bf16_to_f32(logits), 8)
@@ -254,7 +254,7 @@ def cpu_baselines(budget_s: float = 4.0):
     full = t1 + slope * (T - n1)
     flops = 2.0 * T * 8 * 3 * H * I
     out["moe_prefill"] = rec(round(flops / full / 1e12, 6), "TFLOP/s",
-                             f"config 4 slices: tokens 0..{n1 - 1} in {t1:.2f} s and 0..{n2 - 1} "
+                             f"slices: tokens 0..{n1 - 1} in {t1:.2f} s and 0..{n2 - 1} "
                              f"in {t2:.2f} s (experts grouped, gate/up/down matvecNvfp4Cpu + "
                              f"geluTanh), the line through both extrapolated to all {T} tokens: "
                              f"{full:.0f} s")
