@@ -40,6 +40,28 @@ def test_gemm_one_hot_rows_select_weights_exactly(M, N, K):
     assert np.array_equal(got, oracle.matvec(w.codes, w.scales, A))
 
 
+def test_gemm_one_hot_every_scale_byte():
+    """All 256 E4M3 scale bytes -- zero, the subnormals, both signs, 0x7F / 0xFF = +-480 --
+    each in 32 blocks, through the MFMA GEMM's exact bf16 dequantisation: one-hot rows pick
+    single weights, bit for bit the reference decoder's values (negative scales flip the
+    code's sign; +-480 x 6 = +-2880 is exact in bf16)."""
+    rng = np.random.default_rng(31)
+    N, K, M = 256, 512, 300
+    w = synth.nvfp4_weights(rng, N, K)
+    w.scales[:] = (np.arange(N * K // 16) * 37 % 256).astype(np.uint8).reshape(N, K // 16)
+    perm = rng.integers(0, K, size=M)
+    A = np.zeros((M, K), np.float32)
+    A[np.arange(M), perm] = 1.0
+    got = bf16(gemm(synth.bf16_from_f32(A), w))
+    want = oracle.decode(w.codes, w.scales)[:, perm].T + np.float32(0.0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # and a dense product over every byte value against the fp64 contraction
+    A2 = synth.normal_bf16(rng, (M, K))
+    got2 = bf16(gemm(A2, w))
+    want2 = bf16(A2).astype(np.float64) @ dequant_f64(w.codes, w.scales).T
+    assert outside_bf16(got2, want2, 2e-3) == 0
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 224, 704), (300, 448, 2816), (513, 256, 1024),
                                    (130, 1408, 2816)])
 def test_gemm_random(M, N, K):
