@@ -41,9 +41,8 @@
 //    its scales 4, one line each.  Chunked (WS = 0, bf16 A): codes arrive two stages
 //    per load (64 bytes of a row, 16 rows per instruction) and scales four (16 bytes
 //    of a row), about 3.5x fewer line touches than one stage per load.  Per stage
-//    (WS = 4 or 3 buffers): fp32 [hi | lo] A, whose W wraps at K mid-chunk when K / 64
-//    is odd, and tiles that must fit two workgroups per CU.  Each
-//    wave dequantises its B fragments in registers right before its MFMAs
+//    (WS = 4 buffers): fp32 [hi | lo] A, whose W wraps at K mid-chunk when K / 64 is
+//    odd.  Each wave dequantises its B fragments in registers right before its MFMAs
 //    (cvt_scalef32_pk_f32_fp4 with 2^120 in the scale operand, x 2^-120 E4M3 scale,
 //    keep the exact high halves as bf16).  The packed form keeps W's LDS traffic 4x
 //    smaller than a bf16 copy.
@@ -79,12 +78,11 @@ constexpr int kWCpol = 0;
 // NT = 2 only W rows 0..127 are used (the half-width tile: 2 x 2 waves, both wave rows
 // on the same 128 W rows), the stage layout staying that of 256 rows.  WS: W's LDS
 // buffers -- 0: chunked (two 2-stage code buffers, two 4-stage scale buffers; no K wrap);
-// 4: per-stage ring, W loads with the same two stages of latency cover as A's; 3:
-// per-stage ring with one stage of cover, for tiles that must fit two workgroups per CU.
+// 4: per-stage ring, W loads with the same two stages of latency cover as A's.
 constexpr int kCodeChunk = 2 * kWCode;   // 16 KiB: codes of 2 stages, 64 bytes per row
 constexpr int kScaleChunk = 4 * kWScale; // 4 KiB: scales of 4 stages, 16 bytes per row
 template <int MT, int WC = 4, int NT = 8 / WC, int WS = 0> struct Layout {
-    static_assert(WS == 0 || WS == 3 || WS == 4, "W buffers");
+    static_assert(WS == 0 || WS == 4, "W buffers");
     static constexpr int kWR = 4 / WC;
     static constexpr int kNT = NT;
     static constexpr int kBM = 32 * MT * kWR;
@@ -380,10 +378,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
     // of stages s+4, s+5).  Stage x's wait needs A(x+1) and W(x+2), both in window x-2,
     // and leaves window x-1 in flight: two stages of latency cover for every load.
     // The prologue issues windows -4 .. -1 (W(0) alone, then W(1) A(0), W(2) A(1), W(3)
-    // A(2)); with WS = 3, W(3) would overwrite W(0) before it is read, so window -1
-    // repeats W(2) (the same bytes into the same buffer: harmless to a concurrent read)
-    // and window 0 adds W(3) first (the wait before stage 1's barrier, which needs it,
-    // makes it land).
+    // A(2)).
     if constexpr (kChunk) {
         load_scales(0);
         load_codes_part(0, 0, kCodeLoads);
@@ -398,7 +393,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
         load_a(0, kofs(0), 0, kALoads);
         load_w(2, kofs(2));
         load_a(1, kofs(1), 0, kALoads);
-        load_w((WS == 4 ? 3 : 2), kofs(WS == 4 ? 3 : 2));
+        load_w(3, kofs(3));
         load_a(2, kofs(2), 0, kA1);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 + kALoads + kA1) : "memory");
     }
@@ -457,10 +452,6 @@ __device__ __forceinline__ void gemm_tile(uint8_t *lds, __amdgpu_buffer_rsrc_t r
             if constexpr (ph == 0)
                 load_scales(s / 4 + 1);
         } else {
-            if constexpr (WS == 3 && ph == 0) {
-                if (s == 0)
-                    load_w(0, kofs(3));
-            }
             load_w((int)((s + 4) % WS), kofs(s + 4));
         }
         load_a(buf, kofs(s + kStages), 0, kA1);

@@ -27,15 +27,14 @@
 //   combine  as in the prefill regime.
 // Prefill regime: MFMA grouped GEMMs on the gemm_core tile (bf16 MFMA on exactly
 // dequantised weights).
-//   m-tiles  per expert, 256-row tiles plus one tail tile of 256, 128 or 64 rows, big
-//            tiles first; token rows are gathered through the pair list by the
+//   m-tiles  per expert, 256-row tiles plus one tail tile of 1 to 8 blocks of 32 rows,
+//            big tiles first; token rows are gathered through the pair list by the
 //            A-tile DMA loads (no permuted copy of x).
 //   gate/up  each 256-wide W tile holds 128 gate rows and the same 128 up rows, placed
 //            so that a lane's two accumulator sets are gate and up of one h column:
 //            GeGLU epilogue in registers -> h[pos] (bf16).
-//   down     h rows are contiguous per expert -> d[pos] (bf16); 128-row tiles, two
-//            workgroups per CU, so one's prologue and epilogue hide under the other's
-//            MFMAs (K = I is short).
+//   down     h rows are contiguous per expert -> d[pos] (bf16), over the gate/up
+//            GEMM's m-tiles, one workgroup per CU.
 //   combine  y[t] = sum_j w[t,j] d[pos(t,j)] in slot order j, fp32 -> bf16: a fixed
 //            summation order, no float atomics, so results are deterministic.
 #include <type_traits>
