@@ -1822,7 +1822,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
             const uint32_t pair = t * k + (ok ? j : 0);
             wt[jj] = ok ? uniform_f(a.w[pair]) : 0.0f;
             const uint32_t pos = uniform(v.pos_of_pair[pair]);
-            dv[jj] = load_b128(rd, ok ? (pos * H + c) * 2 : kOutOfRange);
+            // streaming policy: every d row is read once (33.2 vs 34.2 us at 4096 tokens)
+            dv[jj] = load_b128<APEX_WEIGHT_CPOL>(rd, ok ? (pos * H + c) * 2 : kOutOfRange);
         }
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
